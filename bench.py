@@ -1,0 +1,271 @@
+"""Decode-step benchmark: paged decode + KV write at the Qwen2-0.5B shape on one MI355X.
+
+One *step* is one decode-layer call of the attention backend on the
+headline workload (c2: 14 query / 2 kv heads, head_dim 64, block 16, bf16,
+batch 64, kv_len ~ U{128..2048}): the KV write of the step's 64 new tokens
+followed by the paged decode over every sequence's blocks. Successive steps
+use successive layers of a pool that holds >= 1 GiB in total (the same step
+metadata, a different layer's K/V, as in a real engine step), so the
+256 MB Infinity Cache cannot serve the reads and the measured bandwidth is
+HBM bandwidth. All inputs are resident in HBM before timing starts.
+
+Printed (one JSON line): ``value`` = algorithmic bytes of the layer call
+(decode + write) / µs per layer call, in GB/s; ``roofline`` for the decode
+launch (partition + cross-partition reduce kernels) against 8 TB/s; and
+``cpu_baseline`` = the oracle's PyTorch CPU path (the reference's
+per-sequence gather + SDPA loop) timed on this host's cores on the same
+workload in fp32.
+
+    python bench.py [--steps K] [--warmup W] [--workload c2] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "mini-vllm-continuous-batching-lab_amd")]
+
+import torch  # noqa: E402
+
+from benchmarks.paged_decode_workloads import (  # noqa: E402
+    HEADLINE, SPECS, decode_bytes, make_layout, write_bytes)
+
+METRIC = "paged decode µs/layer-call + achieved HBM GB/s (% peak), Qwen2-0.5B bs64"
+PEAK_HBM_GBS = 8000.0
+MIN_WORKING_SET = 1 << 30
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_layers(spec, layout, n_layers, device, seed):
+    """Per-layer pools (K, V), queries and new-token K/V, N(0,1) in bf16, made on the GPU."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    nb, hkv, bs, d = layout.num_blocks, spec.num_kv_heads, spec.block_size, spec.head_dim
+    b = len(layout.kv_lens)
+    layers = []
+    for _ in range(n_layers):
+        layers.append(dict(
+            k=torch.randn(nb, hkv, bs, d, generator=g, device=device).to(spec.dtype),
+            v=torch.randn(nb, hkv, bs, d, generator=g, device=device).to(spec.dtype),
+            q=torch.randn(b, spec.num_q_heads, d, generator=g, device=device).to(spec.dtype),
+            nk=torch.randn(b, hkv, d, generator=g, device=device).to(spec.dtype),
+            nv=torch.randn(b, hkv, d, generator=g, device=device).to(spec.dtype),
+        ))
+    return layers
+
+
+_SLEEP_CYCLES_PER_MS = None
+
+
+def _hold_gpu(stream, ms):
+    """Keep the GPU busy for about ``ms`` so the host can enqueue the timed
+    launches ahead of it (torch's bounded clock-spin kernel)."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        torch.cuda._sleep(1_000_000)
+        b.record(stream)
+        b.synchronize()
+        _SLEEP_CYCLES_PER_MS = 1_000_000 / max(a.elapsed_time(b), 1e-3)
+    torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS * ms))
+
+
+def time_loop(fn, n, stream):
+    """GPU time per iteration: the launches run back to back on the GPU
+    (host overhead hidden behind a held GPU), bracketed by HIP events."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    _hold_gpu(stream, 5 + 0.06 * n)
+    start.record(stream)
+    for i in range(n):
+        fn(i)
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1e3 / n  # µs per iteration
+
+
+def wall_loop(fn, n):
+    """Host-inclusive time per iteration (Python wrapper + launch + GPU)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e6 / n
+
+
+def cpu_baseline(spec, layout, layer, budget_s=12.0):
+    """The oracle's CPU path (reference loops, fp32) on a bounded sample:
+    whole layer calls (write + decode of the full batch) repeated until
+    ``budget_s`` of CPU time or 7 calls, median reported."""
+    from oracle import paged_ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    kc = layer["k"].float().cpu()
+    vc = layer["v"].float().cpu()
+    q, nk, nv = layer["q"].float().cpu(), layer["nk"].float().cpu(), layer["nv"].float().cpu()
+    bt = layout.block_table()
+    kv = torch.tensor(layout.kv_lens, dtype=torch.int64)
+    slots = layout.new_token_slots()
+
+    def call():
+        paged_ref.write_to_paged_cache(nk, nv, kc, vc, slots, spec.block_size)
+        return paged_ref.decode_from_tables(q, kc, vc, bt, kv, spec.block_size)
+
+    call()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 7 and (len(times) < 2 or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    us = statistics.median(times) * 1e6
+    nbytes = decode_bytes(layout, spec.dtype) + write_bytes(layout, spec.dtype)
+    return {
+        "value": round(nbytes / us / 1e3, 4),
+        "unit": "GB/s",
+        "us_per_layer_call": round(us, 1),
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{len(times)} full layer calls (write of {len(layout.kv_lens)} tokens + "
+                   f"decode of {len(layout.kv_lens)} sequences, {spec.name} shape) in fp32 with "
+                   f"torch.set_num_threads({cores}); median; GB/s on the bf16 workload's "
+                   f"algorithmic bytes"),
+    }
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(SPECS))
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the decode hot path runs on a single MI355X "
+              f"(requested --gpus {args.gpus}, WORLD_SIZE {world}); multi-GPU sharding is "
+              f"design-only in this build.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+
+    from mini_vllm.attention import _hip
+    from mini_vllm.attention.paged_attention_gpu import (
+        hip_cache_write, hip_decode_attention, plan_decode)
+
+    _hip.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    spec = SPECS[args.workload]
+    layout = make_layout(spec, args.seed)
+    bs = spec.block_size
+    pool_bytes = 2 * layout.num_blocks * spec.num_kv_heads * bs * spec.head_dim * 2
+    n_layers = max(2, math.ceil(MIN_WORKING_SET / pool_bytes))
+    log(f"[bench] workload {spec.name}: B={len(layout.kv_lens)} blocks={layout.num_blocks} "
+        f"layers={n_layers} ({n_layers * pool_bytes / 2**30:.2f} GiB of K/V)")
+    layers = build_layers(spec, layout, n_layers, dev, args.seed)
+    bt = layout.block_table().to(dev)
+    kv = torch.tensor(layout.kv_lens, dtype=torch.int64, device=dev)
+    slots = layout.new_token_slots().to(dev)
+    outs = [torch.empty_like(L["q"]) for L in layers]
+    stream = torch.cuda.current_stream(dev)
+
+    # per-step validation/planning (once per engine step, shared by all layers)
+    t0 = time.perf_counter()
+    plan = plan_decode(bt, kv, bs, layout.num_blocks, dev)
+    plan_us = (time.perf_counter() - t0) * 1e6
+
+    def layer_call(i):
+        L = layers[i % n_layers]
+        hip_cache_write(L["nk"], L["nv"], L["k"], L["v"], slots, bs)
+        outs[i % n_layers] = hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs)
+
+    def decode_only(i):
+        L = layers[i % n_layers]
+        hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs)
+
+    def write_only(i):
+        L = layers[i % n_layers]
+        hip_cache_write(L["nk"], L["nv"], L["k"], L["v"], slots, bs)
+
+    for i in range(args.warmup):
+        layer_call(i)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup done ({args.warmup} steps); timing {args.steps} steps")
+    us_step = time_loop(layer_call, args.steps, stream)
+    us_decode = time_loop(decode_only, args.steps, stream)
+    us_write = time_loop(write_only, args.steps, stream)
+    us_wall = wall_loop(layer_call, args.steps)
+    log(f"[bench] layer call {us_step:.2f} us, decode {us_decode:.2f} us, write {us_write:.2f} us")
+
+    dec_bytes = decode_bytes(layout, spec.dtype)
+    wr_bytes = write_bytes(layout, spec.dtype)
+    gbs = (dec_bytes + wr_bytes) / us_step / 1e3
+    dec_gbs = dec_bytes / us_decode / 1e3
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if spec.dtype == torch.bfloat16 else str(spec.dtype).replace("torch.", ""),
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{spec.name}: paged decode layer call (KV write + decode), "
+                         f"{spec.num_q_heads} q / {spec.num_kv_heads} kv heads, head_dim "
+                         f"{spec.head_dim}, block {bs}, batch {len(layout.kv_lens)}, "
+                         f"kv_len {spec.ctx}"),
+            "batch": len(layout.kv_lens),
+            "mean_kv_len": round(sum(layout.kv_lens) / len(layout.kv_lens), 1),
+            "layers_rotated": n_layers,
+            "parallelism": "single GPU",
+        },
+        "us_per_layer_call": round(us_step, 3),
+        "decode_us": round(us_decode, 3),
+        "write_us": round(us_write, 3),
+        "host_inclusive_us_per_layer_call": round(us_wall, 3),
+        "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "plan_us_per_step": round(plan_us, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged decode launch (partition + reduce kernels)",
+            "achieved": round(dec_gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(dec_gbs / PEAK_HBM_GBS, 4),
+            "algorithmic_bytes": dec_bytes,
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(spec, layout, layers[0])
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

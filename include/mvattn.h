@@ -1,0 +1,179 @@
+/*
+ * mvattn.h — C ABI of the MI355X (gfx950) paged-attention decode step.
+ *
+ * Two kernels sit behind this ABI, called once per transformer layer per
+ * engine step by the mini_vllm attention backend:
+ *   - the KV-cache write (scatter of new K/V rows by slot index into the
+ *     paged block pool), and
+ *   - the paged decode attention (block-table gather of K/V, scaled QK^T,
+ *     softmax, GQA grouping, PV accumulate), split over context partitions
+ *     with a cross-partition log-sum-exp reduce.
+ * Two helpers prepare and validate per-step metadata on the device so that
+ * the per-layer calls need no host synchronisation.
+ *
+ * Conventions
+ *   - All pointers are device pointers unless stated otherwise.
+ *   - Strides are in ELEMENTS; the innermost (head_dim) dimension of every
+ *     tensor is contiguous.
+ *   - KV pool layout (per layer, K and V separately):
+ *       [num_blocks, num_kv_heads, block_size, head_dim], contiguous.
+ *     Physical slot s lives at block s / block_size, offset s % block_size.
+ *   - `stream` is a hipStream_t passed as void* (0 = null stream).
+ *     Every call only enqueues work on that stream; none synchronises.
+ *   - Return value: MV_OK (0) or a negative MV_ERR_* code; the message of
+ *     the last error on the calling thread is returned by mv_last_error().
+ *     No entry point aborts the process.
+ *   - The library allocates no device memory and keeps no state other
+ *     than the thread-local error string.
+ */
+#ifndef MVATTN_H
+#define MVATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MVATTN_ABI_VERSION 1
+
+/* Element types of query / key / value / cache / output. */
+#define MV_DTYPE_F32 0
+#define MV_DTYPE_F16 1
+#define MV_DTYPE_BF16 2
+
+/* Return codes. */
+#define MV_OK 0
+#define MV_ERR_INVALID_ARGUMENT (-1) /* shape / pointer / alignment problem */
+#define MV_ERR_UNSUPPORTED (-2)      /* head_dim, block_size, GQA ratio, dtype */
+#define MV_ERR_HIP (-3)              /* a HIP runtime call failed */
+
+/* Status words written by mv_kv_slots_check (int32[2], device memory). */
+#define MV_SLOTS_OUT_OF_RANGE 0 /* # slots < -1 or >= num_blocks*block_size */
+#define MV_SLOTS_DUPLICATES 1   /* # (i < j) pairs with slot[i] == slot[j] >= 0 */
+
+/* Status words written by mv_decode_plan (int32[8], device memory). */
+#define MV_PLAN_NUM_ITEMS 0     /* number of (sequence, partition) work items */
+#define MV_PLAN_BAD_KV_LEN 1    /* # sequences with kv_len < 1 */
+#define MV_PLAN_INSUFFICIENT 2  /* # sequences whose table row cannot cover kv_len */
+#define MV_PLAN_BAD_BLOCK 3     /* # table entries used by kv_len outside [0, num_blocks) */
+#define MV_PLAN_MAX_PARTS 4     /* max partitions of any sequence */
+#define MV_PLAN_MIN_KV_LEN 5    /* min kv_len (clamped to int32) */
+#define MV_PLAN_WORDS 8
+
+/* Version of this ABI (MVATTN_ABI_VERSION of the built library). */
+int mv_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mv_last_error(void);
+
+/* Tokens per decode partition (context split unit) of the built kernels. */
+int mv_decode_partition_tokens(void);
+
+/*
+ * KV-cache write.
+ * Replaces the launch of `_cache_write_kernel` in `triton_cache_write`
+ * (mini_vllm/attention/paged_attention_gpu.py:90-154, kernel :32-87) and
+ * follows `write_to_paged_cache` (mini_vllm/cache/cache_write.py:25-74):
+ *   for t in [0, num_tokens): s = slot_mapping[t]; s == -1 skips;
+ *     key_cache[s / block_size, h, s % block_size, :] = key[t, h, :]
+ *     value_cache[... same ...]                        = value[t, h, :]
+ * The copy is bitwise. Unlike the Triton kernel it reads strided key/value
+ * (e.g. V as a column view of a fused QKV projection) without a staging
+ * copy. Slots outside [0, num_blocks*block_size) are skipped, never
+ * written; mv_kv_slots_check reports them (and duplicates) beforehand.
+ * Duplicate slots must be rejected by the caller: parallel writes to one
+ * slot have no defined winner.
+ */
+int mv_kv_cache_write(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                      const void* value, int64_t value_stride_tok, int64_t value_stride_head,
+                      void* key_cache, void* value_cache, const int64_t* slot_mapping,
+                      int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream);
+
+/*
+ * Slot validation for mv_kv_cache_write.
+ * Replaces the host-side duplicate check of `triton_cache_write`
+ * (paged_attention_gpu.py:126-135, `slot_mapping.unique()`) and the range
+ * check of `write_to_paged_cache` (cache_write.py:61-66). Writes
+ * status[MV_SLOTS_OUT_OF_RANGE] and status[MV_SLOTS_DUPLICATES] (int32[2],
+ * device) without sorting. The caller reads the two words back.
+ */
+int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t total_slots,
+                      int32_t* status, void* stream);
+
+/*
+ * Per-step decode metadata: validation + work list.
+ * Replaces the per-layer `kv_len_after.clone().to(int32)` of
+ * `AttentionBackendGPU.decode_attention` (paged_attention_gpu.py:560-562)
+ * and the `(kv_len_after < 1).any()` check of `triton_decode_attention`
+ * (:294-300); adds the table-coverage check of `gather_paged_kv`
+ * (mini_vllm/cache/cache_read.py:60-67).
+ *   kv_len      [num_seqs] int64 (kv_len_is_i64=1) or int32
+ *   block_table [num_seqs, max_blocks] (row stride bt_stride), int64
+ *               (bt_is_i64=1) or int32, -1 padded
+ * Outputs: kv_len_i32[num_seqs] (0 for rejected sequences), work_items
+ * (int32 pairs (seq, partition), capacity work_capacity pairs) and
+ * status[MV_PLAN_WORDS]. One work group; enqueue only.
+ */
+int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
+                   int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs, int32_t max_blocks,
+                   int32_t block_size, int64_t num_blocks, int32_t* kv_len_i32,
+                   int32_t* work_items, int64_t work_capacity, int32_t* status, void* stream);
+
+/* Bytes of fp32 workspace mv_paged_decode needs for `max_partitions`
+ * partitions per sequence (0 when max_partitions <= 1). */
+size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t head_dim,
+                                       int32_t max_partitions);
+
+/*
+ * Paged decode attention.
+ * Replaces the launch of `_paged_decode_kernel` in `triton_decode_attention`
+ * (paged_attention_gpu.py:252-321, kernel :162-249); the math is that of
+ * `AttentionBackendRef.decode_attention`
+ * (mini_vllm/attention/paged_attention_ref.py:102-161):
+ *   out[b, hq, :] = softmax(scale * q[b, hq] . K_b[hk]^T) V_b[hk],
+ *   hk = hq / (num_q_heads / num_kv_heads), over kv_len[b] tokens whose
+ *   token j lives at block block_table[b, j / block_size], offset
+ *   j % block_size.
+ * kv_len_i32 and work_items come from mv_decode_plan on the same metadata
+ * (num_work_items = status[MV_PLAN_NUM_ITEMS], max_partitions =
+ * status[MV_PLAN_MAX_PARTS]). Output rows of sequences that the plan
+ * rejected are left untouched. Supported: head_dim 64 or 128,
+ * block_size a power of two, num_q_heads / num_kv_heads in [1, 16],
+ * dtype F32 / F16 / BF16 (query, caches and output share it).
+ */
+int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                    const void* key_cache, const void* value_cache, const void* block_table,
+                    int32_t bt_is_i64, int64_t bt_stride, const int32_t* kv_len_i32,
+                    const int32_t* work_items, int32_t num_work_items, void* out,
+                    int64_t out_stride_tok, int64_t out_stride_head, float scale,
+                    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                    int32_t max_partitions, int32_t dtype, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
+ * Prefix gather (prefill support).
+ * Replaces the launch of `_gather_prefix_kv_kernel` in `gather_prefix_kv`
+ * (mini_vllm/attention/paged_attention_gpu.py:391-446, kernel :329-388),
+ * semantics of `gather_paged_kv` (mini_vllm/cache/cache_read.py:19-84):
+ *   out[cu_tokens[i] + p, h, :] = cache[bt[seq_rows[i], p / bs], h, p % bs, :]
+ *   for p < cu_tokens[i+1] - cu_tokens[i], i < num_seqs.
+ * seq_rows [num_seqs] and cu_tokens [num_seqs + 1] are int64 device arrays;
+ * the caller guarantees every table entry read is a pool block (entries
+ * outside [0, num_blocks) produce zero rows). head_dim * element bytes must
+ * be a multiple of 16.
+ */
+int mv_gather_paged_kv(const void* key_cache, const void* value_cache, const void* block_table,
+                       int32_t bt_is_i64, int64_t bt_stride, const int64_t* seq_rows,
+                       const int64_t* cu_tokens, int32_t num_seqs, int64_t total_tokens,
+                       void* out_key, void* out_value, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MVATTN_H */

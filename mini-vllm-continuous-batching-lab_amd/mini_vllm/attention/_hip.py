@@ -1,0 +1,127 @@
+"""ctypes binding of libmvattn.so (declarations: include/mvattn.h).
+
+``torch`` is imported first on purpose: torch ships its own
+``libamdhip64.so.7``; loading the kernel library afterwards makes the
+dynamic linker resolve its HIP dependency to that already-loaded runtime,
+so torch tensors, streams and our kernels share one HIP runtime.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must be loaded before the kernel library)
+
+ABI_VERSION = 1
+
+MV_OK = 0
+MV_ERR_INVALID_ARGUMENT = -1
+MV_ERR_UNSUPPORTED = -2
+MV_ERR_HIP = -3
+
+MV_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+# status words (mvattn.h)
+MV_SLOTS_OUT_OF_RANGE = 0
+MV_SLOTS_DUPLICATES = 1
+MV_PLAN_NUM_ITEMS = 0
+MV_PLAN_BAD_KV_LEN = 1
+MV_PLAN_INSUFFICIENT = 2
+MV_PLAN_BAD_BLOCK = 3
+MV_PLAN_MAX_PARTS = 4
+MV_PLAN_MIN_KV_LEN = 5
+MV_PLAN_WORDS = 8
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+DEFAULT_LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libmvattn.so")
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/mvattn.h.
+SIGNATURES = {
+    "mv_abi_version": (ctypes.c_int, []),
+    "mv_last_error": (ctypes.c_char_p, []),
+    "mv_decode_partition_tokens": (ctypes.c_int, []),
+    "mv_kv_cache_write": (ctypes.c_int, [
+        _P, _I64, _I64,            # key, strides
+        _P, _I64, _I64,            # value, strides
+        _P, _P, _P,                # key_cache, value_cache, slot_mapping
+        _I64, _I32, _I32, _I32,    # num_tokens, num_kv_heads, head_dim, block_size
+        _I64, _I32, _P,            # num_blocks, dtype, stream
+    ]),
+    "mv_kv_slots_check": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "mv_decode_plan": (ctypes.c_int, [
+        _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride
+        _I32, _I32, _I32, _I64,    # num_seqs, max_blocks, block_size, num_blocks
+        _P, _P, _I64, _P, _P,      # kv_len_i32, work_items, capacity, status, stream
+    ]),
+    "mv_paged_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
+    "mv_paged_decode": (ctypes.c_int, [
+        _P, _I64, _I64,            # query, strides
+        _P, _P, _P, _I32, _I64,    # key_cache, value_cache, block_table, bt_is_i64, bt_stride
+        _P, _P, _I32,              # kv_len_i32, work_items, num_work_items
+        _P, _I64, _I64,            # out, strides
+        _F, _I32, _I32, _I32, _I32,  # scale, num_seqs, num_q_heads, num_kv_heads, head_dim
+        _I32, _I64, _I32, _I32,    # block_size, num_blocks, max_partitions, dtype
+        _P, _SZ, _P,               # workspace, workspace_bytes, stream
+    ]),
+    "mv_gather_paged_kv": (ctypes.c_int, [
+        _P, _P, _P, _I32, _I64,    # key_cache, value_cache, block_table, bt_is_i64, bt_stride
+        _P, _P, _I32, _I64,        # seq_rows, cu_tokens, num_seqs, total_tokens
+        _P, _P, _I32, _I32, _I32,  # out_key, out_value, num_kv_heads, head_dim, block_size
+        _I64, _I32, _P,            # num_blocks, dtype, stream
+    ]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library_path() -> str:
+    return os.environ.get("MVATTN_LIB", DEFAULT_LIB_PATH)
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load (once) and type the kernel library; RuntimeError if it is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = path or library_path()
+        if not os.path.exists(p):
+            raise RuntimeError(
+                f"HIP kernel library not found at {p}; build it with "
+                f"`python {os.path.join(_PKG_ROOT, 'build_lib.py')}`"
+            )
+        lib = ctypes.CDLL(p)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        if lib.mv_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"{p}: ABI version {lib.mv_abi_version()} != expected {ABI_VERSION}"
+            )
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero return code of a library call."""
+    if rc == MV_OK:
+        return
+    msg = (load().mv_last_error() or b"").decode(errors="replace")
+    if rc == MV_ERR_UNSUPPORTED:
+        raise RuntimeError(f"{what}: unsupported: {msg}")
+    if rc == MV_ERR_INVALID_ARGUMENT:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg} (code {rc})")
