@@ -11,7 +11,7 @@ HBM bandwidth. All inputs are resident in HBM before timing starts.
 
 Printed (one JSON line): ``value`` = algorithmic bytes of the layer call
 (decode + write) / µs per layer call, in GB/s; ``roofline`` for the decode
-launch (partition + cross-partition reduce kernels) against 8 TB/s; and
+kernel (one launch, cross-partition merge fused) against 8 TB/s; and
 ``cpu_baseline`` = the oracle's PyTorch CPU path (the reference's
 per-sequence gather + SDPA loop) timed on this host's cores on the same
 workload in fp32.
@@ -189,7 +189,8 @@ def main(argv=None) -> int:
 
     # per-step validation/planning (once per engine step, shared by all layers)
     t0 = time.perf_counter()
-    plan = plan_decode(bt, kv, bs, layout.num_blocks, dev)
+    plan = plan_decode(bt, kv, bs, layout.num_blocks, dev, spec.head_dim, spec.dtype,
+                       spec.num_kv_heads)
     plan_us = (time.perf_counter() - t0) * 1e6
 
     def layer_call(i):
@@ -248,9 +249,11 @@ def main(argv=None) -> int:
         "host_inclusive_us_per_layer_call": round(us_wall, 3),
         "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "plan_us_per_step": round(plan_us, 1),
+        "partition_tokens": plan.partition_tokens,
+        "work_groups": plan.num_items * spec.num_kv_heads,
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged decode launch (partition + reduce kernels)",
+            "kernel": "paged_decode_kernel (one launch, partition merge fused)",
             "achieved": round(dec_gbs, 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

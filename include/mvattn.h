@@ -8,8 +8,9 @@
  *   - the paged decode attention (block-table gather of K/V, scaled QK^T,
  *     softmax, GQA grouping, PV accumulate), split over context partitions
  *     with a cross-partition log-sum-exp reduce.
- * Two helpers prepare and validate per-step metadata on the device so that
- * the per-layer calls need no host synchronisation.
+ * Two helpers validate per-step metadata on the device (slots; lengths and
+ * block tables, plus the decode work list) so that the per-layer calls
+ * need no host synchronisation.
  *
  * Conventions
  *   - All pointers are device pointers unless stated otherwise.
@@ -60,6 +61,7 @@ extern "C" {
 #define MV_PLAN_BAD_BLOCK 3     /* # table entries used by kv_len outside [0, num_blocks) */
 #define MV_PLAN_MAX_PARTS 4     /* max partitions of any sequence */
 #define MV_PLAN_MIN_KV_LEN 5    /* min kv_len (clamped to int32) */
+#define MV_PLAN_PARTITION_TOKENS 6 /* tokens per partition chosen for this step */
 #define MV_PLAN_WORDS 8
 
 /* Version of this ABI (MVATTN_ABI_VERSION of the built library). */
@@ -68,8 +70,9 @@ int mv_abi_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* mv_last_error(void);
 
-/* Tokens per decode partition (context split unit) of the built kernels. */
-int mv_decode_partition_tokens(void);
+/* Tokens one decode work group iteration covers for (head_dim, dtype):
+ * partitions are multiples of it (0 for an unsupported pair). */
+int mv_decode_chunk_tokens(int32_t head_dim, int32_t dtype);
 
 /*
  * KV-cache write.
@@ -104,7 +107,7 @@ int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t t
                       int32_t* status, void* stream);
 
 /*
- * Per-step decode metadata: validation + work list.
+ * Per-step decode metadata: validation, partition size, work list.
  * Replaces the per-layer `kv_len_after.clone().to(int32)` of
  * `AttentionBackendGPU.decode_attention` (paged_attention_gpu.py:560-562)
  * and the `(kv_len_after < 1).any()` check of `triton_decode_attention`
@@ -113,14 +116,20 @@ int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t t
  *   kv_len      [num_seqs] int64 (kv_len_is_i64=1) or int32
  *   block_table [num_seqs, max_blocks] (row stride bt_stride), int64
  *               (bt_is_i64=1) or int32, -1 padded
- * Outputs: kv_len_i32[num_seqs] (0 for rejected sequences), work_items
- * (int32 pairs (seq, partition), capacity work_capacity pairs) and
- * status[MV_PLAN_WORDS]. One work group; enqueue only.
+ * Chooses the partition size: the smallest multiple of chunk_tokens
+ * (mv_decode_chunk_tokens) that keeps the number of (sequence, kv head,
+ * partition) work groups near target_groups. Outputs: kv_len_i32[num_seqs]
+ * (0 for rejected sequences), work_items (int32 pairs (seq, partition),
+ * capacity work_capacity pairs; num_seqs * ceil(max_blocks * block_size /
+ * chunk_tokens) always suffices), counters[num_seqs * num_kv_heads] set to
+ * zero, and status[MV_PLAN_WORDS]. One work group; enqueue only.
  */
 int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                    int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs, int32_t max_blocks,
-                   int32_t block_size, int64_t num_blocks, int32_t* kv_len_i32,
-                   int32_t* work_items, int64_t work_capacity, int32_t* status, void* stream);
+                   int32_t block_size, int64_t num_blocks, int32_t chunk_tokens,
+                   int32_t num_kv_heads, int32_t target_groups, int32_t* kv_len_i32,
+                   int32_t* work_items, int64_t work_capacity, int32_t* counters,
+                   int32_t* status, void* stream);
 
 /* Bytes of fp32 workspace mv_paged_decode needs for `max_partitions`
  * partitions per sequence (0 when max_partitions <= 1). */
@@ -128,7 +137,7 @@ size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, in
                                        int32_t max_partitions);
 
 /*
- * Paged decode attention.
+ * Paged decode attention (one kernel launch).
  * Replaces the launch of `_paged_decode_kernel` in `triton_decode_attention`
  * (paged_attention_gpu.py:252-321, kernel :162-249); the math is that of
  * `AttentionBackendRef.decode_attention`
@@ -137,22 +146,27 @@ size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, in
  *   hk = hq / (num_q_heads / num_kv_heads), over kv_len[b] tokens whose
  *   token j lives at block block_table[b, j / block_size], offset
  *   j % block_size.
- * kv_len_i32 and work_items come from mv_decode_plan on the same metadata
- * (num_work_items = status[MV_PLAN_NUM_ITEMS], max_partitions =
- * status[MV_PLAN_MAX_PARTS]). Output rows of sequences that the plan
- * rejected are left untouched. Supported: head_dim 64 or 128,
- * block_size a power of two, num_q_heads / num_kv_heads in [1, 16],
- * dtype F32 / F16 / BF16 (query, caches and output share it).
+ * kv_len_i32, work_items, counters and the partition size come from
+ * mv_decode_plan on the same metadata (num_work_items =
+ * status[MV_PLAN_NUM_ITEMS], partition_tokens =
+ * status[MV_PLAN_PARTITION_TOKENS], max_partitions =
+ * status[MV_PLAN_MAX_PARTS]). Sequences split into several partitions are
+ * merged inside the same launch (log-sum-exp over fp32 partials in
+ * `workspace`, mv_paged_decode_workspace_bytes); calls sharing one plan's
+ * counters or one workspace must be ordered on one stream. Output rows of
+ * sequences the plan rejected are left untouched. Supported: head_dim 64
+ * or 128, block_size a power of two, num_q_heads / num_kv_heads in
+ * [1, 16], dtype F32 / F16 / BF16 (query, caches and output share it).
  */
 int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
                     const void* key_cache, const void* value_cache, const void* block_table,
                     int32_t bt_is_i64, int64_t bt_stride, const int32_t* kv_len_i32,
-                    const int32_t* work_items, int32_t num_work_items, void* out,
+                    const int32_t* work_items, int32_t num_work_items, int32_t partition_tokens,
+                    int32_t max_partitions, int32_t* counters, void* out,
                     int64_t out_stride_tok, int64_t out_stride_head, float scale,
                     int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
-                    int32_t head_dim, int32_t block_size, int64_t num_blocks,
-                    int32_t max_partitions, int32_t dtype, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Prefix gather (prefill support).

@@ -7,32 +7,47 @@
 //   token j of sequence b at block_table[b, j / BS], offset j % BS.
 //
 // Work decomposition
-//   The context of every sequence is cut into partitions of kPartition
-//   tokens. One work group of kWaves wavefronts handles one
-//   (sequence, kv head, partition) and serves all n_rep query heads of the
-//   GQA group, so every K/V byte is read from HBM exactly once.
-//   Each wave owns kTilesPerWave consecutive 16-token tiles.
+//   Every sequence's context is cut into partitions of P tokens (P is
+//   chosen per step by the plan kernel, a multiple of the chunk below). One
+//   work group of kWaves wavefronts handles one (sequence, kv head,
+//   partition) and serves all n_rep query heads of the GQA group, so every
+//   K/V byte is read from HBM exactly once. The work group walks its
+//   partition in chunks of kWaves * TPW 16-token tiles; wave w owns tiles
+//   [w*TPW, (w+1)*TPW) of every chunk. A chunk goes HBM -> registers ->
+//   LDS tile; the registers are refilled with the next chunk while the
+//   staged one is computed.
 //
 // Per tile (16 tokens x D) and wave, with lane = 16*g + t (g = 0..3):
-//   * lane loads K[token t][g*D/4 .. (g+1)*D/4) straight from HBM into
-//     registers (16-byte loads); the same for V.
+//   * Coalesced loads: load instruction c of lane l fetches the 16-byte
+//     chunk 64c + l of the tile's row-major bytes, so each instruction reads
+//     1 KiB of contiguous HBM (a whole pool block row set when BS >= 16).
+//     K and V tiles land in per-wave LDS tiles whose rows are padded by
+//     16 bytes.
 //   * S^T = K Q^T on MFMA (16x16x32 for 16-bit types, 16x16x4 for fp32):
-//     A = K tile (M = tokens), B = Q^T (N = query heads of the group,
-//     rows >= n_rep are zero). The k-slot -> head_dim mapping is the same
-//     for both operands, so the contraction is over all D dims whatever
-//     the hardware's k order.
+//     A = K tile (M = tokens), read from LDS as row t, dims
+//     [g*D/4, (g+1)*D/4); B = Q^T (N = query heads of the group, rows >=
+//     n_rep zero) from registers. Both operands use the same k-slot -> dim
+//     mapping, so the contraction covers all D dims whatever the hardware's
+//     k order.
 //   * The accumulator holds S^T[token 4g+e][head t] in lane (g, t), slot e
-//     -- exactly the A-operand layout of the P V MFMA (M = heads,
-//     K = tokens), so the probabilities never leave registers.
-//   * V needs K = tokens in each lane, i.e. a transpose: the V tile goes
-//     through a per-wave LDS tile (rows padded so the 4 lane groups hit
-//     disjoint banks) and is read back column-wise.
-//   Softmax is two-phase per wave (max over all of the wave's logits, then
-//   exp2), so the accumulator is never rescaled inside a partition; the
-//   kWaves partial results are merged through LDS at the end.
-//   Sequences with one partition write the output directly; longer ones
-//   write (normalised partial, max, sum) in fp32 and a second kernel merges
-//   the partitions with a log-sum-exp reduce.
+//     -- the A-operand layout of the P V MFMA (M = heads, K = tokens), so
+//     the probabilities never leave registers.
+//   * V needs K = tokens in each lane: it is read from its LDS tile
+//     column-wise (rows 0,4,8,12 of a column read start 16 banks apart, so
+//     the four lane groups never collide).
+//   Softmax is online across chunks (one rescale per chunk) and exact
+//   within a chunk. The kWaves wave results are merged through LDS.
+//
+// Cross-partition merge (fused): a sequence with one partition writes the
+// output directly. Otherwise each work group writes its normalised partial
+// (o, max, sum) in fp32 with device-coherent stores, waits for them to
+// complete and bumps the (sequence, kv head) counter; the work group that
+// brings the counter to n_parts merges all partials with a log-sum-exp
+// reduce (device-coherent loads), writes the output and resets the counter
+// to zero. (A __threadfence() here would write back and invalidate the
+// whole L2 of the XCD in every wave, which costs ~10x the kernel.)
+// Counters are zeroed by the plan kernel, so every call that shares a plan
+// must run on one stream.
 #include <algorithm>
 #include <climits>
 
@@ -41,40 +56,67 @@
 namespace mv {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kTilesPerWave = 4;
+// Launch geometry (build-time tunables; the defaults are the shipped shape).
+#ifndef MV_DECODE_WAVES
+#define MV_DECODE_WAVES 4
+#endif
+#ifndef MV_DECODE_WAVE_BYTES
+#define MV_DECODE_WAVE_BYTES 4096  // K bytes per wave per chunk
+#endif
+#ifndef MV_DECODE_WAVES_PER_SIMD
+#define MV_DECODE_WAVES_PER_SIMD 1  // register budget hint (1 = compiler's choice)
+#endif
+constexpr int kWaves = MV_DECODE_WAVES;
 constexpr int kTile = 16;
-constexpr int kPartition = kWaves * kTilesPerWave * kTile;  // 256 tokens
-constexpr int kMaxGroup = 16;                                 // MFMA N: q heads per kv head
+constexpr int kMaxGroup = 16;   // MFMA N: query heads per kv head
+constexpr int kMaxParts = 256;  // partitions per sequence (the plan enforces it)
+constexpr int kMergeLoads = 8;  // partial loads in flight per output element
 constexpr float kNegInf = -__builtin_huge_valf();
+
+template <int DTYPE, int D>
+struct Traits {
+  static constexpr int kElemBytes = Elem<DTYPE>::bytes;
+  static constexpr int kRowBytes = D * kElemBytes;  // one token row of one head
+  static constexpr int kTileBytes = kTile * kRowBytes;
+  static constexpr int kTilesPerWave =
+      kTileBytes >= MV_DECODE_WAVE_BYTES ? 1 : MV_DECODE_WAVE_BYTES / kTileBytes;
+  static constexpr int kChunk = kWaves * kTilesPerWave * kTile;  // tokens per iteration
+  static constexpr int kLoads = kTileBytes / (64 * 16);          // 16-byte loads per lane per tile
+  static constexpr int kRowChunks = kRowBytes / 16;
+  static constexpr int kLdsRow = kRowBytes + 16;
+  static constexpr int kLdsTile = kTile * kLdsRow;
+  static constexpr int kLaneElems = D / 4;                         // MFMA: dims per lane per token
+  static constexpr int kLaneChunks = kLaneElems * kElemBytes / 16;  // 16-byte pieces of those
+  static constexpr int kWaveLds = 2 * kTilesPerWave * kLdsTile;     // K and V tiles
+  static constexpr int kMergeBytes = kWaves * kMaxGroup * D * 4;          // wave merge
+  static constexpr int kPartsBytes = 2 * kMaxGroup * kMaxParts * 4;       // partition merge
+  static constexpr int kLdsBytes0 = kWaves * kWaveLds > kMergeBytes ? kWaves * kWaveLds : kMergeBytes;
+  static constexpr int kLdsBytes = kLdsBytes0 > kPartsBytes ? kLdsBytes0 : kPartsBytes;
+};
 
 struct DecodeArgs {
   const void* q;
   int64_t q_stride_tok, q_stride_head;  // elements
-  const void* k_cache;
-  const void* v_cache;
+  const char* k_cache;
+  const char* v_cache;
   const void* block_table;
   int64_t bt_stride;  // elements
   const int32_t* kv_len;
   const int32_t* work;  // (seq, partition) pairs
+  int32_t* counters;    // [num_seqs * num_kv_heads], zero at rest
   void* out;
   int64_t out_stride_tok, out_stride_head;  // elements
   float* ws_o;                              // [num_seqs, Hq, max_parts, D]
-  float2* ws_ml;                            // [num_seqs, Hq, max_parts]: (max, sum)
+  float* ws_ml;                             // [num_seqs, Hq, max_parts, 2]: (max, sum)
   float scale_log2;                         // scale * log2(e)
-  int32_t num_q_heads, num_kv_heads, n_rep, bs_log2, max_parts;
+  int32_t num_q_heads, num_kv_heads, n_rep, bs_log2, max_parts, part_tokens;
   int64_t num_blocks;
 };
-
-template <typename BT>
-__device__ __forceinline__ int64_t load_block_id(const BT* row, int idx) {
-  return static_cast<int64_t>(row[idx]);
-}
 
 // --------------------------------------------------------------- MFMA ----
 
 // S^T tile update: acc += K(16 tokens x 32 dims) * Q^T(32 dims x 16 heads)
-// for the 16-bit types; one call per 16-byte chunk of the lane's dims.
+// for the 16-bit types; one call per 16-byte piece of the lane's dims.
 template <int DTYPE>
 __device__ __forceinline__ f32x4 mfma_qk(const uint4& k, const uint4& q, f32x4 acc);
 template <>
@@ -89,7 +131,7 @@ __device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_F16>(const uint4& k, const uin
 }
 template <>
 __device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_F32>(const uint4& k, const uint4& q, f32x4 acc) {
-  // 4 dims per 16-byte chunk, one 16x16x4 fp32 MFMA per dim slot.
+  // 4 dims per 16-byte piece, one 16x16x4 fp32 MFMA per dim slot.
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.x), __uint_as_float(q.x), acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.y), __uint_as_float(q.y), acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.z), __uint_as_float(q.z), acc, 0, 0, 0);
@@ -97,187 +139,230 @@ __device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_F32>(const uint4& k, const uin
   return acc;
 }
 
-// ------------------------------------------------------- kernel traits ---
+// O tile update for one 16-token tile: o[c] += P(16 heads x 16 tokens) V(16 tokens x 16 dims).
+template <int DTYPE, int D, int LDS_ROW>
+__device__ __forceinline__ void mfma_pv(const float (&p)[4], const char* v_tile, int g, int t,
+                                        f32x4 (&o)[D / 16]) {
+  if constexpr (DTYPE == MV_DTYPE_F32) {
+    const float* vt = reinterpret_cast<const float*>(v_tile);
+    constexpr int rs = LDS_ROW / 4;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float vv = vt[(4 * g + e) * rs + 16 * c + t];
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[e], vv, o[c], 0, 0, 0);
+      }
+    }
+  } else {
+    const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_tile);
+    constexpr int rs = LDS_ROW / 2;
+    s16x4 pa;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pa[e] = static_cast<short>(from_f32<DTYPE>(p[e]));
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      s16x4 vb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vb[e] = static_cast<short>(vt[(4 * g + e) * rs + 16 * c + t]);
+      if constexpr (DTYPE == MV_DTYPE_BF16) {
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[c], 0, 0, 0);
+      } else {
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa),
+                                                    __builtin_bit_cast(f16x4, vb), o[c], 0, 0, 0);
+      }
+    }
+  }
+}
 
-template <int DTYPE, int D>
-struct Traits {
-  static constexpr int kElemBytes = Elem<DTYPE>::bytes;
-  static constexpr int kLaneElems = D / 4;                        // dims per lane per token
-  static constexpr int kLaneChunks = kLaneElems * kElemBytes / 16;  // 16-byte loads per lane
-  // LDS row of the V tile: D elements + pad. Rows 0,4,8,12 start 32 bytes
-  // (16-bit) / 64 bytes (fp32) apart modulo the bank width, so the four
-  // lane groups of a column read never share a bank.
-  static constexpr int kPadBytes = kElemBytes == 2 ? 8 : 16;
-  static constexpr int kRowBytes = D * kElemBytes + kPadBytes;
-  static constexpr int kVTileBytes = kTile * kRowBytes;
-  static constexpr int kMergeBytes = kWaves * kMaxGroup * D * 4;
-  static constexpr int kUnionBytes =
-      (kWaves * kVTileBytes > kMergeBytes ? kWaves * kVTileBytes : kMergeBytes);
-};
+// Device-coherent (agent-scope) fp32 store / load: `global_store/load ... sc1`
+// on gfx950, visible across the XCDs' separate L2 caches without any cache
+// writeback or invalidate.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this
+// wave's vector memory operations, stores included, are complete.
+constexpr unsigned kWaitVmcnt0 = 0x0F70;
 
-// ---------------------------------------------------- partition kernel ---
+// Stops the compiler from moving LDS accesses of one wave across this
+// point; the hardware completes one wave's LDS accesses in issue order.
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ----------------------------------------------------------- the kernel ---
 
 template <int DTYPE, int D, typename BT>
-__global__ __launch_bounds__(kWaves * 64) void paged_decode_partition_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kWaves * 64)
+__attribute__((amdgpu_waves_per_eu(MV_DECODE_WAVES_PER_SIMD))) void paged_decode_kernel(DecodeArgs a) {
   using Tr = Traits<DTYPE, D>;
   using raw_t = typename Elem<DTYPE>::raw;
-  constexpr int C = Tr::kLaneChunks;
+  constexpr int TPW = Tr::kTilesPerWave;
+  constexpr int L = Tr::kLoads;
+  constexpr int QC = Tr::kLaneChunks;
 
-  __shared__ __attribute__((aligned(16))) char s_union[Tr::kUnionBytes];
+  __shared__ __attribute__((aligned(16))) char s_lds[Tr::kLdsBytes];
   __shared__ float s_max[kWaves][kMaxGroup];
   __shared__ float s_sum[kWaves][kMaxGroup];
+  __shared__ int s_last;
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int t = lane & 15;  // token row (loads) / head column (results)
-  const int g = lane >> 4;  // dim quarter (loads) / token quad (results)
+  const int t = lane & 15;  // MFMA: token row (K operand) / head column (results)
+  const int g = lane >> 4;  // MFMA: dim quarter (K operand) / token quad (results)
 
   const int item = blockIdx.x / a.num_kv_heads;
   const int h = blockIdx.x - item * a.num_kv_heads;
   const int b = a.work[2 * item];
   const int part = a.work[2 * item + 1];
   const int kv = a.kv_len[b];
-  const int n_parts = (kv + kPartition - 1) / kPartition;
-  const int tile0 = part * kPartition + wave * kTilesPerWave * kTile;
+  const int n_parts = (kv + a.part_tokens - 1) / a.part_tokens;
+  const int tok_begin = part * a.part_tokens;
+  const int tok_end = min(kv, tok_begin + a.part_tokens);
+  const int n_chunks = (tok_end - tok_begin + Tr::kChunk - 1) / Tr::kChunk;
   const int bs_mask = (1 << a.bs_log2) - 1;
   const BT* bt_row = static_cast<const BT*>(a.block_table) + b * a.bt_stride;
-  const raw_t* kc = static_cast<const raw_t*>(a.k_cache);
-  const raw_t* vc = static_cast<const raw_t*>(a.v_cache);
 
-  // ---- issue every K and V load of the wave up front ------------------
-  uint4 kr[kTilesPerWave][C];
-  uint4 vr[kTilesPerWave][C];
+  char* k_lds = s_lds + wave * Tr::kWaveLds;
+  char* v_lds = k_lds + TPW * Tr::kLdsTile;
+
+  // Coalesced tile loads of chunk `ch`: piece 64c + lane of tile i.
+  auto load_chunk = [&](int ch, uint4 (&kr)[TPW][L], uint4 (&vr)[TPW][L]) {
 #pragma unroll
-  for (int i = 0; i < kTilesPerWave; ++i) {
-    const int j = tile0 + i * kTile + t;
-    bool ok = j < kv;
-    int64_t base = 0;
-    if (ok) {
-      const int64_t blk = load_block_id(bt_row, j >> a.bs_log2);
-      ok = blk >= 0 && blk < a.num_blocks;  // the plan rejects such tables
-      base = (((blk * a.num_kv_heads + h) << a.bs_log2) + (j & bs_mask)) * D + g * Tr::kLaneElems;
-    }
-    const uint4* kp = reinterpret_cast<const uint4*>(kc + base);
-    const uint4* vp = reinterpret_cast<const uint4*>(vc + base);
+    for (int i = 0; i < TPW; ++i) {
+      const int tile_tok = tok_begin + ch * Tr::kChunk + (wave * TPW + i) * kTile;
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      kr[i][c] = ok ? kp[c] : make_uint4(0, 0, 0, 0);
-      vr[i][c] = ok ? vp[c] : make_uint4(0, 0, 0, 0);
+      for (int c = 0; c < L; ++c) {
+        const int piece = 64 * c + lane;
+        const int row = piece / Tr::kRowChunks;
+        const int col = piece - row * Tr::kRowChunks;
+        const int j = tile_tok + row;
+        bool ok = j < tok_end;
+        int64_t off = 0;
+        if (ok) {
+          const int64_t blk = static_cast<int64_t>(bt_row[j >> a.bs_log2]);
+          ok = blk >= 0 && blk < a.num_blocks;  // the plan rejects such tables
+          off = (((blk * a.num_kv_heads + h) << a.bs_log2) + (j & bs_mask)) * Tr::kRowBytes + col * 16;
+        }
+        kr[i][c] = ok ? *reinterpret_cast<const uint4*>(a.k_cache + off) : make_uint4(0, 0, 0, 0);
+        vr[i][c] = ok ? *reinterpret_cast<const uint4*>(a.v_cache + off) : make_uint4(0, 0, 0, 0);
+      }
     }
-  }
+  };
 
   // ---- Q^T operand: head t of the group, dims of quarter g --------------
-  uint4 qr[C];
+  uint4 qr[QC];
   {
     const bool ok = t < a.n_rep;
     const raw_t* qp = static_cast<const raw_t*>(a.q) + b * a.q_stride_tok +
                       (h * a.n_rep + (ok ? t : 0)) * a.q_stride_head + g * Tr::kLaneElems;
 #pragma unroll
-    for (int c = 0; c < C; ++c) qr[c] = ok ? reinterpret_cast<const uint4*>(qp)[c] : make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < QC; ++c)
+      qr[c] = ok ? reinterpret_cast<const uint4*>(qp)[c] : make_uint4(0, 0, 0, 0);
   }
 
-  // ---- S^T = K Q^T ------------------------------------------------------
-  float s[kTilesPerWave][4];
-  float m = kNegInf;
-#pragma unroll
-  for (int i = 0; i < kTilesPerWave; ++i) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < C; ++c) acc = mfma_qk<DTYPE>(kr[i][c], qr[c], acc);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int j = tile0 + i * kTile + 4 * g + e;
-      s[i][e] = j < kv ? acc[e] * a.scale_log2 : kNegInf;
-      m = fmaxf(m, s[i][e]);
-    }
-  }
-  // Row max over the wave: lanes t, t+16, t+32, t+48 hold head t.
-  m = fmaxf(m, __shfl_xor(m, 16));
-  m = fmaxf(m, __shfl_xor(m, 32));
-  const float m_ref = m == kNegInf ? 0.f : m;
-
-  // ---- P = exp2(S - m), rounded to the MFMA input type -------------------
-  // The row sum uses the rounded values, so the result is an exact convex
-  // combination of the V rows up to the fp32 accumulation.
-  float l = 0.f;
-  float p[kTilesPerWave][4];
-#pragma unroll
-  for (int i = 0; i < kTilesPerWave; ++i) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float pe = __builtin_amdgcn_exp2f(s[i][e] - m_ref);
-      p[i][e] = to_f32<DTYPE>(from_f32<DTYPE>(pe));
-      l += p[i][e];
-    }
-  }
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-
-  // ---- O = P V, V transposed through LDS ---------------------------------
-  char* v_tile = s_union + wave * Tr::kVTileBytes;
-  f32x4 o[D / 16];
+  float m_run = kNegInf;  // running max of head t (log2 domain)
+  float l_run = 0.f;      // running sum of head t
+  f32x4 o[D / 16];        // O[head 4g+e][dim 16c+t]
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Writes the chunk held in registers to the wave's LDS tiles.
+  auto stage_chunk = [&](const uint4 (&kr)[TPW][L], const uint4 (&vr)[TPW][L]) {
 #pragma unroll
-  for (int i = 0; i < kTilesPerWave; ++i) {
-    // Row t of the tile, bytes [g*D*eb/4, (g+1)*D*eb/4).
-    char* wrow = v_tile + t * Tr::kRowBytes + g * (Tr::kLaneElems * Tr::kElemBytes);
-    if constexpr (Tr::kElemBytes == 2) {
+    for (int i = 0; i < TPW; ++i) {
 #pragma unroll
-      for (int c = 0; c < C; ++c) {
-        reinterpret_cast<uint2*>(wrow)[2 * c] = make_uint2(vr[i][c].x, vr[i][c].y);
-        reinterpret_cast<uint2*>(wrow)[2 * c + 1] = make_uint2(vr[i][c].z, vr[i][c].w);
+      for (int c = 0; c < L; ++c) {
+        const int piece = 64 * c + lane;
+        const int row = piece / Tr::kRowChunks;
+        const int col = piece - row * Tr::kRowChunks;
+        const int lo = i * Tr::kLdsTile + row * Tr::kLdsRow + col * 16;
+        *reinterpret_cast<uint4*>(k_lds + lo) = kr[i][c];
+        *reinterpret_cast<uint4*>(v_lds + lo) = vr[i][c];
       }
-    } else {
-#pragma unroll
-      for (int c = 0; c < C; ++c) reinterpret_cast<uint4*>(wrow)[c] = vr[i][c];
     }
-    // LDS accesses of one wave complete in issue order; the barrier only
-    // stops the compiler from moving the reads above the writes.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
 
-    if constexpr (DTYPE == MV_DTYPE_F32) {
-      const float* vt = reinterpret_cast<const float*>(v_tile);
-      constexpr int rs = Tr::kRowBytes / 4;
+  // Attention over the chunk staged in LDS (online softmax update).
+  auto compute_chunk = [&](int ch) {
+    // S^T = K Q^T
+    float s[TPW][4];
+    float mc = kNegInf;
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
+    for (int i = 0; i < TPW; ++i) {
+      const char* krow = k_lds + i * Tr::kLdsTile + t * Tr::kLdsRow + g * (Tr::kLaneElems * Tr::kElemBytes);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float vv = vt[(4 * g + e) * rs + 16 * c + t];
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[i][e], vv, o[c], 0, 0, 0);
-        }
-      }
-    } else {
-      const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_tile);
-      constexpr int rs = Tr::kRowBytes / 2;
-      s16x4 pa;
+      for (int c = 0; c < QC; ++c) acc = mfma_qk<DTYPE>(reinterpret_cast<const uint4*>(krow)[c], qr[c], acc);
+      const int tile_tok = tok_begin + ch * Tr::kChunk + (wave * TPW + i) * kTile;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pa[e] = static_cast<short>(from_f32<DTYPE>(p[i][e]));
-#pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        s16x4 vb;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vb[e] = static_cast<short>(vt[(4 * g + e) * rs + 16 * c + t]);
-        if constexpr (DTYPE == MV_DTYPE_BF16) {
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[c], 0, 0, 0);
-        } else {
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa),
-                                                      __builtin_bit_cast(f16x4, vb), o[c], 0, 0, 0);
-        }
+      for (int e = 0; e < 4; ++e) {
+        s[i][e] = tile_tok + 4 * g + e < tok_end ? acc[e] * a.scale_log2 : kNegInf;
+        mc = fmaxf(mc, s[i][e]);
       }
     }
-    __builtin_amdgcn_wave_barrier();
+    // head t's max over the chunk: lanes t, t+16, t+32, t+48
+    mc = fmaxf(mc, __shfl_xor(mc, 16));
+    mc = fmaxf(mc, __shfl_xor(mc, 32));
+    const float m_new = fmaxf(m_run, mc);
+    const float m_ref = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
+
+    // P = exp2(S - m), rounded to the MFMA input type; the sum uses the
+    // rounded values so O / l is an exact convex combination of V rows.
+    float p[TPW][4];
+    float lc = 0.f;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        p[i][e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[i][e] - m_ref)));
+        lc += p[i][e];
+      }
+    }
+    lc += __shfl_xor(lc, 16);
+    lc += __shfl_xor(lc, 32);
+    l_run = l_run * alpha + lc;
+    m_run = m_new;
+
+    // rescale O rows (head 4g+e takes the alpha of lane 4g+e)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float ar = __shfl(alpha, 4 * g + e);
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) o[c][e] *= ar;
+    }
+    // O += P V
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) mfma_pv<DTYPE, D, Tr::kLdsRow>(p[i], v_lds + i * Tr::kLdsTile, g, t, o);
+  };
+
+  // ---- chunk loop: the next chunk's loads are in flight while the staged
+  // chunk is computed (registers -> LDS tile -> registers refill) ---------
+  {
+    uint4 kr[TPW][L], vr[TPW][L];
+    load_chunk(0, kr, vr);
+    for (int ch = 0; ch < n_chunks; ++ch) {
+      stage_chunk(kr, vr);
+      wave_lds_order();
+      if (ch + 1 < n_chunks) load_chunk(ch + 1, kr, vr);
+      compute_chunk(ch);
+      wave_lds_order();  // the next iteration overwrites the tiles
+    }
   }
 
   // ---- merge the waves ------------------------------------------------------
-  __syncthreads();  // every wave is done with its V tile (s_union is reused)
-  float* s_o = reinterpret_cast<float*>(s_union);  // [kWaves][kMaxGroup][D]
+  __syncthreads();  // every wave is done with its tiles (s_lds is reused)
+  float* s_o = reinterpret_cast<float*>(s_lds);  // [kWaves][kMaxGroup][D]
   if (g == 0) {
-    s_max[wave][t] = m;
-    s_sum[wave][t] = l;
+    s_max[wave][t] = m_run;
+    s_sum[wave][t] = l_run;
   }
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
@@ -290,6 +375,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_partition_kernel(Dec
   __syncthreads();
 
   const int n_out = a.n_rep * D;
+  const int64_t slot_base = (static_cast<int64_t>(b) * a.num_q_heads + h * a.n_rep) * a.max_parts;
   for (int idx = threadIdx.x; idx < n_out; idx += kWaves * 64) {
     const int r = idx / D;
     const int d = idx - r * D;
@@ -306,60 +392,81 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_partition_kernel(Dec
         acc += s_o[(w * kMaxGroup + r) * D + d] * f;
       }
     }
-    const int hq = h * a.n_rep + r;
     if (n_parts == 1) {
-      raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + hq * a.out_stride_head;
+      raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head;
       op[d] = from_f32<DTYPE>(acc / sum);
     } else {
-      const int64_t slot = (static_cast<int64_t>(b) * a.num_q_heads + hq) * a.max_parts + part;
-      a.ws_o[slot * D + d] = acc / sum;
-      if (d == 0) a.ws_ml[slot] = make_float2(mx, sum);
+      const int64_t slot = slot_base + static_cast<int64_t>(r) * a.max_parts + part;
+      store_coherent(a.ws_o + slot * D + d, acc / sum);
+      if (d == 0) {
+        store_coherent(a.ws_ml + 2 * slot, mx);
+        store_coherent(a.ws_ml + 2 * slot + 1, sum);
+      }
     }
   }
-}
+  if (n_parts == 1) return;
 
-// ---------------------------------------------------- partition reduce ---
-
-struct ReduceArgs {
-  const float* ws_o;
-  const float2* ws_ml;
-  const int32_t* kv_len;
-  void* out;
-  int64_t out_stride_tok, out_stride_head;
-  int32_t num_q_heads, max_parts;
-};
-
-// One wave per (sequence, query head): out = sum_p w_p o_p / sum_p w_p with
-// w_p = sum_p * exp2(max_p - max). Single-partition sequences were written
-// by the partition kernel.
-template <int DTYPE, int D>
-__global__ __launch_bounds__(64) void paged_decode_reduce_kernel(ReduceArgs a) {
-  using raw_t = typename Elem<DTYPE>::raw;
-  const int b = blockIdx.x / a.num_q_heads;
-  const int hq = blockIdx.x - b * a.num_q_heads;
-  const int kv = a.kv_len[b];
-  const int n_parts = (kv + kPartition - 1) / kPartition;
-  if (n_parts <= 1) return;
-  const int64_t slot0 = (static_cast<int64_t>(b) * a.num_q_heads + hq) * a.max_parts;
-  const float2* ml = a.ws_ml + slot0;
-  float mx = kNegInf;
-  for (int p = 0; p < n_parts; ++p) mx = fmaxf(mx, ml[p].x);
-  constexpr int kPerLane = D / 64;
-  float acc[kPerLane];
-#pragma unroll
-  for (int k = 0; k < kPerLane; ++k) acc[k] = 0.f;
-  float sum = 0.f;
-  for (int p = 0; p < n_parts; ++p) {
-    const float2 v = ml[p];
-    const float w = v.y * __builtin_amdgcn_exp2f(v.x - mx);
-    sum += w;
-    const float* op = a.ws_o + (slot0 + p) * D;
-#pragma unroll
-    for (int k = 0; k < kPerLane; ++k) acc[k] += w * op[threadIdx.x + 64 * k];
+  // ---- cross-partition merge by the last work group --------------------
+  // The partials above are device-coherent stores; once every wave has
+  // seen them acknowledged (vmcnt(0)), the counter increment publishes
+  // them. The work group that completes the count reads all partials
+  // with device-coherent loads. No L2 writeback/invalidate is involved.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(&a.counters[b * a.num_kv_heads + h], 1,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == n_parts - 1;
   }
-  raw_t* dst = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + hq * a.out_stride_head;
+  __syncthreads();
+  if (!s_last) return;
+  // (max, sum) of every partial of the group's heads -> LDS in one round of
+  // loads; per-head normalised weights; then each output element streams
+  // its partials kMergeLoads at a time.
+  float* s_m = reinterpret_cast<float*>(s_lds);  // [n_rep][n_parts]
+  float* s_w = s_m + kMaxGroup * kMaxParts;      // [n_rep][n_parts]
+  const int n_ml = a.n_rep * n_parts;
+  for (int i = threadIdx.x; i < n_ml; i += kWaves * 64) {
+    const int r = i / n_parts;
+    const int64_t sl = slot_base + static_cast<int64_t>(r) * a.max_parts + (i - r * n_parts);
+    s_m[i] = load_coherent(a.ws_ml + 2 * sl);
+    s_w[i] = load_coherent(a.ws_ml + 2 * sl + 1);
+  }
+  __syncthreads();
+  if (threadIdx.x < a.n_rep) {
+    float* m_r = s_m + threadIdx.x * n_parts;
+    float* w_r = s_w + threadIdx.x * n_parts;
+    float mx = kNegInf;
+    for (int p = 0; p < n_parts; ++p) mx = fmaxf(mx, m_r[p]);
+    float sum = 0.f;
+    for (int p = 0; p < n_parts; ++p) {
+      w_r[p] *= __builtin_amdgcn_exp2f(m_r[p] - mx);
+      sum += w_r[p];
+    }
+    const float inv = 1.f / sum;
+    for (int p = 0; p < n_parts; ++p) w_r[p] *= inv;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < n_out; idx += kWaves * 64) {
+    const int r = idx / D;
+    const int d = idx - r * D;
+    const int64_t s0 = slot_base + static_cast<int64_t>(r) * a.max_parts;
+    const float* w_r = s_w + r * n_parts;
+    float acc = 0.f;
+    for (int p0 = 0; p0 < n_parts; p0 += kMergeLoads) {
+      float ov[kMergeLoads];
 #pragma unroll
-  for (int k = 0; k < kPerLane; ++k) dst[threadIdx.x + 64 * k] = from_f32<DTYPE>(acc[k] / sum);
+      for (int u = 0; u < kMergeLoads; ++u)
+        ov[u] = p0 + u < n_parts ? load_coherent(a.ws_o + (s0 + p0 + u) * D + d) : 0.f;
+#pragma unroll
+      for (int u = 0; u < kMergeLoads; ++u)
+        if (p0 + u < n_parts) acc += w_r[p0 + u] * ov[u];
+    }
+    raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head;
+    op[d] = from_f32<DTYPE>(acc);
+  }
+  if (threadIdx.x == 0)  // ready for the next call
+    __hip_atomic_store(&a.counters[b * a.num_kv_heads + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------- plan ---
@@ -368,19 +475,44 @@ struct PlanArgs {
   const void* kv_len;
   const void* block_table;
   int64_t bt_stride;
-  int32_t num_seqs, max_blocks, bs_log2;
+  int32_t num_seqs, max_blocks, bs_log2, chunk_tokens, num_kv_heads, target_groups;
   int64_t num_blocks;
   int32_t* kv_out;
   int32_t* work;
   int64_t work_cap;
+  int32_t* counters;
   int32_t* status;
 };
 
 constexpr int kPlanThreads = 1024;
 
+__device__ int block_sum(int v, int* scratch) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int total = 0;
+  for (int w = 0; w < kPlanThreads / 64; ++w) total += scratch[w];
+  return total;
+}
+
+__device__ int block_max(int v, int* scratch) {
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int m = 0;
+  for (int w = 0; w < kPlanThreads / 64; ++w) m = max(m, scratch[w]);
+  return m;
+}
+
+// One work group: validates kv_len and the table entries each sequence
+// reads, picks the partition size, builds the (sequence, partition) list
+// and zeroes the merge counters.
 template <typename KV, typename BT>
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   __shared__ int s_scan[kPlanThreads];
+  __shared__ int s_red[kPlanThreads / 64];
   __shared__ int s_cnt[4];  // bad kv_len, insufficient table, bad block id, max partitions
   __shared__ int s_min_kv;
   const int tid = threadIdx.x;
@@ -391,24 +523,44 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const KV* kvp = static_cast<const KV*>(a.kv_len);
   const BT* btp = static_cast<const BT*>(a.block_table);
   const int64_t bs = int64_t(1) << a.bs_log2;
+  auto valid_len = [&](int64_t kv) {
+    return kv >= 1 && (kv + bs - 1) / bs <= a.max_blocks && kv <= INT_MAX / 2;
+  };
+
+  // pass 1: validate lengths, count chunks
+  int chunks = 0, max_chunks = 0;
+  for (int b = tid; b < a.num_seqs; b += kPlanThreads) {
+    const int64_t kv = static_cast<int64_t>(kvp[b]);
+    atomicMin(&s_min_kv, static_cast<int>(std::max<int64_t>(std::min<int64_t>(kv, INT_MAX), INT_MIN)));
+    if (kv < 1) atomicAdd(&s_cnt[0], 1);
+    else if (!valid_len(kv)) atomicAdd(&s_cnt[1], 1);
+    else {
+      const int c = static_cast<int>((kv + a.chunk_tokens - 1) / a.chunk_tokens);
+      chunks += c;
+      max_chunks = max(max_chunks, c);
+    }
+    a.kv_out[b] = valid_len(kv) ? static_cast<int32_t>(kv) : 0;
+  }
+  const int total_chunks = block_sum(chunks, s_red);
+  const int most_chunks = block_max(max_chunks, s_red);
+  const int64_t groups = static_cast<int64_t>(total_chunks) * a.num_kv_heads;
+  // enough work groups for the device, at most kMaxParts partitions per sequence
+  const int per_part = static_cast<int>(std::max<int64_t>(
+      std::max<int64_t>(1, groups / std::max(1, a.target_groups)),
+      (most_chunks + kMaxParts - 1) / kMaxParts));
+  const int part_tokens = per_part * a.chunk_tokens;
+
+  // pass 2: work list
   int64_t running = 0;
   for (int base = 0; base < a.num_seqs; base += kPlanThreads) {
     const int b = base + tid;
     int np = 0;
     if (b < a.num_seqs) {
       const int64_t kv = static_cast<int64_t>(kvp[b]);
-      int32_t kv32 = 0;
-      atomicMin(&s_min_kv, static_cast<int>(std::max<int64_t>(std::min<int64_t>(kv, INT_MAX), INT_MIN)));
-      if (kv < 1) {
-        atomicAdd(&s_cnt[0], 1);
-      } else if ((kv + bs - 1) / bs > a.max_blocks || kv > INT_MAX - kPartition) {
-        atomicAdd(&s_cnt[1], 1);
-      } else {
-        kv32 = static_cast<int32_t>(kv);
-        np = (kv32 + kPartition - 1) / kPartition;
+      if (valid_len(kv)) {
+        np = static_cast<int>((kv + part_tokens - 1) / part_tokens);
         atomicMax(&s_cnt[3], np);
       }
-      a.kv_out[b] = kv32;
     }
     s_scan[tid] = np;
     __syncthreads();
@@ -430,20 +582,22 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     __syncthreads();
   }
 
-  // Every table entry a valid sequence will read must be a pool block.
+  // pass 3: every table entry a valid sequence reads must be a pool block
   const int64_t n = static_cast<int64_t>(a.num_seqs) * a.max_blocks;
   int bad = 0;
   for (int64_t i = tid; i < n; i += kPlanThreads) {
     const int64_t b = i / a.max_blocks;
     const int64_t j = i - b * a.max_blocks;
     const int64_t kv = static_cast<int64_t>(kvp[b]);
-    if (kv < 1 || (kv + bs - 1) / bs > a.max_blocks) continue;
+    if (!valid_len(kv)) continue;
     if (j < (kv + bs - 1) / bs) {
       const int64_t blk = static_cast<int64_t>(btp[b * a.bt_stride + j]);
       bad += (blk < 0 || blk >= a.num_blocks);
     }
   }
   if (bad) atomicAdd(&s_cnt[2], bad);
+  const int64_t nc = static_cast<int64_t>(a.num_seqs) * a.num_kv_heads;
+  for (int64_t i = tid; i < nc; i += kPlanThreads) a.counters[i] = 0;
   __syncthreads();
   if (tid == 0) {
     a.status[MV_PLAN_NUM_ITEMS] = static_cast<int32_t>(std::min<int64_t>(running, INT_MAX));
@@ -452,7 +606,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     a.status[MV_PLAN_BAD_BLOCK] = s_cnt[2];
     a.status[MV_PLAN_MAX_PARTS] = s_cnt[3];
     a.status[MV_PLAN_MIN_KV_LEN] = a.num_seqs > 0 ? s_min_kv : 0;
-    a.status[6] = 0;
+    a.status[MV_PLAN_PARTITION_TOKENS] = part_tokens;
     a.status[7] = 0;
   }
 }
@@ -463,46 +617,45 @@ size_t ws_o_bytes(int64_t num_seqs, int64_t hq, int64_t d, int64_t parts) {
   return static_cast<size_t>(num_seqs * hq * parts * d * 4);
 }
 
+template <int DTYPE, int D>
+int chunk_of() { return Traits<DTYPE, D>::kChunk; }
+
+int chunk_tokens(int head_dim, int dtype) {
+  const bool d64 = head_dim == 64;
+  switch (dtype) {
+    case MV_DTYPE_F32: return d64 ? chunk_of<MV_DTYPE_F32, 64>() : chunk_of<MV_DTYPE_F32, 128>();
+    case MV_DTYPE_F16: return d64 ? chunk_of<MV_DTYPE_F16, 64>() : chunk_of<MV_DTYPE_F16, 128>();
+    default: return d64 ? chunk_of<MV_DTYPE_BF16, 64>() : chunk_of<MV_DTYPE_BF16, 128>();
+  }
+}
+
 template <int DTYPE, int D, typename BT>
-int launch_decode(const DecodeArgs& a, int num_items, int num_seqs, hipStream_t s) {
-  if (num_items > 0) {
-    const int64_t grid = static_cast<int64_t>(num_items) * a.num_kv_heads;
-    if (grid > INT_MAX) return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: grid too large");
-    paged_decode_partition_kernel<DTYPE, D, BT>
-        <<<static_cast<unsigned>(grid), kWaves * 64, 0, s>>>(a);
-  }
-  if (a.max_parts > 1 && num_seqs > 0) {
-    ReduceArgs r;
-    r.ws_o = a.ws_o;
-    r.ws_ml = a.ws_ml;
-    r.kv_len = a.kv_len;
-    r.out = a.out;
-    r.out_stride_tok = a.out_stride_tok;
-    r.out_stride_head = a.out_stride_head;
-    r.num_q_heads = a.num_q_heads;
-    r.max_parts = a.max_parts;
-    paged_decode_reduce_kernel<DTYPE, D><<<num_seqs * a.num_q_heads, 64, 0, s>>>(r);
-  }
+int launch_decode(const DecodeArgs& a, int num_items, hipStream_t s) {
+  const int64_t grid = static_cast<int64_t>(num_items) * a.num_kv_heads;
+  if (grid > INT_MAX) return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: grid too large");
+  paged_decode_kernel<DTYPE, D, BT><<<static_cast<unsigned>(grid), kWaves * 64, 0, s>>>(a);
   return check_launch("mv_paged_decode");
 }
 
 template <int DTYPE, int D>
-int launch_decode_bt(const DecodeArgs& a, bool bt64, int num_items, int num_seqs, hipStream_t s) {
-  return bt64 ? launch_decode<DTYPE, D, int64_t>(a, num_items, num_seqs, s)
-              : launch_decode<DTYPE, D, int32_t>(a, num_items, num_seqs, s);
+int launch_decode_bt(const DecodeArgs& a, bool bt64, int num_items, hipStream_t s) {
+  return bt64 ? launch_decode<DTYPE, D, int64_t>(a, num_items, s)
+              : launch_decode<DTYPE, D, int32_t>(a, num_items, s);
 }
 
 template <int DTYPE>
-int launch_decode_d(const DecodeArgs& a, int d, bool bt64, int num_items, int num_seqs,
-                    hipStream_t s) {
-  return d == 64 ? launch_decode_bt<DTYPE, 64>(a, bt64, num_items, num_seqs, s)
-                 : launch_decode_bt<DTYPE, 128>(a, bt64, num_items, num_seqs, s);
+int launch_decode_d(const DecodeArgs& a, int d, bool bt64, int num_items, hipStream_t s) {
+  return d == 64 ? launch_decode_bt<DTYPE, 64>(a, bt64, num_items, s)
+                 : launch_decode_bt<DTYPE, 128>(a, bt64, num_items, s);
 }
 
 }  // namespace
 }  // namespace mv
 
-extern "C" int mv_decode_partition_tokens(void) { return mv::kPartition; }
+extern "C" int mv_decode_chunk_tokens(int32_t head_dim, int32_t dtype) {
+  if ((head_dim != 64 && head_dim != 128) || mv::dtype_bytes(dtype) == 0) return 0;
+  return mv::chunk_tokens(head_dim, dtype);
+}
 
 extern "C" size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
                                                   int32_t head_dim, int32_t max_partitions) {
@@ -515,15 +668,18 @@ extern "C" size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_
 extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                               int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs,
                               int32_t max_blocks, int32_t block_size, int64_t num_blocks,
+                              int32_t chunk_tokens, int32_t num_kv_heads, int32_t target_groups,
                               int32_t* kv_len_i32, int32_t* work_items, int64_t work_capacity,
-                              int32_t* status, void* stream) {
+                              int32_t* counters, int32_t* status, void* stream) {
   using namespace mv;
   if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null status");
-  if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0 || num_blocks < 0)
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: negative size");
+  if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0 || num_blocks < 0 || num_kv_heads <= 0)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: bad sizes");
+  if (chunk_tokens <= 0 || chunk_tokens % kTile)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: chunk_tokens %d", chunk_tokens);
   if (!is_pow2(block_size))
     return fail(MV_ERR_UNSUPPORTED, "mv_decode_plan: block_size %d is not a power of 2", block_size);
-  if (num_seqs > 0 && (!kv_len || !kv_len_i32 || (max_blocks > 0 && !block_table)))
+  if (num_seqs > 0 && (!kv_len || !kv_len_i32 || !counters || (max_blocks > 0 && !block_table)))
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null pointer");
   if (work_capacity > 0 && !work_items)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null work list");
@@ -534,10 +690,14 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
   a.num_seqs = num_seqs;
   a.max_blocks = max_blocks;
   a.bs_log2 = ilog2_exact(block_size);
+  a.chunk_tokens = chunk_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.target_groups = target_groups;
   a.num_blocks = num_blocks;
   a.kv_out = kv_len_i32;
   a.work = work_items;
   a.work_cap = work_capacity;
+  a.counters = counters;
   a.status = status;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (kv_len_is_i64) {
@@ -554,10 +714,11 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
                                const void* key_cache, const void* value_cache,
                                const void* block_table, int32_t bt_is_i64, int64_t bt_stride,
                                const int32_t* kv_len_i32, const int32_t* work_items,
-                               int32_t num_work_items, void* out, int64_t out_stride_tok,
-                               int64_t out_stride_head, float scale, int32_t num_seqs,
-                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                               int32_t block_size, int64_t num_blocks, int32_t max_partitions,
+                               int32_t num_work_items, int32_t partition_tokens,
+                               int32_t max_partitions, int32_t* counters, void* out,
+                               int64_t out_stride_tok, int64_t out_stride_head, float scale,
+                               int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t block_size, int64_t num_blocks,
                                int32_t dtype, void* workspace, size_t workspace_bytes,
                                void* stream) {
   using namespace mv;
@@ -577,27 +738,33 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
                 kMaxGroup);
   if (num_seqs < 0 || num_work_items < 0 || num_blocks <= 0 || max_partitions < 0)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: bad sizes");
+  const int chunk = chunk_tokens(head_dim, dtype);
+  if (partition_tokens <= 0 || partition_tokens % chunk)
+    return fail(MV_ERR_INVALID_ARGUMENT,
+                "mv_paged_decode: partition_tokens %d is not a positive multiple of %d",
+                partition_tokens, chunk);
   if (num_seqs == 0 || num_work_items == 0) return MV_OK;
   if (!query || !key_cache || !value_cache || !block_table || !kv_len_i32 || !work_items || !out)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: null pointer");
   // 16-byte loads of q rows and cache rows.
-  const uintptr_t qa = reinterpret_cast<uintptr_t>(query);
-  if ((qa | reinterpret_cast<uintptr_t>(key_cache) | reinterpret_cast<uintptr_t>(value_cache)) % 16 ||
+  if ((reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key_cache) |
+       reinterpret_cast<uintptr_t>(value_cache)) % 16 ||
       (q_stride_tok * eb) % 16 || (q_stride_head * eb) % 16)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: query/cache rows not 16-byte aligned");
-  if (num_work_items > max_partitions * static_cast<int64_t>(num_seqs) && max_partitions > 0)
+  if (max_partitions > 0 && num_work_items > max_partitions * static_cast<int64_t>(num_seqs))
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: work list larger than the plan allows");
 
   DecodeArgs a;
   a.q = query;
   a.q_stride_tok = q_stride_tok;
   a.q_stride_head = q_stride_head;
-  a.k_cache = key_cache;
-  a.v_cache = value_cache;
+  a.k_cache = static_cast<const char*>(key_cache);
+  a.v_cache = static_cast<const char*>(value_cache);
   a.block_table = block_table;
   a.bt_stride = bt_stride;
   a.kv_len = kv_len_i32;
   a.work = work_items;
+  a.counters = counters;
   a.out = out;
   a.out_stride_tok = out_stride_tok;
   a.out_stride_head = out_stride_head;
@@ -607,6 +774,7 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
   a.n_rep = n_rep;
   a.bs_log2 = ilog2_exact(block_size);
   a.max_parts = max_partitions;
+  a.part_tokens = partition_tokens;
   a.num_blocks = num_blocks;
   a.ws_o = nullptr;
   a.ws_ml = nullptr;
@@ -618,15 +786,16 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
                   workspace_bytes, need);
     if (reinterpret_cast<uintptr_t>(workspace) % 256)
       return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: workspace not 256-byte aligned");
+    if (!counters) return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: null counters");
     const size_t o = ws_o_bytes(num_seqs, num_q_heads, head_dim, max_partitions);
     a.ws_o = static_cast<float*>(workspace);
-    a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + ((o + 255) / 256) * 256);
+    a.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((o + 255) / 256) * 256);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bt64 = bt_is_i64 != 0;
   switch (dtype) {
-    case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, bt64, num_work_items, num_seqs, s);
-    case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, bt64, num_work_items, num_seqs, s);
-    default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, bt64, num_work_items, num_seqs, s);
+    case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, bt64, num_work_items, s);
+    case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, bt64, num_work_items, s);
+    default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, bt64, num_work_items, s);
   }
 }

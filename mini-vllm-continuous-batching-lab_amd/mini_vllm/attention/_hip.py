@@ -32,6 +32,7 @@ MV_PLAN_INSUFFICIENT = 2
 MV_PLAN_BAD_BLOCK = 3
 MV_PLAN_MAX_PARTS = 4
 MV_PLAN_MIN_KV_LEN = 5
+MV_PLAN_PARTITION_TOKENS = 6
 MV_PLAN_WORDS = 8
 
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
@@ -47,7 +48,7 @@ _F = ctypes.c_float
 SIGNATURES = {
     "mv_abi_version": (ctypes.c_int, []),
     "mv_last_error": (ctypes.c_char_p, []),
-    "mv_decode_partition_tokens": (ctypes.c_int, []),
+    "mv_decode_chunk_tokens": (ctypes.c_int, [_I32, _I32]),
     "mv_kv_cache_write": (ctypes.c_int, [
         _P, _I64, _I64,            # key, strides
         _P, _I64, _I64,            # value, strides
@@ -59,16 +60,18 @@ SIGNATURES = {
     "mv_decode_plan": (ctypes.c_int, [
         _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride
         _I32, _I32, _I32, _I64,    # num_seqs, max_blocks, block_size, num_blocks
-        _P, _P, _I64, _P, _P,      # kv_len_i32, work_items, capacity, status, stream
+        _I32, _I32, _I32,          # chunk_tokens, num_kv_heads, target_groups
+        _P, _P, _I64, _P, _P, _P,  # kv_len_i32, work_items, capacity, counters, status, stream
     ]),
     "mv_paged_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
     "mv_paged_decode": (ctypes.c_int, [
         _P, _I64, _I64,            # query, strides
         _P, _P, _P, _I32, _I64,    # key_cache, value_cache, block_table, bt_is_i64, bt_stride
         _P, _P, _I32,              # kv_len_i32, work_items, num_work_items
+        _I32, _I32, _P,            # partition_tokens, max_partitions, counters
         _P, _I64, _I64,            # out, strides
         _F, _I32, _I32, _I32, _I32,  # scale, num_seqs, num_q_heads, num_kv_heads, head_dim
-        _I32, _I64, _I32, _I32,    # block_size, num_blocks, max_partitions, dtype
+        _I32, _I64, _I32,          # block_size, num_blocks, dtype
         _P, _SZ, _P,               # workspace, workspace_bytes, stream
     ]),
     "mv_gather_paged_kv": (ctypes.c_int, [

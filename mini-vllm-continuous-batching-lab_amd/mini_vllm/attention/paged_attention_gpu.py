@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 import threading
 import weakref
 from dataclasses import dataclass
@@ -221,8 +222,22 @@ class DecodePlan:
     block_table: torch.Tensor  # [num_seqs, max_blocks] int32/int64 on the device
     kv_len_i32: torch.Tensor   # [num_seqs] int32
     work: torch.Tensor         # [2 * capacity] int32 (seq, partition) pairs
+    counters: torch.Tensor     # [num_seqs * num_kv_heads] int32, zero between calls
     num_items: int
     max_parts: int
+    partition_tokens: int
+
+
+# Work groups per compute unit the partition size aims for (override:
+# MVATTN_GROUPS_PER_CU).
+GROUPS_PER_CU = int(os.environ.get("MVATTN_GROUPS_PER_CU", "4"))
+_CU_COUNT: dict = {}
+
+
+def _target_groups(device: torch.device) -> int:
+    if device not in _CU_COUNT:
+        _CU_COUNT[device] = torch.cuda.get_device_properties(device).multi_processor_count
+    return GROUPS_PER_CU * _CU_COUNT[device]
 
 
 def plan_decode(
@@ -231,8 +246,11 @@ def plan_decode(
     block_size: int,
     num_blocks: int,
     device: torch.device,
+    head_dim: int,
+    dtype: torch.dtype,
+    num_kv_heads: int,
 ) -> DecodePlan:
-    """Validate decode metadata and build the (sequence, partition) work list.
+    """Validate decode metadata, pick the partition size, build the work list.
 
     Raises ``ValueError`` (message contains "kv_len") when a sequence has
     ``kv_len_after < 1`` (reference paged_attention_gpu.py:294-300) and
@@ -241,9 +259,11 @@ def plan_decode(
     cache_read.py:60-67 raises "insufficient" for the former; the Triton
     kernel silently skips -1 entries). One host synchronisation per
     distinct (block_table, kv_len_after) pair; later calls with the same,
-    unmodified tensors reuse the plan.
+    unmodified tensors (the other layers of the step) reuse the plan.
     """
-    extra = (block_size, num_blocks, device)
+    lib = _hip.load()
+    chunk = lib.mv_decode_chunk_tokens(head_dim, _hip.MV_DTYPE[dtype])
+    extra = (block_size, num_blocks, device, chunk, num_kv_heads)
     cached = _cache_get("plan", (block_table, kv_len_after), extra)
     if cached is not None:
         return cached
@@ -263,19 +283,19 @@ def plan_decode(
         kv = kv.to(torch.int64)
     kv = kv.contiguous()
 
-    lib = _hip.load()
     num_seqs = kv.shape[0]
     max_blocks = bt.shape[1] if bt.dim() == 2 else 0
-    part = lib.mv_decode_partition_tokens()
-    cap = num_seqs * max(1, math.ceil(max_blocks * block_size / part))
+    cap = num_seqs * max(1, math.ceil(max_blocks * block_size / chunk))
     kv32 = torch.empty(max(num_seqs, 1), dtype=torch.int32, device=device)
     work = torch.empty(2 * max(cap, 1), dtype=torch.int32, device=device)
+    counters = torch.empty(max(num_seqs * num_kv_heads, 1), dtype=torch.int32, device=device)
     status = torch.empty(_hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
     _hip.check(
         lib.mv_decode_plan(
             _ptr(kv), int(kv.dtype == torch.int64), _ptr(bt), int(bt.dtype == torch.int64),
             bt.stride(0) if bt.dim() == 2 else 0, num_seqs, max_blocks, block_size,
-            num_blocks, _ptr(kv32), _ptr(work), cap, _ptr(status), _stream(device),
+            num_blocks, chunk, num_kv_heads, _target_groups(device), _ptr(kv32), _ptr(work),
+            cap, _ptr(counters), _ptr(status), _stream(device),
         ),
         "mv_decode_plan",
     )
@@ -298,7 +318,8 @@ def plan_decode(
     num_items = st[_hip.MV_PLAN_NUM_ITEMS]
     if num_items > cap:
         raise RuntimeError(f"decode plan: {num_items} work items exceed capacity {cap}")
-    plan = DecodePlan(bt, kv32, work, num_items, st[_hip.MV_PLAN_MAX_PARTS])
+    plan = DecodePlan(bt, kv32, work, counters, num_items, st[_hip.MV_PLAN_MAX_PARTS],
+                      st[_hip.MV_PLAN_PARTITION_TOKENS])
     _cache_put("plan", (block_table, kv_len_after), extra, plan)
     return plan
 
@@ -347,7 +368,8 @@ def hip_decode_attention(
 
     device = query.device
     num_blocks = key_cache.shape[0]
-    plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device)
+    plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
+                       query.dtype, num_kv_heads)
     output = torch.empty(query.shape, dtype=query.dtype, device=device)
     if total_decode == 0 or plan.num_items == 0:
         return output
@@ -364,9 +386,10 @@ def hip_decode_attention(
             _ptr(query), query.stride(0), query.stride(1),
             _ptr(key_cache), _ptr(value_cache), _ptr(bt), int(bt.dtype == torch.int64),
             bt.stride(0), _ptr(plan.kv_len_i32), _ptr(plan.work), plan.num_items,
+            plan.partition_tokens, plan.max_parts, _ptr(plan.counters),
             _ptr(output), output.stride(0), output.stride(1),
             float(head_dim ** -0.5), total_decode, num_q_heads, num_kv_heads, head_dim,
-            block_size, num_blocks, plan.max_parts, _hip.MV_DTYPE[query.dtype],
+            block_size, num_blocks, _hip.MV_DTYPE[query.dtype],
             _ptr(ws), ws.numel() if ws is not None else 0, _stream(device),
         ),
         "mv_paged_decode",

@@ -60,7 +60,10 @@ def test_every_declared_symbol_is_exported_and_typed(lib):
 
 def test_abi_queries(lib):
     assert lib.mv_abi_version() == _hip.ABI_VERSION == 1
-    assert lib.mv_decode_partition_tokens() == 256
+    assert lib.mv_decode_chunk_tokens(64, 2) == 128      # 4 waves x 2 tiles x 16
+    assert lib.mv_decode_chunk_tokens(128, 2) == 64      # 4 waves x 1 tile x 16
+    assert lib.mv_decode_chunk_tokens(64, 0) == 64
+    assert lib.mv_decode_chunk_tokens(96, 2) == 0
 
 
 def test_workspace_bytes(lib):
@@ -69,19 +72,43 @@ def test_workspace_bytes(lib):
     assert lib.mv_paged_decode_workspace_bytes(64, 14, 64, 8) == -(-o // 256) * 256 + 64 * 14 * 8 * 8
 
 
+DECODE_PARAMS = [
+    "query", "q_stride_tok", "q_stride_head", "key_cache", "value_cache", "block_table",
+    "bt_is_i64", "bt_stride", "kv_len_i32", "work_items", "num_work_items", "partition_tokens",
+    "max_partitions", "counters", "out", "out_stride_tok", "out_stride_head", "scale",
+    "num_seqs", "num_q_heads", "num_kv_heads", "head_dim", "block_size", "num_blocks", "dtype",
+    "workspace", "workspace_bytes", "stream",
+]
+
+
+def _decode_args(**kw):
+    base = dict(query=None, q_stride_tok=0, q_stride_head=0, key_cache=None, value_cache=None,
+                block_table=None, bt_is_i64=1, bt_stride=0, kv_len_i32=None, work_items=None,
+                num_work_items=1, partition_tokens=128, max_partitions=1, counters=None, out=None,
+                out_stride_tok=0, out_stride_head=0, scale=0.125, num_seqs=1, num_q_heads=14,
+                num_kv_heads=2, head_dim=64, block_size=16, num_blocks=10, dtype=2,
+                workspace=None, workspace_bytes=0, stream=None)
+    base.update(kw)
+    return [base[k] for k in DECODE_PARAMS]
+
+
+def test_decode_param_list_matches_header():
+    assert len(DECODE_PARAMS) == len(_hip.SIGNATURES["mv_paged_decode"][1])
+
+
 def test_decode_rejects_unsupported_shapes_on_host(lib):
-    args = [None, 0, 0, None, None, None, 1, 0, None, None, 1, None, 0, 0, 0.125,
-            1, 14, 2, 96, 16, 10, 1, 2, None, 0, None]
-    assert lib.mv_paged_decode(*args) == _hip.MV_ERR_UNSUPPORTED
+    """Argument checks return before any device work (null pointers are fine)."""
+    assert lib.mv_paged_decode(*_decode_args(head_dim=96)) == _hip.MV_ERR_UNSUPPORTED
     assert b"head_dim 96" in lib.mv_last_error()
-    args[18], args[19] = 64, 12  # block_size not a power of two
-    assert lib.mv_paged_decode(*args) == _hip.MV_ERR_UNSUPPORTED
-    args[19], args[16], args[17] = 16, 14, 3  # 14 % 3 != 0
-    assert lib.mv_paged_decode(*args) == _hip.MV_ERR_INVALID_ARGUMENT
-    args[16], args[17] = 34, 2  # 17 query heads per kv head
-    assert lib.mv_paged_decode(*args) == _hip.MV_ERR_UNSUPPORTED
-    args[16], args[17], args[22] = 14, 2, 7  # dtype 7
-    assert lib.mv_paged_decode(*args) == _hip.MV_ERR_UNSUPPORTED
+    assert lib.mv_paged_decode(*_decode_args(block_size=12)) == _hip.MV_ERR_UNSUPPORTED
+    assert lib.mv_paged_decode(*_decode_args(num_kv_heads=3)) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert lib.mv_paged_decode(*_decode_args(num_q_heads=34)) == _hip.MV_ERR_UNSUPPORTED
+    assert lib.mv_paged_decode(*_decode_args(dtype=7)) == _hip.MV_ERR_UNSUPPORTED
+    assert lib.mv_paged_decode(*_decode_args(partition_tokens=100)) == _hip.MV_ERR_INVALID_ARGUMENT
+    # nothing to do is not an error
+    assert lib.mv_paged_decode(*_decode_args(num_work_items=0)) == _hip.MV_OK
+    # work to do but null pointers
+    assert lib.mv_paged_decode(*_decode_args()) == _hip.MV_ERR_INVALID_ARGUMENT
 
 
 def test_write_rejects_bad_sizes_on_host(lib):
