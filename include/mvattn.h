@@ -74,6 +74,11 @@ const char* mv_last_error(void);
  * partitions are multiples of it (0 for an unsupported pair). */
 int mv_decode_chunk_tokens(int32_t head_dim, int32_t dtype);
 
+/* Decode work groups one compute unit holds at once for (head_dim, dtype)
+ * (LDS-limited); times the CU count it is the work-group count that runs in
+ * a single dispatch round, the natural target_groups of mv_decode_plan. */
+int mv_decode_groups_per_cu(int32_t head_dim, int32_t dtype);
+
 /*
  * KV-cache write.
  * Replaces the launch of `_cache_write_kernel` in `triton_cache_write`
@@ -118,11 +123,13 @@ int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t t
  *               (bt_is_i64=1) or int32, -1 padded
  * Chooses the partition size: the smallest multiple of chunk_tokens
  * (mv_decode_chunk_tokens) that keeps the number of (sequence, kv head,
- * partition) work groups near target_groups. Outputs: kv_len_i32[num_seqs]
- * (0 for rejected sequences), work_items (int32 pairs (seq, partition),
- * capacity work_capacity pairs; num_seqs * ceil(max_blocks * block_size /
- * chunk_tokens) always suffices), counters[num_seqs * num_kv_heads] set to
- * zero, and status[MV_PLAN_WORDS]. One work group; enqueue only.
+ * partition) work groups within target_groups (at most 128 partitions per
+ * sequence). Outputs: kv_len_i32[num_seqs] (0 for rejected sequences),
+ * work_items (int32 quadruples (seq, partition, kv_len, 0), 16-byte
+ * aligned, capacity work_capacity quadruples; num_seqs * ceil(max_blocks *
+ * block_size / chunk_tokens) always suffices), counters[num_seqs *
+ * num_kv_heads] set to zero, and status[MV_PLAN_WORDS]. One work group;
+ * enqueue only.
  */
 int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                    int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs, int32_t max_blocks,

@@ -12,31 +12,28 @@
 //   work group of kWaves wavefronts handles one (sequence, kv head,
 //   partition) and serves all n_rep query heads of the GQA group, so every
 //   K/V byte is read from HBM exactly once. The work group walks its
-//   partition in chunks of kWaves * TPW 16-token tiles; wave w owns tiles
-//   [w*TPW, (w+1)*TPW) of every chunk. A chunk goes HBM -> registers ->
-//   LDS tile; the registers are refilled with the next chunk while the
-//   staged one is computed.
+//   partition in chunks of kWaves 16-token tiles, one tile per wave.
 //
 // Per tile (16 tokens x D) and wave, with lane = 16*g + t (g = 0..3):
-//   * Coalesced loads: load instruction c of lane l fetches the 16-byte
-//     chunk 64c + l of the tile's row-major bytes, so each instruction reads
-//     1 KiB of contiguous HBM (a whole pool block row set when BS >= 16).
-//     K and V tiles land in per-wave LDS tiles whose rows are padded by
-//     16 bytes.
+//   * HBM -> LDS without registers: global_load_lds_dwordx4 writes lane l's
+//     16 bytes to LDS slot (64c + l) of load instruction c. Each lane
+//     fetches the 16-byte piece that belongs in its slot under an XOR
+//     swizzle (slot s of row r holds piece s ^ sw(r)), so every load
+//     instruction still reads 1 KiB of contiguous HBM while the reads
+//     below are bank-conflict free with unpadded rows. Two LDS buffers per
+//     wave: the next tile streams in while the current one is computed.
 //   * S^T = K Q^T on MFMA (16x16x32 for 16-bit types, 16x16x4 for fp32):
-//     A = K tile (M = tokens), read from LDS as row t, dims
-//     [g*D/4, (g+1)*D/4); B = Q^T (N = query heads of the group, rows >=
-//     n_rep zero) from registers. Both operands use the same k-slot -> dim
-//     mapping, so the contraction covers all D dims whatever the hardware's
-//     k order.
+//     A = K tile (M = tokens), row t, dims [g*D/4, (g+1)*D/4) from LDS;
+//     B = Q^T (N = query heads of the group, rows >= n_rep zero) from
+//     registers. Both operands use the same k-slot -> dim mapping, so the
+//     contraction covers all D dims whatever the hardware's k order.
 //   * The accumulator holds S^T[token 4g+e][head t] in lane (g, t), slot e
 //     -- the A-operand layout of the P V MFMA (M = heads, K = tokens), so
 //     the probabilities never leave registers.
 //   * V needs K = tokens in each lane: it is read from its LDS tile
-//     column-wise (rows 0,4,8,12 of a column read start 16 banks apart, so
-//     the four lane groups never collide).
-//   Softmax is online across chunks (one rescale per chunk) and exact
-//   within a chunk. The kWaves wave results are merged through LDS.
+//     column-wise.
+//   Softmax is online across tiles (one rescale per tile) and exact within
+//   a tile. The kWaves wave results are merged through LDS.
 //
 // Cross-partition merge (fused): a sequence with one partition writes the
 // output directly. Otherwise each work group writes its normalised partial
@@ -60,39 +57,51 @@ namespace {
 #ifndef MV_DECODE_WAVES
 #define MV_DECODE_WAVES 4
 #endif
-#ifndef MV_DECODE_WAVE_BYTES
-#define MV_DECODE_WAVE_BYTES 4096  // K bytes per wave per chunk
-#endif
-#ifndef MV_DECODE_WAVES_PER_SIMD
-#define MV_DECODE_WAVES_PER_SIMD 1  // register budget hint (1 = compiler's choice)
-#endif
 constexpr int kWaves = MV_DECODE_WAVES;
 constexpr int kTile = 16;
 constexpr int kMaxGroup = 16;   // MFMA N: query heads per kv head
-constexpr int kMaxParts = 256;  // partitions per sequence (the plan enforces it)
-constexpr int kMergeLoads = 8;  // partial loads in flight per output element
+constexpr int kMaxParts = 128;  // partitions per sequence (the plan enforces it)
+constexpr int kMergeParts = 8;  // partitions merged per round of loads
 constexpr float kNegInf = -__builtin_huge_valf();
 
 template <int DTYPE, int D>
 struct Traits {
   static constexpr int kElemBytes = Elem<DTYPE>::bytes;
-  static constexpr int kRowBytes = D * kElemBytes;  // one token row of one head
-  static constexpr int kTileBytes = kTile * kRowBytes;
-  static constexpr int kTilesPerWave =
-      kTileBytes >= MV_DECODE_WAVE_BYTES ? 1 : MV_DECODE_WAVE_BYTES / kTileBytes;
-  static constexpr int kChunk = kWaves * kTilesPerWave * kTile;  // tokens per iteration
-  static constexpr int kLoads = kTileBytes / (64 * 16);          // 16-byte loads per lane per tile
-  static constexpr int kRowChunks = kRowBytes / 16;
-  static constexpr int kLdsRow = kRowBytes + 16;
-  static constexpr int kLdsTile = kTile * kLdsRow;
-  static constexpr int kLaneElems = D / 4;                         // MFMA: dims per lane per token
-  static constexpr int kLaneChunks = kLaneElems * kElemBytes / 16;  // 16-byte pieces of those
-  static constexpr int kWaveLds = 2 * kTilesPerWave * kLdsTile;     // K and V tiles
-  static constexpr int kMergeBytes = kWaves * kMaxGroup * D * 4;          // wave merge
-  static constexpr int kPartsBytes = 2 * kMaxGroup * kMaxParts * 4;       // partition merge
-  static constexpr int kLdsBytes0 = kWaves * kWaveLds > kMergeBytes ? kWaves * kWaveLds : kMergeBytes;
-  static constexpr int kLdsBytes = kLdsBytes0 > kPartsBytes ? kLdsBytes0 : kPartsBytes;
+  static constexpr int kRowBytes = D * kElemBytes;     // one token row of one head
+  static constexpr int kTileBytes = kTile * kRowBytes;  // 2 KiB (D=64, 16-bit) .. 8 KiB
+  static constexpr int kChunk = kWaves * kTile;         // tokens per work-group iteration
+  static constexpr int kLoads = kTileBytes / 1024;      // 1 KiB load instructions per tile
+  static constexpr int kRowPieces = kRowBytes / 16;     // 16-byte pieces per row: 8, 16, 32
+  static constexpr int kLaneElems = D / 4;              // MFMA: dims per lane per token
+  static constexpr int kLanePieces = kLaneElems * kElemBytes / 16;
+  static constexpr int kElemsPerPiece = 16 / kElemBytes;
+  static constexpr int kWaveLds = 2 * 2 * kTileBytes;   // 2 buffers x (K, V)
+  // LDS is one union, laid out per phase:
+  //   tiles:  [kWaves][2 buffers][K, V][kTileBytes]
+  //   merges: [0, kPartsBytes) wave o / partition (max, weight) staging,
+  //           then the per-wave (max, sum) and the last-group flag.
+  static constexpr int kWaveOBytes = kWaves * kMaxGroup * D * 4;     // wave merge o
+  static constexpr int kPartsBytes0 = (2 * kMaxGroup * kMergeParts + 3 * kMaxGroup) * 4;  // partition merge
+  static constexpr int kPartsBytes = kPartsBytes0 > kWaveOBytes ? kPartsBytes0 : kWaveOBytes;
+  static constexpr int kStatsOffset = kPartsBytes;                    // s_max, s_sum
+  static constexpr int kFlagOffset = kStatsOffset + 2 * kWaves * kMaxGroup * 4;
+  static constexpr int kMergeEnd = kFlagOffset + 16;
+  static constexpr int kLdsBytes = kWaves * kWaveLds > kMergeEnd ? kWaves * kWaveLds : kMergeEnd;
+  // Work groups one CU holds (160 KiB of LDS on gfx950), and the matching
+  // register budget: waves per SIMD = groups * kWaves / 4 (at least 1).
+  static constexpr int kGroupsPerCU = (160 * 1024) / kLdsBytes;
+  static constexpr int kWavesPerSimd = kGroupsPerCU * kWaves / 4 > 0 ? kGroupsPerCU * kWaves / 4 : 1;
+  static_assert(kLoads >= 1 && kRowPieces >= 8, "tile geometry");
 };
+
+// Swizzle of the 16-byte pieces of LDS row r: slot s holds piece s ^ sw(r).
+// With it, a K-operand read (16 rows, one piece each) and a transposed V
+// read (rows 4g+e, two to four neighbouring pieces each) touch 16 distinct
+// 4-bank groups.
+template <int ROW_PIECES>
+__device__ __forceinline__ int piece_swizzle(int r) {
+  return ROW_PIECES == 8 ? (r >> 1) & 7 : r & 15;
+}
 
 struct DecodeArgs {
   const void* q;
@@ -102,7 +111,7 @@ struct DecodeArgs {
   const void* block_table;
   int64_t bt_stride;  // elements
   const int32_t* kv_len;
-  const int32_t* work;  // (seq, partition) pairs
+  const int32_t* work;  // (seq, partition, kv_len, 0) quadruples
   int32_t* counters;    // [num_seqs * num_kv_heads], zero at rest
   void* out;
   int64_t out_stride_tok, out_stride_head;  // elements
@@ -139,32 +148,45 @@ __device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_F32>(const uint4& k, const uin
   return acc;
 }
 
-// O tile update for one 16-token tile: o[c] += P(16 heads x 16 tokens) V(16 tokens x 16 dims).
-template <int DTYPE, int D, int LDS_ROW>
+// O tile update for one 16-token tile from its swizzled LDS tile:
+// o[c] += P(16 heads x 16 tokens) V(16 tokens x 16 dims), V element
+// (row 4g+e, column 16c+t) per lane.
+template <int DTYPE, int D>
 __device__ __forceinline__ void mfma_pv(const float (&p)[4], const char* v_tile, int g, int t,
                                         f32x4 (&o)[D / 16]) {
+  using Tr = Traits<DTYPE, D>;
+  constexpr int RP = Tr::kRowPieces;
+  constexpr int EPP = Tr::kElemsPerPiece;
+  int row_base[4], row_sw[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    row_base[e] = (4 * g + e) * RP * 16;
+    row_sw[e] = piece_swizzle<RP>(4 * g + e);
+  }
   if constexpr (DTYPE == MV_DTYPE_F32) {
-    const float* vt = reinterpret_cast<const float*>(v_tile);
-    constexpr int rs = LDS_ROW / 4;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
+      const int col = 16 * c + t;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float vv = vt[(4 * g + e) * rs + 16 * c + t];
+        const int off = row_base[e] + (((col / EPP) ^ row_sw[e]) << 4) + (col % EPP) * 4;
+        const float vv = *reinterpret_cast<const float*>(v_tile + off);
         o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[e], vv, o[c], 0, 0, 0);
       }
     }
   } else {
-    const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_tile);
-    constexpr int rs = LDS_ROW / 2;
     s16x4 pa;
 #pragma unroll
     for (int e = 0; e < 4; ++e) pa[e] = static_cast<short>(from_f32<DTYPE>(p[e]));
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
+      const int col = 16 * c + t;
       s16x4 vb;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vb[e] = static_cast<short>(vt[(4 * g + e) * rs + 16 * c + t]);
+      for (int e = 0; e < 4; ++e) {
+        const int off = row_base[e] + (((col / EPP) ^ row_sw[e]) << 4) + (col % EPP) * 2;
+        vb[e] = *reinterpret_cast<const short*>(v_tile + off);
+      }
       if constexpr (DTYPE == MV_DTYPE_BF16) {
         o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[c], 0, 0, 0);
       } else {
@@ -198,19 +220,27 @@ __device__ __forceinline__ void wave_lds_order() {
 
 // ----------------------------------------------------------- the kernel ---
 
+// s_waitcnt vmcnt(N), N <= 63 (expcnt and lgkmcnt at their maxima; vmcnt
+// is split over bits [3:0] and [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+}
+
 template <int DTYPE, int D, typename BT>
 __global__ __launch_bounds__(kWaves * 64)
-__attribute__((amdgpu_waves_per_eu(MV_DECODE_WAVES_PER_SIMD))) void paged_decode_kernel(DecodeArgs a) {
+__attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged_decode_kernel(DecodeArgs a) {
   using Tr = Traits<DTYPE, D>;
   using raw_t = typename Elem<DTYPE>::raw;
-  constexpr int TPW = Tr::kTilesPerWave;
   constexpr int L = Tr::kLoads;
-  constexpr int QC = Tr::kLaneChunks;
+  constexpr int RP = Tr::kRowPieces;
+  constexpr int QP = Tr::kLanePieces;
 
   __shared__ __attribute__((aligned(16))) char s_lds[Tr::kLdsBytes];
-  __shared__ float s_max[kWaves][kMaxGroup];
-  __shared__ float s_sum[kWaves][kMaxGroup];
-  __shared__ int s_last;
+  float (*s_max)[kMaxGroup] = reinterpret_cast<float (*)[kMaxGroup]>(s_lds + Tr::kStatsOffset);
+  float (*s_sum)[kMaxGroup] = s_max + kWaves;
+  int& s_last = *reinterpret_cast<int*>(s_lds + Tr::kFlagOffset);
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -219,51 +249,72 @@ __attribute__((amdgpu_waves_per_eu(MV_DECODE_WAVES_PER_SIMD))) void paged_decode
 
   const int item = blockIdx.x / a.num_kv_heads;
   const int h = blockIdx.x - item * a.num_kv_heads;
-  const int b = a.work[2 * item];
-  const int part = a.work[2 * item + 1];
-  const int kv = a.kv_len[b];
+  const int4 wi = reinterpret_cast<const int4*>(a.work)[item];  // (seq, partition, kv_len, -)
+  const int b = wi.x;
+  const int part = wi.y;
+  const int kv = wi.z;
   const int n_parts = (kv + a.part_tokens - 1) / a.part_tokens;
   const int tok_begin = part * a.part_tokens;
   const int tok_end = min(kv, tok_begin + a.part_tokens);
   const int n_chunks = (tok_end - tok_begin + Tr::kChunk - 1) / Tr::kChunk;
   const int bs_mask = (1 << a.bs_log2) - 1;
   const BT* bt_row = static_cast<const BT*>(a.block_table) + b * a.bt_stride;
+  char* wave_lds = s_lds + wave * Tr::kWaveLds;  // [buffer][K, V][tile bytes]
 
-  char* k_lds = s_lds + wave * Tr::kWaveLds;
-  char* v_lds = k_lds + TPW * Tr::kLdsTile;
+  // LDS slot (64c + lane) of this wave's tile: its row, and the global
+  // piece it holds under the swizzle.
+  int slot_row[L], slot_piece[L];
+#pragma unroll
+  for (int c = 0; c < L; ++c) {
+    const int slot = 64 * c + lane;
+    slot_row[c] = slot / RP;
+    slot_piece[c] = (slot % RP) ^ piece_swizzle<RP>(slot_row[c]);
+  }
 
-  // Coalesced tile loads of chunk `ch`: piece 64c + lane of tile i.
-  auto load_chunk = [&](int ch, uint4 (&kr)[TPW][L], uint4 (&vr)[TPW][L]) {
+  // Block ids of this lane's slots in chunk `ch` (rows past the partition
+  // end read the last token's entry, so every call issues L loads).
+  auto load_block_ids = [&](int ch, int64_t (&blk)[L]) {
+    const int tile_tok = tok_begin + ch * Tr::kChunk + wave * kTile;
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int tile_tok = tok_begin + ch * Tr::kChunk + (wave * TPW + i) * kTile;
+    for (int c = 0; c < L; ++c) {
+      const int j = min(tile_tok + slot_row[c], tok_end - 1);
+      blk[c] = static_cast<int64_t>(bt_row[j >> a.bs_log2]);
+    }
+  };
+
+  // Issues the HBM -> LDS loads of this wave's tile of chunk `ch` into
+  // buffer `buf`; records which slots hold a token of the partition. Every
+  // call issues exactly 2L load instructions (the vmcnt waits count on it):
+  // slots outside the partition read the first pool row, and their V slots
+  // are zeroed once the loads have landed.
+  auto issue_tile = [&](int ch, int buf, const int64_t (&blk)[L], bool (&valid)[L]) {
+    const int tile_tok = tok_begin + ch * Tr::kChunk + wave * kTile;
+    char* kdst = wave_lds + buf * 2 * Tr::kTileBytes;
+    char* vdst = kdst + Tr::kTileBytes;
 #pragma unroll
-      for (int c = 0; c < L; ++c) {
-        const int piece = 64 * c + lane;
-        const int row = piece / Tr::kRowChunks;
-        const int col = piece - row * Tr::kRowChunks;
-        const int j = tile_tok + row;
-        bool ok = j < tok_end;
-        int64_t off = 0;
-        if (ok) {
-          const int64_t blk = static_cast<int64_t>(bt_row[j >> a.bs_log2]);
-          ok = blk >= 0 && blk < a.num_blocks;  // the plan rejects such tables
-          off = (((blk * a.num_kv_heads + h) << a.bs_log2) + (j & bs_mask)) * Tr::kRowBytes + col * 16;
-        }
-        kr[i][c] = ok ? *reinterpret_cast<const uint4*>(a.k_cache + off) : make_uint4(0, 0, 0, 0);
-        vr[i][c] = ok ? *reinterpret_cast<const uint4*>(a.v_cache + off) : make_uint4(0, 0, 0, 0);
-      }
+    for (int c = 0; c < L; ++c) {
+      const int j = tile_tok + slot_row[c];
+      // the plan rejects tables with entries outside the pool; the bound
+      // check only keeps a bad table from reading outside it
+      const bool ok = j < tok_end && blk[c] >= 0 && blk[c] < a.num_blocks;
+      const int64_t off =
+          ok ? (((blk[c] * a.num_kv_heads + h) << a.bs_log2) + (j & bs_mask)) * Tr::kRowBytes +
+                   slot_piece[c] * 16
+             : 0;
+      valid[c] = ok;
+      __builtin_amdgcn_global_load_lds(a.k_cache + off, kdst + c * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(a.v_cache + off, vdst + c * 1024, 16, 0, 0);
     }
   };
 
   // ---- Q^T operand: head t of the group, dims of quarter g --------------
-  uint4 qr[QC];
+  uint4 qr[QP];
   {
     const bool ok = t < a.n_rep;
     const raw_t* qp = static_cast<const raw_t*>(a.q) + b * a.q_stride_tok +
                       (h * a.n_rep + (ok ? t : 0)) * a.q_stride_head + g * Tr::kLaneElems;
 #pragma unroll
-    for (int c = 0; c < QC; ++c)
+    for (int c = 0; c < QP; ++c)
       qr[c] = ok ? reinterpret_cast<const uint4*>(qp)[c] : make_uint4(0, 0, 0, 0);
   }
 
@@ -273,64 +324,45 @@ __attribute__((amdgpu_waves_per_eu(MV_DECODE_WAVES_PER_SIMD))) void paged_decode
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Writes the chunk held in registers to the wave's LDS tiles.
-  auto stage_chunk = [&](const uint4 (&kr)[TPW][L], const uint4 (&vr)[TPW][L]) {
+  // Attention over this wave's tile of chunk `ch` in buffer `buf`.
+  auto compute_tile = [&](int ch, int buf) {
+    const char* k_tile = wave_lds + buf * 2 * Tr::kTileBytes;
+    const char* v_tile = k_tile + Tr::kTileBytes;
+    // S^T = K Q^T: lane (g, t) reads row t, pieces g*QP .. g*QP+QP-1
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const int ksw = piece_swizzle<RP>(t);
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-#pragma unroll
-      for (int c = 0; c < L; ++c) {
-        const int piece = 64 * c + lane;
-        const int row = piece / Tr::kRowChunks;
-        const int col = piece - row * Tr::kRowChunks;
-        const int lo = i * Tr::kLdsTile + row * Tr::kLdsRow + col * 16;
-        *reinterpret_cast<uint4*>(k_lds + lo) = kr[i][c];
-        *reinterpret_cast<uint4*>(v_lds + lo) = vr[i][c];
-      }
+    for (int c = 0; c < QP; ++c) {
+      const uint4 kp = *reinterpret_cast<const uint4*>(k_tile + (t * RP + ((g * QP + c) ^ ksw)) * 16);
+      acc = mfma_qk<DTYPE>(kp, qr[c], acc);
     }
-  };
-
-  // Attention over the chunk staged in LDS (online softmax update).
-  auto compute_chunk = [&](int ch) {
-    // S^T = K Q^T
-    float s[TPW][4];
+    const int tile_tok = tok_begin + ch * Tr::kChunk + wave * kTile;
+    float s[4];
     float mc = kNegInf;
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const char* krow = k_lds + i * Tr::kLdsTile + t * Tr::kLdsRow + g * (Tr::kLaneElems * Tr::kElemBytes);
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < QC; ++c) acc = mfma_qk<DTYPE>(reinterpret_cast<const uint4*>(krow)[c], qr[c], acc);
-      const int tile_tok = tok_begin + ch * Tr::kChunk + (wave * TPW + i) * kTile;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[i][e] = tile_tok + 4 * g + e < tok_end ? acc[e] * a.scale_log2 : kNegInf;
-        mc = fmaxf(mc, s[i][e]);
-      }
+    for (int e = 0; e < 4; ++e) {
+      s[e] = tile_tok + 4 * g + e < tok_end ? acc[e] * a.scale_log2 : kNegInf;
+      mc = fmaxf(mc, s[e]);
     }
-    // head t's max over the chunk: lanes t, t+16, t+32, t+48
+    // head t's max over the tile: lanes t, t+16, t+32, t+48
     mc = fmaxf(mc, __shfl_xor(mc, 16));
     mc = fmaxf(mc, __shfl_xor(mc, 32));
     const float m_new = fmaxf(m_run, mc);
     const float m_ref = m_new == kNegInf ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
-
     // P = exp2(S - m), rounded to the MFMA input type; the sum uses the
     // rounded values so O / l is an exact convex combination of V rows.
-    float p[TPW][4];
+    float p[4];
     float lc = 0.f;
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        p[i][e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[i][e] - m_ref)));
-        lc += p[i][e];
-      }
+    for (int e = 0; e < 4; ++e) {
+      p[e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e] - m_ref)));
+      lc += p[e];
     }
     lc += __shfl_xor(lc, 16);
     lc += __shfl_xor(lc, 32);
     l_run = l_run * alpha + lc;
     m_run = m_new;
-
     // rescale O rows (head 4g+e takes the alpha of lane 4g+e)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -338,22 +370,51 @@ __attribute__((amdgpu_waves_per_eu(MV_DECODE_WAVES_PER_SIMD))) void paged_decode
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) o[c][e] *= ar;
     }
-    // O += P V
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) mfma_pv<DTYPE, D, Tr::kLdsRow>(p[i], v_lds + i * Tr::kLdsTile, g, t, o);
+    mfma_pv<DTYPE, D>(p, v_tile, g, t, o);
   };
 
-  // ---- chunk loop: the next chunk's loads are in flight while the staged
-  // chunk is computed (registers -> LDS tile -> registers refill) ---------
+  // Zeroes the V slots of tokens that were not loaded (P is 0 there, but
+  // the stale LDS bytes could hold NaN/Inf and 0 * NaN = NaN).
+  auto zero_invalid_v = [&](int buf, const bool (&valid)[L]) {
+    char* vdst = wave_lds + buf * 2 * Tr::kTileBytes + Tr::kTileBytes;
+#pragma unroll
+    for (int c = 0; c < L; ++c)
+      if (!valid[c]) *reinterpret_cast<uint4*>(vdst + c * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
+  };
+
+  // ---- tile loop ---------------------------------------------------------
+  // Step ch: (1) load the block ids of chunk ch+2, (2) issue chunk ch+1's
+  // tile into the other buffer, (3) wait for chunk ch's tile, (4) compute.
+  // The block ids of ch+1 were loaded before chunk ch's tile was issued, so
+  // using them never waits on that tile (vmcnt retires loads in order), and
+  // two tiles are in flight while a third is computed.
+  auto step = [&](int ch, int buf, const bool (&val_cur)[L], const int64_t (&blk_next)[L],
+                  bool (&val_next)[L], int64_t (&blk_pref)[L]) {
+    const bool has1 = ch + 1 < n_chunks;
+    const bool has2 = ch + 2 < n_chunks;
+    if (has2) load_block_ids(ch + 2, blk_pref);
+    if (has1) issue_tile(ch + 1, buf ^ 1, blk_next, val_next);
+    asm volatile("" ::: "memory");
+    if (has2) wait_vmcnt<3 * L>();
+    else if (has1) wait_vmcnt<2 * L>();
+    else wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    zero_invalid_v(buf, val_cur);
+    wave_lds_order();
+    compute_tile(ch, buf);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile's LDS reads are done
+    wave_lds_order();
+  };
   {
-    uint4 kr[TPW][L], vr[TPW][L];
-    load_chunk(0, kr, vr);
-    for (int ch = 0; ch < n_chunks; ++ch) {
-      stage_chunk(kr, vr);
-      wave_lds_order();
-      if (ch + 1 < n_chunks) load_chunk(ch + 1, kr, vr);
-      compute_chunk(ch);
-      wave_lds_order();  // the next iteration overwrites the tiles
+    int64_t blk_a[L], blk_b[L];
+    bool val_a[L], val_b[L];
+    load_block_ids(0, blk_a);
+    if (n_chunks > 1) load_block_ids(1, blk_b);
+    issue_tile(0, 0, blk_a, val_a);
+    for (int ch = 0; ch < n_chunks; ch += 2) {
+      step(ch, 0, val_a, blk_b, val_b, blk_a);
+      if (ch + 1 >= n_chunks) break;
+      step(ch + 1, 1, val_b, blk_a, val_a, blk_b);
     }
   }
 
@@ -420,50 +481,89 @@ __attribute__((amdgpu_waves_per_eu(MV_DECODE_WAVES_PER_SIMD))) void paged_decode
   }
   __syncthreads();
   if (!s_last) return;
-  // (max, sum) of every partial of the group's heads -> LDS in one round of
-  // loads; per-head normalised weights; then each output element streams
-  // its partials kMergeLoads at a time.
-  float* s_m = reinterpret_cast<float*>(s_lds);  // [n_rep][n_parts]
-  float* s_w = s_m + kMaxGroup * kMaxParts;      // [n_rep][n_parts]
-  const int n_ml = a.n_rep * n_parts;
-  for (int i = threadIdx.x; i < n_ml; i += kWaves * 64) {
-    const int r = i / n_parts;
-    const int64_t sl = slot_base + static_cast<int64_t>(r) * a.max_parts + (i - r * n_parts);
-    s_m[i] = load_coherent(a.ws_ml + 2 * sl);
-    s_w[i] = load_coherent(a.ws_ml + 2 * sl + 1);
-  }
-  __syncthreads();
-  if (threadIdx.x < a.n_rep) {
-    float* m_r = s_m + threadIdx.x * n_parts;
-    float* w_r = s_w + threadIdx.x * n_parts;
-    float mx = kNegInf;
-    for (int p = 0; p < n_parts; ++p) mx = fmaxf(mx, m_r[p]);
-    float sum = 0.f;
-    for (int p = 0; p < n_parts; ++p) {
-      w_r[p] *= __builtin_amdgcn_exp2f(m_r[p] - mx);
-      sum += w_r[p];
-    }
-    const float inv = 1.f / sum;
-    for (int p = 0; p < n_parts; ++p) w_r[p] *= inv;
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < n_out; idx += kWaves * 64) {
-    const int r = idx / D;
-    const int d = idx - r * D;
-    const int64_t s0 = slot_base + static_cast<int64_t>(r) * a.max_parts;
-    const float* w_r = s_w + r * n_parts;
-    float acc = 0.f;
-    for (int p0 = 0; p0 < n_parts; p0 += kMergeLoads) {
-      float ov[kMergeLoads];
+  // One round of loads per kMergeParts partitions: every thread issues the
+  // partial values of its outputs together with its share of the
+  // (max, sum) pairs, which go through LDS to form the per-head weights.
+  float* s_m = reinterpret_cast<float*>(s_lds);  // [kMaxGroup][kMergeParts]
+  float* s_w = s_m + kMaxGroup * kMergeParts;    // [kMaxGroup][kMergeParts]
+  float* s_f = s_w + kMaxGroup * kMergeParts;    // [kMaxGroup] running max
+  float* s_g = s_f + kMaxGroup;                  // [kMaxGroup] rescale of the running sums
+  float* s_n = s_g + kMaxGroup;                  // [kMaxGroup] running weight sum
+  constexpr int kOuts = (kMaxGroup * D + kWaves * 64 - 1) / (kWaves * 64);
+  float acc[kOuts];
 #pragma unroll
-      for (int u = 0; u < kMergeLoads; ++u)
-        ov[u] = p0 + u < n_parts ? load_coherent(a.ws_o + (s0 + p0 + u) * D + d) : 0.f;
+  for (int k = 0; k < kOuts; ++k) acc[k] = 0.f;
+  if (threadIdx.x < kMaxGroup) {
+    s_f[threadIdx.x] = kNegInf;
+    s_n[threadIdx.x] = 0.f;
+  }
+  for (int p0 = 0; p0 < n_parts; p0 += kMergeParts) {
+    const int np = min(kMergeParts, n_parts - p0);
+    // (1) loads: partial values of this thread's outputs + (max, sum) pairs
+    float ov[kOuts][kMergeParts];
 #pragma unroll
-      for (int u = 0; u < kMergeLoads; ++u)
-        if (p0 + u < n_parts) acc += w_r[p0 + u] * ov[u];
+    for (int k = 0; k < kOuts; ++k) {
+      const int idx = threadIdx.x + k * kWaves * 64;
+      const int r = idx / D;
+      const int d = idx - r * D;
+      const int64_t s0 = slot_base + static_cast<int64_t>(r) * a.max_parts + p0;
+#pragma unroll
+      for (int pp = 0; pp < kMergeParts; ++pp)
+        ov[k][pp] = (idx < n_out && pp < np) ? load_coherent(a.ws_o + (s0 + pp) * D + d) : 0.f;
     }
-    raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head;
-    op[d] = from_f32<DTYPE>(acc);
+    float mv = kNegInf, lv = 0.f;
+    const int mi = threadIdx.x;  // (head, partition) pair of this thread
+    const int mr = mi / kMergeParts, mp = mi - mr * kMergeParts;
+    if (mi < kMaxGroup * kMergeParts && mr < a.n_rep && mp < np) {
+      const int64_t sl = slot_base + static_cast<int64_t>(mr) * a.max_parts + p0 + mp;
+      mv = load_coherent(a.ws_ml + 2 * sl);
+      lv = load_coherent(a.ws_ml + 2 * sl + 1);
+    }
+    __syncthreads();  // previous round's LDS readers are done
+    if (mi < kMaxGroup * kMergeParts) {
+      s_m[mi] = mv;
+      s_w[mi] = lv;
+    }
+    __syncthreads();
+    // (2) per-head weights of this round, relative to the running max
+    if (threadIdx.x < a.n_rep) {
+      const int r = threadIdx.x;
+      float mx = s_f[r];
+      for (int pp = 0; pp < np; ++pp) mx = fmaxf(mx, s_m[r * kMergeParts + pp]);
+      const float g = s_f[r] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(s_f[r] - mx);
+      float sum = s_n[r] * g;
+      for (int pp = 0; pp < np; ++pp) {
+        const float w = s_w[r * kMergeParts + pp] * __builtin_amdgcn_exp2f(s_m[r * kMergeParts + pp] - mx);
+        s_w[r * kMergeParts + pp] = w;
+        sum += w;
+      }
+      s_f[r] = mx;
+      s_g[r] = g;
+      s_n[r] = sum;
+    }
+    __syncthreads();
+    // (3) accumulate
+#pragma unroll
+    for (int k = 0; k < kOuts; ++k) {
+      const int idx = threadIdx.x + k * kWaves * 64;
+      if (idx < n_out) {
+        const int r = idx / D;
+        float sacc = acc[k] * s_g[r];
+#pragma unroll
+        for (int pp = 0; pp < kMergeParts; ++pp) sacc += s_w[r * kMergeParts + pp] * ov[k][pp];
+        acc[k] = sacc;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kOuts; ++k) {
+    const int idx = threadIdx.x + k * kWaves * 64;
+    if (idx < n_out) {
+      const int r = idx / D;
+      const int d = idx - r * D;
+      raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head;
+      op[d] = from_f32<DTYPE>(acc[k] / s_n[r]);
+    }
   }
   if (threadIdx.x == 0)  // ready for the next call
     __hip_atomic_store(&a.counters[b * a.num_kv_heads + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -545,8 +645,9 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const int most_chunks = block_max(max_chunks, s_red);
   const int64_t groups = static_cast<int64_t>(total_chunks) * a.num_kv_heads;
   // enough work groups for the device, at most kMaxParts partitions per sequence
+  const int64_t target = std::max(1, a.target_groups);
   const int per_part = static_cast<int>(std::max<int64_t>(
-      std::max<int64_t>(1, groups / std::max(1, a.target_groups)),
+      std::max<int64_t>(1, (groups + target - 1) / target),
       (most_chunks + kMaxParts - 1) / kMaxParts));
   const int part_tokens = per_part * a.chunk_tokens;
 
@@ -574,8 +675,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     for (int p = 0; p < np; ++p) {
       const int64_t idx = start + p;
       if (idx < a.work_cap) {
-        a.work[2 * idx] = b;
-        a.work[2 * idx + 1] = p;
+        reinterpret_cast<int4*>(a.work)[idx] = make_int4(b, p, static_cast<int>(kvp[b]), 0);
       }
     }
     running += s_scan[kPlanThreads - 1];
@@ -617,17 +717,19 @@ size_t ws_o_bytes(int64_t num_seqs, int64_t hq, int64_t d, int64_t parts) {
   return static_cast<size_t>(num_seqs * hq * parts * d * 4);
 }
 
-template <int DTYPE, int D>
-int chunk_of() { return Traits<DTYPE, D>::kChunk; }
-
-int chunk_tokens(int head_dim, int dtype) {
+template <template <int, int> class Q>
+int trait_value(int head_dim, int dtype) {
   const bool d64 = head_dim == 64;
   switch (dtype) {
-    case MV_DTYPE_F32: return d64 ? chunk_of<MV_DTYPE_F32, 64>() : chunk_of<MV_DTYPE_F32, 128>();
-    case MV_DTYPE_F16: return d64 ? chunk_of<MV_DTYPE_F16, 64>() : chunk_of<MV_DTYPE_F16, 128>();
-    default: return d64 ? chunk_of<MV_DTYPE_BF16, 64>() : chunk_of<MV_DTYPE_BF16, 128>();
+    case MV_DTYPE_F32: return d64 ? Q<MV_DTYPE_F32, 64>::value : Q<MV_DTYPE_F32, 128>::value;
+    case MV_DTYPE_F16: return d64 ? Q<MV_DTYPE_F16, 64>::value : Q<MV_DTYPE_F16, 128>::value;
+    default: return d64 ? Q<MV_DTYPE_BF16, 64>::value : Q<MV_DTYPE_BF16, 128>::value;
   }
 }
+template <int DTYPE, int D> struct ChunkOf { static constexpr int value = Traits<DTYPE, D>::kChunk; };
+template <int DTYPE, int D> struct GroupsOf { static constexpr int value = Traits<DTYPE, D>::kGroupsPerCU; };
+
+int chunk_tokens(int head_dim, int dtype) { return trait_value<ChunkOf>(head_dim, dtype); }
 
 template <int DTYPE, int D, typename BT>
 int launch_decode(const DecodeArgs& a, int num_items, hipStream_t s) {
@@ -655,6 +757,11 @@ int launch_decode_d(const DecodeArgs& a, int d, bool bt64, int num_items, hipStr
 extern "C" int mv_decode_chunk_tokens(int32_t head_dim, int32_t dtype) {
   if ((head_dim != 64 && head_dim != 128) || mv::dtype_bytes(dtype) == 0) return 0;
   return mv::chunk_tokens(head_dim, dtype);
+}
+
+extern "C" int mv_decode_groups_per_cu(int32_t head_dim, int32_t dtype) {
+  if ((head_dim != 64 && head_dim != 128) || mv::dtype_bytes(dtype) == 0) return 0;
+  return mv::trait_value<mv::GroupsOf>(head_dim, dtype);
 }
 
 extern "C" size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,

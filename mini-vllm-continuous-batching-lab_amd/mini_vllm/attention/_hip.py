@@ -49,6 +49,7 @@ SIGNATURES = {
     "mv_abi_version": (ctypes.c_int, []),
     "mv_last_error": (ctypes.c_char_p, []),
     "mv_decode_chunk_tokens": (ctypes.c_int, [_I32, _I32]),
+    "mv_decode_groups_per_cu": (ctypes.c_int, [_I32, _I32]),
     "mv_kv_cache_write": (ctypes.c_int, [
         _P, _I64, _I64,            # key, strides
         _P, _I64, _I64,            # value, strides

@@ -221,23 +221,27 @@ class DecodePlan:
 
     block_table: torch.Tensor  # [num_seqs, max_blocks] int32/int64 on the device
     kv_len_i32: torch.Tensor   # [num_seqs] int32
-    work: torch.Tensor         # [2 * capacity] int32 (seq, partition) pairs
+    work: torch.Tensor         # [4 * capacity] int32 (seq, partition, kv_len, 0)
     counters: torch.Tensor     # [num_seqs * num_kv_heads] int32, zero between calls
     num_items: int
     max_parts: int
     partition_tokens: int
 
 
-# Work groups per compute unit the partition size aims for (override:
-# MVATTN_GROUPS_PER_CU).
-GROUPS_PER_CU = int(os.environ.get("MVATTN_GROUPS_PER_CU", "4"))
+# The partition size aims for as many work groups as the device holds at
+# once (work groups per CU from the library, times the CU count), so the
+# whole grid runs in one dispatch round. MVATTN_GROUPS_PER_CU overrides the
+# per-CU figure.
 _CU_COUNT: dict = {}
 
 
-def _target_groups(device: torch.device) -> int:
+def _target_groups(device: torch.device, head_dim: int, dtype: torch.dtype) -> int:
     if device not in _CU_COUNT:
         _CU_COUNT[device] = torch.cuda.get_device_properties(device).multi_processor_count
-    return GROUPS_PER_CU * _CU_COUNT[device]
+    per_cu = os.environ.get("MVATTN_GROUPS_PER_CU")
+    if per_cu is None:
+        per_cu = _hip.load().mv_decode_groups_per_cu(head_dim, _hip.MV_DTYPE[dtype])
+    return max(1, int(per_cu)) * _CU_COUNT[device]
 
 
 def plan_decode(
@@ -287,14 +291,15 @@ def plan_decode(
     max_blocks = bt.shape[1] if bt.dim() == 2 else 0
     cap = num_seqs * max(1, math.ceil(max_blocks * block_size / chunk))
     kv32 = torch.empty(max(num_seqs, 1), dtype=torch.int32, device=device)
-    work = torch.empty(2 * max(cap, 1), dtype=torch.int32, device=device)
+    work = torch.empty(4 * max(cap, 1), dtype=torch.int32, device=device)
     counters = torch.empty(max(num_seqs * num_kv_heads, 1), dtype=torch.int32, device=device)
     status = torch.empty(_hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
     _hip.check(
         lib.mv_decode_plan(
             _ptr(kv), int(kv.dtype == torch.int64), _ptr(bt), int(bt.dtype == torch.int64),
             bt.stride(0) if bt.dim() == 2 else 0, num_seqs, max_blocks, block_size,
-            num_blocks, chunk, num_kv_heads, _target_groups(device), _ptr(kv32), _ptr(work),
+            num_blocks, chunk, num_kv_heads, _target_groups(device, head_dim, dtype), _ptr(kv32),
+            _ptr(work),
             cap, _ptr(counters), _ptr(status), _stream(device),
         ),
         "mv_decode_plan",

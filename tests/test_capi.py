@@ -60,10 +60,12 @@ def test_every_declared_symbol_is_exported_and_typed(lib):
 
 def test_abi_queries(lib):
     assert lib.mv_abi_version() == _hip.ABI_VERSION == 1
-    assert lib.mv_decode_chunk_tokens(64, 2) == 128      # 4 waves x 2 tiles x 16
-    assert lib.mv_decode_chunk_tokens(128, 2) == 64      # 4 waves x 1 tile x 16
-    assert lib.mv_decode_chunk_tokens(64, 0) == 64
+    assert lib.mv_decode_chunk_tokens(64, 2) == 64       # 4 waves x one 16-token tile
+    assert lib.mv_decode_chunk_tokens(128, 0) == 64
     assert lib.mv_decode_chunk_tokens(96, 2) == 0
+    assert lib.mv_decode_groups_per_cu(64, 2) == 5       # 32 KiB of LDS per group
+    assert lib.mv_decode_groups_per_cu(128, 2) == 2
+    assert lib.mv_decode_groups_per_cu(96, 2) == 0
 
 
 def test_workspace_bytes(lib):
@@ -84,7 +86,7 @@ DECODE_PARAMS = [
 def _decode_args(**kw):
     base = dict(query=None, q_stride_tok=0, q_stride_head=0, key_cache=None, value_cache=None,
                 block_table=None, bt_is_i64=1, bt_stride=0, kv_len_i32=None, work_items=None,
-                num_work_items=1, partition_tokens=128, max_partitions=1, counters=None, out=None,
+                num_work_items=1, partition_tokens=64, max_partitions=1, counters=None, out=None,
                 out_stride_tok=0, out_stride_head=0, scale=0.125, num_seqs=1, num_q_heads=14,
                 num_kv_heads=2, head_dim=64, block_size=16, num_blocks=10, dtype=2,
                 workspace=None, workspace_bytes=0, stream=None)
