@@ -57,11 +57,14 @@ namespace {
 #ifndef MV_DECODE_WAVES
 #define MV_DECODE_WAVES 4
 #endif
+#ifndef MV_DECODE_STAGES
+#define MV_DECODE_STAGES 3
+#endif
 constexpr int kWaves = MV_DECODE_WAVES;
 constexpr int kTile = 16;
 constexpr int kMaxGroup = 16;   // MFMA N: query heads per kv head
-constexpr int kMaxParts = 128;  // partitions per sequence (the plan enforces it)
-constexpr int kMergeParts = 8;  // partitions merged per round of loads
+constexpr int kMaxParts = 128;  // partitions per sequence the plan aims for
+constexpr int kIdCap = 512;     // block ids one partition may span (staged in LDS)
 constexpr float kNegInf = -__builtin_huge_valf();
 
 template <int DTYPE, int D>
@@ -75,23 +78,35 @@ struct Traits {
   static constexpr int kLaneElems = D / 4;              // MFMA: dims per lane per token
   static constexpr int kLanePieces = kLaneElems * kElemBytes / 16;
   static constexpr int kElemsPerPiece = 16 / kElemBytes;
-  static constexpr int kWaveLds = 2 * 2 * kTileBytes;   // 2 buffers x (K, V)
+  // Tile buffers per wave: up to S-1 tiles stream in while one is computed.
+  // Larger tiles get 2 stages so two work groups still fit one CU.
+  static constexpr int kStages = kTileBytes <= 2048 ? MV_DECODE_STAGES
+                                                    : (MV_DECODE_STAGES < 2 ? MV_DECODE_STAGES : 2);
+  static constexpr int kStageBytes = 2 * kTileBytes;    // K tile, V tile
+  static constexpr int kWaveLds = kStages * kStageBytes;
   // LDS is one union, laid out per phase:
-  //   tiles:  [kWaves][2 buffers][K, V][kTileBytes]
-  //   merges: [0, kPartsBytes) wave o / partition (max, weight) staging,
-  //           then the per-wave (max, sum) and the last-group flag.
+  //   tile loop: [kWaves][kStages][K, V][kTileBytes], then the partition's
+  //              block ids (int32, kIdCap);
+  //   merges:    [0, kWaveOBytes) the waves' o, then their (max, sum)
+  //              and the last-group flag.
+  static constexpr int kIdsOffset = kWaves * kWaveLds;
+  static constexpr int kTilesEnd = kIdsOffset + kIdCap * 4;
   static constexpr int kWaveOBytes = kWaves * kMaxGroup * D * 4;     // wave merge o
-  static constexpr int kPartsBytes0 = (2 * kMaxGroup * kMergeParts + 3 * kMaxGroup) * 4;  // partition merge
-  static constexpr int kPartsBytes = kPartsBytes0 > kWaveOBytes ? kPartsBytes0 : kWaveOBytes;
-  static constexpr int kStatsOffset = kPartsBytes;                    // s_max, s_sum
+  static constexpr int kStatsOffset = kWaveOBytes;                    // s_max, s_sum
   static constexpr int kFlagOffset = kStatsOffset + 2 * kWaves * kMaxGroup * 4;
   static constexpr int kMergeEnd = kFlagOffset + 16;
-  static constexpr int kLdsBytes = kWaves * kWaveLds > kMergeEnd ? kWaves * kWaveLds : kMergeEnd;
+  static constexpr int kLdsBytes = kTilesEnd > kMergeEnd ? kTilesEnd : kMergeEnd;
+  static_assert(kStages >= 2 && kStages <= 4, "tile stages");
   // Work groups one CU holds (160 KiB of LDS on gfx950), and the matching
   // register budget: waves per SIMD = groups * kWaves / 4 (at least 1).
   static constexpr int kGroupsPerCU = (160 * 1024) / kLdsBytes;
   static constexpr int kWavesPerSimd = kGroupsPerCU * kWaves / 4 > 0 ? kGroupsPerCU * kWaves / 4 : 1;
+  // Epilogue: 16 threads per query head, D/16 dims each; the partition
+  // merge folds kMergeRound partitions per round of loads.
+  static constexpr int kDimsPerThread = D / 16;
+  static constexpr int kMergeRound = 1024 / D;
   static_assert(kLoads >= 1 && kRowPieces >= 8, "tile geometry");
+  static_assert(kDimsPerThread % 4 == 0, "epilogue vectors");
 };
 
 // Swizzle of the 16-byte pieces of LDS row r: slot s holds piece s ^ sw(r).
@@ -197,26 +212,24 @@ __device__ __forceinline__ void mfma_pv(const float (&p)[4], const char* v_tile,
   }
 }
 
-// Device-coherent (agent-scope) fp32 store / load: `global_store/load ... sc1`
+// Device-coherent (agent-scope) 8-byte store / load: `global_store/load ... sc1`
 // on gfx950, visible across the XCDs' separate L2 caches without any cache
 // writeback or invalidate.
-__device__ __forceinline__ void store_coherent(float* p, float v) {
+__device__ __forceinline__ void store_coherent_u64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float load_coherent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ uint64_t load_coherent_u64(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Two fp32 values in one 8-byte word (lo = first in memory).
+__device__ __forceinline__ uint64_t pack_f32x2(float lo, float hi) {
+  return static_cast<uint64_t>(__float_as_uint(lo)) | (static_cast<uint64_t>(__float_as_uint(hi)) << 32);
+}
+__device__ __forceinline__ float unpack_lo(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
+__device__ __forceinline__ float unpack_hi(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); }
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this
 // wave's vector memory operations, stores included, are complete.
 constexpr unsigned kWaitVmcnt0 = 0x0F70;
-
-// Stops the compiler from moving LDS accesses of one wave across this
-// point; the hardware completes one wave's LDS accesses in issue order.
-__device__ __forceinline__ void wave_lds_order() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // ----------------------------------------------------------- the kernel ---
 
@@ -227,6 +240,40 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt");
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
 }
+
+// Waits until at most R * PER vector memory instructions of this wave are
+// outstanding, R <= RMAX (R is wave-uniform, the count an immediate).
+template <int PER, int RMAX>
+__device__ __forceinline__ void wait_vmcnt_groups(int r) {
+  if constexpr (RMAX == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (r >= RMAX) wait_vmcnt<PER * RMAX>();
+    else wait_vmcnt_groups<PER, RMAX - 1>(r);
+  }
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
+}
+
+// HBM -> LDS copy of 16 bytes per lane: lane l's bytes land at LDS address
+// lds_base + 16 l (lds_base wave-uniform, passed in M0). Written as inline
+// asm on purpose: the compiler then does not see a pending LDS write and
+// does not put a vmcnt(0) in front of every later LDS access (which would
+// wait for the tiles still streaming into the other buffers); the tile loop
+// counts these loads itself. The "memory" clobber keeps LDS accesses of the
+// wave on their side of the copy.
+__device__ __forceinline__ void copy_to_lds_16B(const char* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+
+template <int C>
+struct IntC {
+  static constexpr int value = C;
+};
 
 template <int DTYPE, int D, typename BT>
 __global__ __launch_bounds__(kWaves * 64)
@@ -242,7 +289,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   float (*s_sum)[kMaxGroup] = s_max + kWaves;
   int& s_last = *reinterpret_cast<int*>(s_lds + Tr::kFlagOffset);
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int t = lane & 15;  // MFMA: token row (K operand) / head column (results)
   const int g = lane >> 4;  // MFMA: dim quarter (K operand) / token quad (results)
@@ -259,7 +306,29 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const int n_chunks = (tok_end - tok_begin + Tr::kChunk - 1) / Tr::kChunk;
   const int bs_mask = (1 << a.bs_log2) - 1;
   const BT* bt_row = static_cast<const BT*>(a.block_table) + b * a.bt_stride;
-  char* wave_lds = s_lds + wave * Tr::kWaveLds;  // [buffer][K, V][tile bytes]
+  const int first_blk = tok_begin >> a.bs_log2;
+  const int n_ids = min(((tok_end - 1) >> a.bs_log2) - first_blk + 1, kIdCap);
+  int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
+  const char* wave_tiles = s_lds + wave * Tr::kWaveLds;  // [stage][K, V][tile bytes]
+  const uint32_t wave_tiles_lds = lds_address(s_lds) + wave * Tr::kWaveLds;
+
+  // ---- Q^T operand: head t of the group, dims of quarter g --------------
+  // Columns t >= n_rep repeat head 0 of the group: MFMA columns (and the
+  // softmax state per column) are independent, and those columns are never
+  // written out.
+  uint4 qr[QP];
+  {
+    const raw_t* qp = static_cast<const raw_t*>(a.q) + b * a.q_stride_tok +
+                      (h * a.n_rep + (t < a.n_rep ? t : 0)) * a.q_stride_head + g * Tr::kLaneElems;
+#pragma unroll
+    for (int c = 0; c < QP; ++c) qr[c] = reinterpret_cast<const uint4*>(qp)[c];
+  }
+
+  // ---- the partition's block ids -> LDS (-1: not a pool block) ------------
+  for (int i = threadIdx.x; i < n_ids; i += kWaves * 64) {
+    const int64_t blk = static_cast<int64_t>(bt_row[first_blk + i]);
+    s_ids[i] = (blk >= 0 && blk < a.num_blocks) ? static_cast<int32_t>(blk) : -1;
+  }
 
   // LDS slot (64c + lane) of this wave's tile: its row, and the global
   // piece it holds under the swizzle.
@@ -270,53 +339,44 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     slot_row[c] = slot / RP;
     slot_piece[c] = (slot % RP) ^ piece_swizzle<RP>(slot_row[c]);
   }
-
-  // Block ids of this lane's slots in chunk `ch` (rows past the partition
-  // end read the last token's entry, so every call issues L loads).
-  auto load_block_ids = [&](int ch, int64_t (&blk)[L]) {
-    const int tile_tok = tok_begin + ch * Tr::kChunk + wave * kTile;
+  // The Q registers pass through an empty asm here, so the compiler waits
+  // for their loads now rather than inside the tile loop, where its wait
+  // would also drain the tile copies in flight.
 #pragma unroll
-    for (int c = 0; c < L; ++c) {
-      const int j = min(tile_tok + slot_row[c], tok_end - 1);
-      blk[c] = static_cast<int64_t>(bt_row[j >> a.bs_log2]);
-    }
-  };
+  for (int c = 0; c < QP; ++c) asm volatile("" : "+v"(qr[c].x), "+v"(qr[c].y), "+v"(qr[c].z), "+v"(qr[c].w));
+  __syncthreads();  // block ids visible to every wave
 
-  // Issues the HBM -> LDS loads of this wave's tile of chunk `ch` into
-  // buffer `buf`; records which slots hold a token of the partition. Every
-  // call issues exactly 2L load instructions (the vmcnt waits count on it):
-  // slots outside the partition read the first pool row, and their V slots
-  // are zeroed once the loads have landed.
-  auto issue_tile = [&](int ch, int buf, const int64_t (&blk)[L], bool (&valid)[L]) {
-    const int tile_tok = tok_begin + ch * Tr::kChunk + wave * kTile;
-    char* kdst = wave_lds + buf * 2 * Tr::kTileBytes;
-    char* vdst = kdst + Tr::kTileBytes;
+  // Issues the HBM -> LDS copies of this wave's tile of chunk `k` into
+  // stage ST and returns, one bit per load, which slots hold a token of the
+  // partition. Every call issues exactly 2L load instructions (the vmcnt
+  // waits count on it): slots outside the partition read the first pool
+  // row, and their V slots are zeroed once the loads have landed.
+  auto issue_tile = [&](int k, auto st_c) __attribute__((always_inline)) -> unsigned {
+    constexpr int ST = decltype(st_c)::value;
+    const int tile_tok = tok_begin + k * Tr::kChunk + wave * kTile;
+    int64_t off[L];
+    unsigned valid = 0;
 #pragma unroll
     for (int c = 0; c < L; ++c) {
       const int j = tile_tok + slot_row[c];
-      // the plan rejects tables with entries outside the pool; the bound
-      // check only keeps a bad table from reading outside it
-      const bool ok = j < tok_end && blk[c] >= 0 && blk[c] < a.num_blocks;
-      const int64_t off =
-          ok ? (((blk[c] * a.num_kv_heads + h) << a.bs_log2) + (j & bs_mask)) * Tr::kRowBytes +
-                   slot_piece[c] * 16
-             : 0;
-      valid[c] = ok;
-      __builtin_amdgcn_global_load_lds(a.k_cache + off, kdst + c * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(a.v_cache + off, vdst + c * 1024, 16, 0, 0);
+      const int jj = min(j, tok_end - 1);
+      const int id = s_ids[min((jj >> a.bs_log2) - first_blk, kIdCap - 1)];
+      const bool ok = j < tok_end && id >= 0;
+      off[c] = ok ? (((static_cast<int64_t>(id) * a.num_kv_heads + h) << a.bs_log2) + (jj & bs_mask)) *
+                            Tr::kRowBytes +
+                        slot_piece[c] * 16
+                  : 0;
+      valid |= ok ? (1u << c) : 0u;
     }
-  };
-
-  // ---- Q^T operand: head t of the group, dims of quarter g --------------
-  uint4 qr[QP];
-  {
-    const bool ok = t < a.n_rep;
-    const raw_t* qp = static_cast<const raw_t*>(a.q) + b * a.q_stride_tok +
-                      (h * a.n_rep + (ok ? t : 0)) * a.q_stride_head + g * Tr::kLaneElems;
+    const uint32_t kdst = wave_tiles_lds + ST * Tr::kStageBytes;
 #pragma unroll
-    for (int c = 0; c < QP; ++c)
-      qr[c] = ok ? reinterpret_cast<const uint4*>(qp)[c] : make_uint4(0, 0, 0, 0);
-  }
+    for (int c = 0; c < L; ++c) {
+      copy_to_lds_16B(a.k_cache + off[c], __builtin_amdgcn_readfirstlane(kdst + c * 1024));
+      copy_to_lds_16B(a.v_cache + off[c],
+                      __builtin_amdgcn_readfirstlane(kdst + Tr::kTileBytes + c * 1024));
+    }
+    return valid;
+  };
 
   float m_run = kNegInf;  // running max of head t (log2 domain)
   float l_run = 0.f;      // running sum of head t
@@ -324,9 +384,9 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Attention over this wave's tile of chunk `ch` in buffer `buf`.
-  auto compute_tile = [&](int ch, int buf) {
-    const char* k_tile = wave_lds + buf * 2 * Tr::kTileBytes;
+  // Attention over this wave's tile of chunk `k` in stage `st`.
+  auto compute_tile = [&](int k, int st) __attribute__((always_inline)) {
+    const char* k_tile = wave_tiles + st * Tr::kStageBytes;
     const char* v_tile = k_tile + Tr::kTileBytes;
     // S^T = K Q^T: lane (g, t) reads row t, pieces g*QP .. g*QP+QP-1
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -336,7 +396,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       const uint4 kp = *reinterpret_cast<const uint4*>(k_tile + (t * RP + ((g * QP + c) ^ ksw)) * 16);
       acc = mfma_qk<DTYPE>(kp, qr[c], acc);
     }
-    const int tile_tok = tok_begin + ch * Tr::kChunk + wave * kTile;
+    const int tile_tok = tok_begin + k * Tr::kChunk + wave * kTile;
     float s[4];
     float mc = kNegInf;
 #pragma unroll
@@ -374,51 +434,60 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   };
 
   // Zeroes the V slots of tokens that were not loaded (P is 0 there, but
-  // the stale LDS bytes could hold NaN/Inf and 0 * NaN = NaN).
-  auto zero_invalid_v = [&](int buf, const bool (&valid)[L]) {
-    char* vdst = wave_lds + buf * 2 * Tr::kTileBytes + Tr::kTileBytes;
+  // the pool row read in their place could hold NaN/Inf and 0 * NaN = NaN).
+  auto zero_invalid_v = [&](int st, unsigned valid) __attribute__((always_inline)) {
+    char* vdst = s_lds + wave * Tr::kWaveLds + st * Tr::kStageBytes + Tr::kTileBytes;
 #pragma unroll
     for (int c = 0; c < L; ++c)
-      if (!valid[c]) *reinterpret_cast<uint4*>(vdst + c * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
+      if (!((valid >> c) & 1u))
+        *reinterpret_cast<uint4*>(vdst + c * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
   };
 
   // ---- tile loop ---------------------------------------------------------
-  // Step ch: (1) load the block ids of chunk ch+2, (2) issue chunk ch+1's
-  // tile into the other buffer, (3) wait for chunk ch's tile, (4) compute.
-  // The block ids of ch+1 were loaded before chunk ch's tile was issued, so
-  // using them never waits on that tile (vmcnt retires loads in order), and
-  // two tiles are in flight while a third is computed.
-  auto step = [&](int ch, int buf, const bool (&val_cur)[L], const int64_t (&blk_next)[L],
-                  bool (&val_next)[L], int64_t (&blk_pref)[L]) {
-    const bool has1 = ch + 1 < n_chunks;
-    const bool has2 = ch + 2 < n_chunks;
-    if (has2) load_block_ids(ch + 2, blk_pref);
-    if (has1) issue_tile(ch + 1, buf ^ 1, blk_next, val_next);
+  // S = kStages buffers per wave. Chunk k's tile goes to stage k % S; at
+  // step k the tile of chunk k+S-1 is issued into the stage chunk k-1 has
+  // just released, then the wave waits until only the tiles of chunks
+  // k+1 .. k+S-1 are in flight (vmcnt retires in order and the loop issues
+  // no other vector memory instructions) and computes chunk k.
+  constexpr int S = Tr::kStages;
+  unsigned valid[S];
+  auto step = [&](int k, auto st_c) __attribute__((always_inline)) {
+    constexpr int ST = decltype(st_c)::value;
+    constexpr int NX = (ST + S - 1) % S;
+    if (k + S - 1 < n_chunks) valid[NX] = issue_tile(k + S - 1, IntC<NX>{});
     asm volatile("" ::: "memory");
-    if (has2) wait_vmcnt<3 * L>();
-    else if (has1) wait_vmcnt<2 * L>();
-    else wait_vmcnt<0>();
+    wait_vmcnt_groups<2 * L, S - 1>(n_chunks - 1 - k);
     asm volatile("" ::: "memory");
-    zero_invalid_v(buf, val_cur);
-    wave_lds_order();
-    compute_tile(ch, buf);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile's LDS reads are done
-    wave_lds_order();
+    zero_invalid_v(ST, valid[ST]);
+    compute_tile(k, ST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage's LDS accesses are done
+    asm volatile("" ::: "memory");
   };
-  {
-    int64_t blk_a[L], blk_b[L];
-    bool val_a[L], val_b[L];
-    load_block_ids(0, blk_a);
-    if (n_chunks > 1) load_block_ids(1, blk_b);
-    issue_tile(0, 0, blk_a, val_a);
-    for (int ch = 0; ch < n_chunks; ch += 2) {
-      step(ch, 0, val_a, blk_b, val_b, blk_a);
-      if (ch + 1 >= n_chunks) break;
-      step(ch + 1, 1, val_b, blk_a, val_a, blk_b);
+  valid[0] = issue_tile(0, IntC<0>{});
+  if constexpr (S > 2) {
+    if (1 < n_chunks) valid[1] = issue_tile(1, IntC<1>{});
+  }
+  if constexpr (S > 3) {
+    if (2 < n_chunks) valid[2] = issue_tile(2, IntC<2>{});
+  }
+  for (int k = 0; k < n_chunks; k += S) {
+    step(k, IntC<0>{});
+    if (k + 1 >= n_chunks) break;
+    step(k + 1, IntC<1>{});
+    if constexpr (S > 2) {
+      if (k + 2 >= n_chunks) break;
+      step(k + 2, IntC<2>{});
+    }
+    if constexpr (S > 3) {
+      if (k + 3 >= n_chunks) break;
+      step(k + 3, IntC<3>{});
     }
   }
 
   // ---- merge the waves ------------------------------------------------------
+  // From here on thread (r, q) = (tid / 16, tid % 16) owns dims
+  // [q * kDimsPerThread, (q + 1) * kDimsPerThread) of query head r of the group.
+  constexpr int DPT = Tr::kDimsPerThread;
   __syncthreads();  // every wave is done with its tiles (s_lds is reused)
   float* s_o = reinterpret_cast<float*>(s_lds);  // [kWaves][kMaxGroup][D]
   if (g == 0) {
@@ -435,34 +504,45 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   }
   __syncthreads();
 
-  const int n_out = a.n_rep * D;
+  const int q = threadIdx.x & 15;
   const int64_t slot_base = (static_cast<int64_t>(b) * a.num_q_heads + h * a.n_rep) * a.max_parts;
-  for (int idx = threadIdx.x; idx < n_out; idx += kWaves * 64) {
-    const int r = idx / D;
-    const int d = idx - r * D;
+  for (int r = threadIdx.x >> 4; r < a.n_rep; r += kWaves * 4) {
     float mx = kNegInf;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_max[w][r]);
-    float sum = 0.f, acc = 0.f;
+    float sum = 0.f;
+    float v[DPT];
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) v[i] = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       const float mw = s_max[w][r];
-      if (mw != kNegInf) {
+      if (mw != kNegInf) {  // a wave with no token of the partition holds nothing
         const float f = __builtin_amdgcn_exp2f(mw - mx);
         sum += s_sum[w][r] * f;
-        acc += s_o[(w * kMaxGroup + r) * D + d] * f;
+        const float4* src = reinterpret_cast<const float4*>(s_o + (w * kMaxGroup + r) * D + q * DPT);
+#pragma unroll
+        for (int i = 0; i < DPT / 4; ++i) {
+          const float4 x = src[i];
+          v[4 * i] += x.x * f;
+          v[4 * i + 1] += x.y * f;
+          v[4 * i + 2] += x.z * f;
+          v[4 * i + 3] += x.w * f;
+        }
       }
     }
+    const float inv = 1.f / sum;  // >= 1: the partition's largest logit contributes exp2(0)
     if (n_parts == 1) {
-      raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head;
-      op[d] = from_f32<DTYPE>(acc / sum);
+      raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok +
+                  (h * a.n_rep + r) * a.out_stride_head + q * DPT;
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) op[i] = from_f32<DTYPE>(v[i] * inv);
     } else {
       const int64_t slot = slot_base + static_cast<int64_t>(r) * a.max_parts + part;
-      store_coherent(a.ws_o + slot * D + d, acc / sum);
-      if (d == 0) {
-        store_coherent(a.ws_ml + 2 * slot, mx);
-        store_coherent(a.ws_ml + 2 * slot + 1, sum);
-      }
+      uint64_t* dst = reinterpret_cast<uint64_t*>(a.ws_o + slot * D + q * DPT);
+#pragma unroll
+      for (int i = 0; i < DPT / 2; ++i) store_coherent_u64(dst + i, pack_f32x2(v[2 * i] * inv, v[2 * i + 1] * inv));
+      if (q == 0) store_coherent_u64(reinterpret_cast<uint64_t*>(a.ws_ml) + slot, pack_f32x2(mx, sum));
     }
   }
   if (n_parts == 1) return;
@@ -481,89 +561,56 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   }
   __syncthreads();
   if (!s_last) return;
-  // One round of loads per kMergeParts partitions: every thread issues the
-  // partial values of its outputs together with its share of the
-  // (max, sum) pairs, which go through LDS to form the per-head weights.
-  float* s_m = reinterpret_cast<float*>(s_lds);  // [kMaxGroup][kMergeParts]
-  float* s_w = s_m + kMaxGroup * kMergeParts;    // [kMaxGroup][kMergeParts]
-  float* s_f = s_w + kMaxGroup * kMergeParts;    // [kMaxGroup] running max
-  float* s_g = s_f + kMaxGroup;                  // [kMaxGroup] rescale of the running sums
-  float* s_n = s_g + kMaxGroup;                  // [kMaxGroup] running weight sum
-  constexpr int kOuts = (kMaxGroup * D + kWaves * 64 - 1) / (kWaves * 64);
-  float acc[kOuts];
+  // Log-sum-exp over the partitions, kMergeRound at a time: every thread
+  // issues the (max, sum) pairs of its head and its dims of the partials
+  // of a round together (one memory round trip per round), then folds
+  // them into a running (max, sum, o) with one rescale per round.
+  constexpr int R = Tr::kMergeRound;
+  for (int r = threadIdx.x >> 4; r < a.n_rep; r += kWaves * 4) {
+    const int64_t slot0 = slot_base + static_cast<int64_t>(r) * a.max_parts;
+    float m_all = kNegInf, l_all = 0.f;
+    float acc[DPT];
 #pragma unroll
-  for (int k = 0; k < kOuts; ++k) acc[k] = 0.f;
-  if (threadIdx.x < kMaxGroup) {
-    s_f[threadIdx.x] = kNegInf;
-    s_n[threadIdx.x] = 0.f;
-  }
-  for (int p0 = 0; p0 < n_parts; p0 += kMergeParts) {
-    const int np = min(kMergeParts, n_parts - p0);
-    // (1) loads: partial values of this thread's outputs + (max, sum) pairs
-    float ov[kOuts][kMergeParts];
+    for (int i = 0; i < DPT; ++i) acc[i] = 0.f;
+    for (int p0 = 0; p0 < n_parts; p0 += R) {
+      const int np = min(R, n_parts - p0);
+      // Straight-line loads (entries past the last partition re-read it and
+      // get weight 0), so the whole round is in flight before the first use.
+      uint64_t ml[R];
+      uint64_t ov[R][DPT / 2];
 #pragma unroll
-    for (int k = 0; k < kOuts; ++k) {
-      const int idx = threadIdx.x + k * kWaves * 64;
-      const int r = idx / D;
-      const int d = idx - r * D;
-      const int64_t s0 = slot_base + static_cast<int64_t>(r) * a.max_parts + p0;
+      for (int pp = 0; pp < R; ++pp) {
+        const int64_t slot = slot0 + p0 + min(pp, np - 1);
+        ml[pp] = load_coherent_u64(reinterpret_cast<const uint64_t*>(a.ws_ml) + slot);
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.ws_o + slot * D + q * DPT);
 #pragma unroll
-      for (int pp = 0; pp < kMergeParts; ++pp)
-        ov[k][pp] = (idx < n_out && pp < np) ? load_coherent(a.ws_o + (s0 + pp) * D + d) : 0.f;
-    }
-    float mv = kNegInf, lv = 0.f;
-    const int mi = threadIdx.x;  // (head, partition) pair of this thread
-    const int mr = mi / kMergeParts, mp = mi - mr * kMergeParts;
-    if (mi < kMaxGroup * kMergeParts && mr < a.n_rep && mp < np) {
-      const int64_t sl = slot_base + static_cast<int64_t>(mr) * a.max_parts + p0 + mp;
-      mv = load_coherent(a.ws_ml + 2 * sl);
-      lv = load_coherent(a.ws_ml + 2 * sl + 1);
-    }
-    __syncthreads();  // previous round's LDS readers are done
-    if (mi < kMaxGroup * kMergeParts) {
-      s_m[mi] = mv;
-      s_w[mi] = lv;
-    }
-    __syncthreads();
-    // (2) per-head weights of this round, relative to the running max
-    if (threadIdx.x < a.n_rep) {
-      const int r = threadIdx.x;
-      float mx = s_f[r];
-      for (int pp = 0; pp < np; ++pp) mx = fmaxf(mx, s_m[r * kMergeParts + pp]);
-      const float g = s_f[r] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(s_f[r] - mx);
-      float sum = s_n[r] * g;
-      for (int pp = 0; pp < np; ++pp) {
-        const float w = s_w[r * kMergeParts + pp] * __builtin_amdgcn_exp2f(s_m[r * kMergeParts + pp] - mx);
-        s_w[r * kMergeParts + pp] = w;
-        sum += w;
+        for (int i = 0; i < DPT / 2; ++i) ov[pp][i] = load_coherent_u64(src + i);
       }
-      s_f[r] = mx;
-      s_g[r] = g;
-      s_n[r] = sum;
-    }
-    __syncthreads();
-    // (3) accumulate
+      float m_round = m_all;
 #pragma unroll
-    for (int k = 0; k < kOuts; ++k) {
-      const int idx = threadIdx.x + k * kWaves * 64;
-      if (idx < n_out) {
-        const int r = idx / D;
-        float sacc = acc[k] * s_g[r];
+      for (int pp = 0; pp < R; ++pp) m_round = fmaxf(m_round, unpack_lo(ml[pp]));
+      const float rescale = __builtin_amdgcn_exp2f(m_all - m_round);  // 0 on the first round
+      l_all *= rescale;
 #pragma unroll
-        for (int pp = 0; pp < kMergeParts; ++pp) sacc += s_w[r * kMergeParts + pp] * ov[k][pp];
-        acc[k] = sacc;
+      for (int i = 0; i < DPT; ++i) acc[i] *= rescale;
+#pragma unroll
+      for (int pp = 0; pp < R; ++pp) {
+        const float w =
+            pp < np ? unpack_hi(ml[pp]) * __builtin_amdgcn_exp2f(unpack_lo(ml[pp]) - m_round) : 0.f;
+        l_all += w;
+#pragma unroll
+        for (int i = 0; i < DPT / 2; ++i) {
+          acc[2 * i] += w * unpack_lo(ov[pp][i]);
+          acc[2 * i + 1] += w * unpack_hi(ov[pp][i]);
+        }
       }
+      m_all = m_round;
     }
-  }
+    const float inv = 1.f / l_all;
+    raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head +
+                q * DPT;
 #pragma unroll
-  for (int k = 0; k < kOuts; ++k) {
-    const int idx = threadIdx.x + k * kWaves * 64;
-    if (idx < n_out) {
-      const int r = idx / D;
-      const int d = idx - r * D;
-      raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head;
-      op[d] = from_f32<DTYPE>(acc[k] / s_n[r]);
-    }
+    for (int i = 0; i < DPT; ++i) op[i] = from_f32<DTYPE>(acc[i] * inv);
   }
   if (threadIdx.x == 0)  // ready for the next call
     __hip_atomic_store(&a.counters[b * a.num_kv_heads + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -646,9 +693,13 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const int64_t groups = static_cast<int64_t>(total_chunks) * a.num_kv_heads;
   // enough work groups for the device, at most kMaxParts partitions per sequence
   const int64_t target = std::max(1, a.target_groups);
-  const int per_part = static_cast<int>(std::max<int64_t>(
-      std::max<int64_t>(1, (groups + target - 1) / target),
-      (most_chunks + kMaxParts - 1) / kMaxParts));
+  // A partition spans at most kIdCap table entries (they are staged in LDS):
+  // P <= (kIdCap - 1) * block_size covers a partition that starts mid-block.
+  const int64_t id_cap_chunks = std::max<int64_t>(
+      1, ((static_cast<int64_t>(kIdCap - 1)) << a.bs_log2) / a.chunk_tokens);
+  const int per_part = static_cast<int>(std::min<int64_t>(
+      id_cap_chunks, std::max<int64_t>(std::max<int64_t>(1, (groups + target - 1) / target),
+                                       (most_chunks + kMaxParts - 1) / kMaxParts)));
   const int part_tokens = per_part * a.chunk_tokens;
 
   // pass 2: work list
@@ -850,6 +901,10 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
     return fail(MV_ERR_INVALID_ARGUMENT,
                 "mv_paged_decode: partition_tokens %d is not a positive multiple of %d",
                 partition_tokens, chunk);
+  if ((static_cast<int64_t>(partition_tokens) + block_size - 1) / block_size + 1 > kIdCap)
+    return fail(MV_ERR_INVALID_ARGUMENT,
+                "mv_paged_decode: partition_tokens %d spans more than %d blocks of %d tokens",
+                partition_tokens, kIdCap - 1, block_size);
   if (num_seqs == 0 || num_work_items == 0) return MV_OK;
   if (!query || !key_cache || !value_cache || !block_table || !kv_len_i32 || !work_items || !out)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: null pointer");

@@ -63,7 +63,7 @@ def test_abi_queries(lib):
     assert lib.mv_decode_chunk_tokens(64, 2) == 64       # 4 waves x one 16-token tile
     assert lib.mv_decode_chunk_tokens(128, 0) == 64
     assert lib.mv_decode_chunk_tokens(96, 2) == 0
-    assert lib.mv_decode_groups_per_cu(64, 2) == 5       # 32 KiB of LDS per group
+    assert lib.mv_decode_groups_per_cu(64, 2) == 3       # 3 stages x 4 waves x 4 KiB + 2 KiB ids
     assert lib.mv_decode_groups_per_cu(128, 2) == 2
     assert lib.mv_decode_groups_per_cu(96, 2) == 0
 
@@ -107,6 +107,12 @@ def test_decode_rejects_unsupported_shapes_on_host(lib):
     assert lib.mv_paged_decode(*_decode_args(num_q_heads=34)) == _hip.MV_ERR_UNSUPPORTED
     assert lib.mv_paged_decode(*_decode_args(dtype=7)) == _hip.MV_ERR_UNSUPPORTED
     assert lib.mv_paged_decode(*_decode_args(partition_tokens=100)) == _hip.MV_ERR_INVALID_ARGUMENT
+    # a partition's block ids are staged in LDS: at most 511 blocks per partition
+    assert lib.mv_paged_decode(*_decode_args(block_size=1, partition_tokens=512)) == \
+        _hip.MV_ERR_INVALID_ARGUMENT
+    assert b"spans more than 511 blocks" in lib.mv_last_error()
+    assert lib.mv_paged_decode(*_decode_args(block_size=1, partition_tokens=448,
+                                             num_work_items=0)) == _hip.MV_OK
     # nothing to do is not an error
     assert lib.mv_paged_decode(*_decode_args(num_work_items=0)) == _hip.MV_OK
     # work to do but null pointers
