@@ -62,6 +62,7 @@ extern "C" {
 #define MV_PLAN_MAX_PARTS 4     /* max partitions of any sequence */
 #define MV_PLAN_MIN_KV_LEN 5    /* min kv_len (clamped to int32) */
 #define MV_PLAN_PARTITION_TOKENS 6 /* tokens per partition chosen for this step */
+#define MV_PLAN_IDS_PER_ITEM 7  /* block ids stored per work item (-1: capacity exceeded) */
 #define MV_PLAN_WORDS 8
 
 /* Version of this ABI (MVATTN_ABI_VERSION of the built library). */
@@ -121,22 +122,35 @@ int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t t
  *   kv_len      [num_seqs] int64 (kv_len_is_i64=1) or int32
  *   block_table [num_seqs, max_blocks] (row stride bt_stride), int64
  *               (bt_is_i64=1) or int32, -1 padded
- * Chooses the partition size: the smallest multiple of chunk_tokens
+ * Chooses the partition size P: the smallest multiple of chunk_tokens
  * (mv_decode_chunk_tokens) that keeps the number of (sequence, kv head,
- * partition) work groups within target_groups (at most 128 partitions per
- * sequence). Outputs: kv_len_i32[num_seqs] (0 for rejected sequences),
- * work_items (int32 quadruples (seq, partition, kv_len, 0), 16-byte
- * aligned, capacity work_capacity quadruples; num_seqs * ceil(max_blocks *
- * block_size / chunk_tokens) always suffices), counters[num_seqs *
- * num_kv_heads] set to zero, and status[MV_PLAN_WORDS]. One work group;
- * enqueue only.
+ * partition) work groups within target_groups (aiming at no more than 128
+ * partitions per sequence), capped so that a partition spans at most 511
+ * table entries. Outputs:
+ *   work_items  int32 quadruples (seq, partition, kv_len, 0), 16-byte
+ *               aligned, capacity work_capacity quadruples
+ *               (num_seqs * ceil(max_blocks * block_size / chunk_tokens)
+ *               always suffices);
+ *   block_ids   for work item i, int32 [i * n, (i + 1) * n) with
+ *               n = status[MV_PLAN_IDS_PER_ITEM]: the pool blocks of table
+ *               entries P*p/bs .. of its sequence, -1 past its last block;
+ *               16-byte aligned, block_ids_capacity >=
+ *               mv_decode_block_ids_capacity(num_seqs, max_blocks,
+ *               work_capacity) ints;
+ *   counters    [num_seqs * num_kv_heads] set to zero;
+ *   status      [MV_PLAN_WORDS].
+ * One work group; enqueue only.
  */
 int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                    int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs, int32_t max_blocks,
                    int32_t block_size, int64_t num_blocks, int32_t chunk_tokens,
-                   int32_t num_kv_heads, int32_t target_groups, int32_t* kv_len_i32,
-                   int32_t* work_items, int64_t work_capacity, int32_t* counters,
-                   int32_t* status, void* stream);
+                   int32_t num_kv_heads, int32_t target_groups, int32_t* work_items,
+                   int64_t work_capacity, int32_t* block_ids, int64_t block_ids_capacity,
+                   int32_t* counters, int32_t* status, void* stream);
+
+/* Ints of block_ids storage mv_decode_plan needs (an upper bound for any
+ * kv_len and partition size). */
+int64_t mv_decode_block_ids_capacity(int32_t num_seqs, int32_t max_blocks, int64_t work_capacity);
 
 /* Bytes of fp32 workspace mv_paged_decode needs for `max_partitions`
  * partitions per sequence (0 when max_partitions <= 1). */
@@ -153,23 +167,24 @@ size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, in
  *   hk = hq / (num_q_heads / num_kv_heads), over kv_len[b] tokens whose
  *   token j lives at block block_table[b, j / block_size], offset
  *   j % block_size.
- * kv_len_i32, work_items, counters and the partition size come from
- * mv_decode_plan on the same metadata (num_work_items =
+ * The sequences, lengths and blocks come from mv_decode_plan on the same
+ * metadata: work_items, block_ids, counters, num_work_items =
  * status[MV_PLAN_NUM_ITEMS], partition_tokens =
  * status[MV_PLAN_PARTITION_TOKENS], max_partitions =
- * status[MV_PLAN_MAX_PARTS]). Sequences split into several partitions are
- * merged inside the same launch (log-sum-exp over fp32 partials in
- * `workspace`, mv_paged_decode_workspace_bytes); calls sharing one plan's
- * counters or one workspace must be ordered on one stream. Output rows of
- * sequences the plan rejected are left untouched. Supported: head_dim 64
- * or 128, block_size a power of two, num_q_heads / num_kv_heads in
- * [1, 16], dtype F32 / F16 / BF16 (query, caches and output share it).
+ * status[MV_PLAN_MAX_PARTS]; the block table itself is not read.
+ * Sequences split into several partitions are merged inside the same
+ * launch (log-sum-exp over fp32 partials in `workspace`,
+ * mv_paged_decode_workspace_bytes); calls sharing one plan's counters or
+ * one workspace must be ordered on one stream. Output rows of sequences the
+ * plan rejected are left untouched. Supported: head_dim 64 or 128,
+ * block_size a power of two, num_q_heads / num_kv_heads in [1, 16], dtype
+ * F32 / F16 / BF16 (query, caches and output share it); query rows and
+ * strides, caches, work_items and block_ids 16-byte aligned.
  */
 int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
-                    const void* key_cache, const void* value_cache, const void* block_table,
-                    int32_t bt_is_i64, int64_t bt_stride, const int32_t* kv_len_i32,
-                    const int32_t* work_items, int32_t num_work_items, int32_t partition_tokens,
-                    int32_t max_partitions, int32_t* counters, void* out,
+                    const void* key_cache, const void* value_cache, const int32_t* work_items,
+                    const int32_t* block_ids, int64_t block_ids_capacity, int32_t num_work_items,
+                    int32_t partition_tokens, int32_t max_partitions, int32_t* counters, void* out,
                     int64_t out_stride_tok, int64_t out_stride_head, float scale,
                     int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t dtype,

@@ -86,11 +86,13 @@ struct Traits {
   static constexpr int kWaveLds = kStages * kStageBytes;
   // LDS is one union, laid out per phase:
   //   tile loop: [kWaves][kStages][K, V][kTileBytes], then the partition's
-  //              block ids (int32, kIdCap);
+  //              block ids (int32, kIdCap), then the group's 16 Q rows;
   //   merges:    [0, kWaveOBytes) the waves' o, then their (max, sum)
   //              and the last-group flag.
   static constexpr int kIdsOffset = kWaves * kWaveLds;
-  static constexpr int kTilesEnd = kIdsOffset + kIdCap * 4;
+  static constexpr int kQOffset = kIdsOffset + kIdCap * 4;  // Q rows of the group (16 x D)
+  static constexpr int kQLoads = kTile * kRowBytes / 1024;  // 1 KiB copies of the Q rows
+  static constexpr int kTilesEnd = kQOffset + kTile * kRowBytes;
   static constexpr int kWaveOBytes = kWaves * kMaxGroup * D * 4;     // wave merge o
   static constexpr int kStatsOffset = kWaveOBytes;                    // s_max, s_sum
   static constexpr int kFlagOffset = kStatsOffset + 2 * kWaves * kMaxGroup * 4;
@@ -101,12 +103,12 @@ struct Traits {
   // register budget: waves per SIMD = groups * kWaves / 4 (at least 1).
   static constexpr int kGroupsPerCU = (160 * 1024) / kLdsBytes;
   static constexpr int kWavesPerSimd = kGroupsPerCU * kWaves / 4 > 0 ? kGroupsPerCU * kWaves / 4 : 1;
-  // Epilogue: 16 threads per query head, D/16 dims each; the partition
-  // merge folds kMergeRound partitions per round of loads.
-  static constexpr int kDimsPerThread = D / 16;
+  // Epilogue: 16 threads per query head, D/32 dim pairs each; the
+  // partition merge folds up to kMergeRound partitions per round of loads.
+  static constexpr int kPairsPerThread = D / 32;
   static constexpr int kMergeRound = 1024 / D;
   static_assert(kLoads >= 1 && kRowPieces >= 8, "tile geometry");
-  static_assert(kDimsPerThread % 4 == 0, "epilogue vectors");
+  static_assert(kWaves * 64 >= 256 || kWaves * 64 % 16 == 0, "epilogue mapping");
 };
 
 // Swizzle of the 16-byte pieces of LDS row r: slot s holds piece s ^ sw(r).
@@ -118,23 +120,25 @@ __device__ __forceinline__ int piece_swizzle(int r) {
   return ROW_PIECES == 8 ? (r >> 1) & 7 : r & 15;
 }
 
+// Kernel arguments; the fields the prologue needs come first, so a couple
+// of wide scalar loads fetch them together.
 struct DecodeArgs {
+  const int32_t* work;       // (seq, partition, kv_len, 0) quadruples
+  const int32_t* block_ids;  // [work item][ids_per_item]: the partition's pool blocks, -1 padded
   const void* q;
-  int64_t q_stride_tok, q_stride_head;  // elements
   const char* k_cache;
   const char* v_cache;
-  const void* block_table;
-  int64_t bt_stride;  // elements
-  const int32_t* kv_len;
-  const int32_t* work;  // (seq, partition, kv_len, 0) quadruples
-  int32_t* counters;    // [num_seqs * num_kv_heads], zero at rest
+  int64_t q_stride_tok, q_stride_head;  // elements
+  int32_t ids_per_item;                 // multiple of 4, <= kIdCap
+  int32_t num_kv_heads, n_rep, bs_log2, part_tokens;
+  float scale_log2;                     // scale * log2(e)
+  int32_t num_q_heads, max_parts;
+  int64_t num_blocks;
+  int32_t* counters;  // [num_seqs * num_kv_heads], zero at rest
   void* out;
   int64_t out_stride_tok, out_stride_head;  // elements
   float* ws_o;                              // [num_seqs, Hq, max_parts, D]
   float* ws_ml;                             // [num_seqs, Hq, max_parts, 2]: (max, sum)
-  float scale_log2;                         // scale * log2(e)
-  int32_t num_q_heads, num_kv_heads, n_rep, bs_log2, max_parts, part_tokens;
-  int64_t num_blocks;
 };
 
 // --------------------------------------------------------------- MFMA ----
@@ -275,7 +279,7 @@ struct IntC {
   static constexpr int value = C;
 };
 
-template <int DTYPE, int D, typename BT>
+template <int DTYPE, int D>
 __global__ __launch_bounds__(kWaves * 64)
 __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged_decode_kernel(DecodeArgs a) {
   using Tr = Traits<DTYPE, D>;
@@ -294,9 +298,32 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const int t = lane & 15;  // MFMA: token row (K operand) / head column (results)
   const int g = lane >> 4;  // MFMA: dim quarter (K operand) / token quad (results)
 
+  // The kernel arguments the prologue needs, in SGPRs at once: otherwise
+  // the compiler loads them field by field with a wait in between, which
+  // costs several scalar memory round trips before the first copy.
+  asm volatile("" ::"s"(a.work), "s"(a.block_ids), "s"(a.ids_per_item), "s"(a.num_kv_heads),
+               "s"(a.q), "s"(a.q_stride_tok), "s"(a.q_stride_head), "s"(a.n_rep), "s"(a.k_cache),
+               "s"(a.v_cache), "s"(a.bs_log2), "s"(a.part_tokens));
   const int item = blockIdx.x / a.num_kv_heads;
   const int h = blockIdx.x - item * a.num_kv_heads;
+  const uint32_t lds0 = lds_address(s_lds);
+  int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
+
+  // ---- the work item and its block ids: both addressed by blockIdx alone,
+  // so they travel together (one memory round trip). Waves 0 and 1 copy
+  // 256 ids each; lanes past the list re-read its last 16 bytes. The copy
+  // is issued first: the work item's scalar load must not sit in front of
+  // it (a wait for it would also cover the kernel arguments the copy needs).
+  if (wave * 256 < a.ids_per_item) {
+    const int32_t* src = a.block_ids + static_cast<int64_t>(item) * a.ids_per_item +
+                         min(wave * 256 + 4 * lane, a.ids_per_item - 4);
+    copy_to_lds_16B(reinterpret_cast<const char*>(src),
+                    __builtin_amdgcn_readfirstlane(lds0 + Tr::kIdsOffset + wave * 1024));
+  }
+  asm volatile("" ::: "memory");
   const int4 wi = reinterpret_cast<const int4*>(a.work)[item];  // (seq, partition, kv_len, -)
+  wait_vmcnt<0>();
+  asm volatile("" ::: "memory");
   const int b = wi.x;
   const int part = wi.y;
   const int kv = wi.z;
@@ -305,29 +332,24 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const int tok_end = min(kv, tok_begin + a.part_tokens);
   const int n_chunks = (tok_end - tok_begin + Tr::kChunk - 1) / Tr::kChunk;
   const int bs_mask = (1 << a.bs_log2) - 1;
-  const BT* bt_row = static_cast<const BT*>(a.block_table) + b * a.bt_stride;
-  const int first_blk = tok_begin >> a.bs_log2;
-  const int n_ids = min(((tok_end - 1) >> a.bs_log2) - first_blk + 1, kIdCap);
-  int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
+  const int first_blk = tok_begin >> a.bs_log2;  // s_ids[i] = pool block of table entry first_blk + i
   const char* wave_tiles = s_lds + wave * Tr::kWaveLds;  // [stage][K, V][tile bytes]
-  const uint32_t wave_tiles_lds = lds_address(s_lds) + wave * Tr::kWaveLds;
+  const uint32_t wave_tiles_lds = lds0 + wave * Tr::kWaveLds;
 
-  // ---- Q^T operand: head t of the group, dims of quarter g --------------
-  // Columns t >= n_rep repeat head 0 of the group: MFMA columns (and the
-  // softmax state per column) are independent, and those columns are never
-  // written out.
-  uint4 qr[QP];
-  {
-    const raw_t* qp = static_cast<const raw_t*>(a.q) + b * a.q_stride_tok +
-                      (h * a.n_rep + (t < a.n_rep ? t : 0)) * a.q_stride_head + g * Tr::kLaneElems;
+  // ---- Q rows of the group -> LDS (wave 0). Rows r >= n_rep repeat row
+  // n_rep - 1: MFMA columns (and the softmax state per column) are
+  // independent, and those columns are never written out.
+  if (wave == 0) {
 #pragma unroll
-    for (int c = 0; c < QP; ++c) qr[c] = reinterpret_cast<const uint4*>(qp)[c];
-  }
-
-  // ---- the partition's block ids -> LDS (-1: not a pool block) ------------
-  for (int i = threadIdx.x; i < n_ids; i += kWaves * 64) {
-    const int64_t blk = static_cast<int64_t>(bt_row[first_blk + i]);
-    s_ids[i] = (blk >= 0 && blk < a.num_blocks) ? static_cast<int32_t>(blk) : -1;
+    for (int c = 0; c < Tr::kQLoads; ++c) {
+      const int byte = c * 1024 + 16 * lane;
+      const int row = byte / Tr::kRowBytes;
+      const int col = (byte % Tr::kRowBytes) / Tr::kElemBytes;
+      const raw_t* src = static_cast<const raw_t*>(a.q) + b * a.q_stride_tok +
+                         (h * a.n_rep + min(row, a.n_rep - 1)) * a.q_stride_head + col;
+      copy_to_lds_16B(reinterpret_cast<const char*>(src),
+                      __builtin_amdgcn_readfirstlane(lds0 + Tr::kQOffset + c * 1024));
+    }
   }
 
   // LDS slot (64c + lane) of this wave's tile: its row, and the global
@@ -339,11 +361,6 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     slot_row[c] = slot / RP;
     slot_piece[c] = (slot % RP) ^ piece_swizzle<RP>(slot_row[c]);
   }
-  // The Q registers pass through an empty asm here, so the compiler waits
-  // for their loads now rather than inside the tile loop, where its wait
-  // would also drain the tile copies in flight.
-#pragma unroll
-  for (int c = 0; c < QP; ++c) asm volatile("" : "+v"(qr[c].x), "+v"(qr[c].y), "+v"(qr[c].z), "+v"(qr[c].w));
   __syncthreads();  // block ids visible to every wave
 
   // Issues the HBM -> LDS copies of this wave's tile of chunk `k` into
@@ -360,7 +377,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     for (int c = 0; c < L; ++c) {
       const int j = tile_tok + slot_row[c];
       const int jj = min(j, tok_end - 1);
-      const int id = s_ids[min((jj >> a.bs_log2) - first_blk, kIdCap - 1)];
+      const int id = s_ids[min((jj >> a.bs_log2) - first_blk, kIdCap - 1)];  // -1: not a pool block
       const bool ok = j < tok_end && id >= 0;
       off[c] = ok ? (((static_cast<int64_t>(id) * a.num_kv_heads + h) << a.bs_log2) + (jj & bs_mask)) *
                             Tr::kRowBytes +
@@ -378,6 +395,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     return valid;
   };
 
+  uint4 qr[QP];  // Q^T operand: head t of the group, dims of quarter g (from LDS)
   float m_run = kNegInf;  // running max of head t (log2 domain)
   float l_run = 0.f;      // running sum of head t
   f32x4 o[D / 16];        // O[head 4g+e][dim 16c+t]
@@ -470,6 +488,15 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   if constexpr (S > 3) {
     if (2 < n_chunks) valid[2] = issue_tile(2, IntC<2>{});
   }
+  // Q landed once wave 0's copies older than these tiles are done.
+  asm volatile("" ::: "memory");
+  if (wave == 0) wait_vmcnt_groups<2 * L, S - 1>(min(S - 1, n_chunks));
+  __syncthreads();  // Q rows visible to every wave
+  {
+    const char* q_row = s_lds + Tr::kQOffset + t * Tr::kRowBytes;
+#pragma unroll
+    for (int c = 0; c < QP; ++c) qr[c] = *reinterpret_cast<const uint4*>(q_row + (g * QP + c) * 16);
+  }
   for (int k = 0; k < n_chunks; k += S) {
     step(k, IntC<0>{});
     if (k + 1 >= n_chunks) break;
@@ -485,9 +512,10 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   }
 
   // ---- merge the waves ------------------------------------------------------
-  // From here on thread (r, q) = (tid / 16, tid % 16) owns dims
-  // [q * kDimsPerThread, (q + 1) * kDimsPerThread) of query head r of the group.
-  constexpr int DPT = Tr::kDimsPerThread;
+  // From here on thread (r, q) = (tid / 16, tid % 16) owns the dim pairs
+  // (32j + 2q, 32j + 2q + 1), j < D/32, of query head r of the group: each
+  // load or store instruction then covers 128 contiguous bytes per head.
+  constexpr int NPAIR = Tr::kPairsPerThread;
   __syncthreads();  // every wave is done with its tiles (s_lds is reused)
   float* s_o = reinterpret_cast<float*>(s_lds);  // [kWaves][kMaxGroup][D]
   if (g == 0) {
@@ -506,42 +534,43 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
 
   const int q = threadIdx.x & 15;
   const int64_t slot_base = (static_cast<int64_t>(b) * a.num_q_heads + h * a.n_rep) * a.max_parts;
+  auto out_row = [&](int r) { return static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head; };
   for (int r = threadIdx.x >> 4; r < a.n_rep; r += kWaves * 4) {
     float mx = kNegInf;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_max[w][r]);
     float sum = 0.f;
-    float v[DPT];
+    float2 v[NPAIR];
 #pragma unroll
-    for (int i = 0; i < DPT; ++i) v[i] = 0.f;
+    for (int j = 0; j < NPAIR; ++j) v[j] = make_float2(0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       const float mw = s_max[w][r];
       if (mw != kNegInf) {  // a wave with no token of the partition holds nothing
         const float f = __builtin_amdgcn_exp2f(mw - mx);
         sum += s_sum[w][r] * f;
-        const float4* src = reinterpret_cast<const float4*>(s_o + (w * kMaxGroup + r) * D + q * DPT);
+        const float* src = s_o + (w * kMaxGroup + r) * D + 2 * q;
 #pragma unroll
-        for (int i = 0; i < DPT / 4; ++i) {
-          const float4 x = src[i];
-          v[4 * i] += x.x * f;
-          v[4 * i + 1] += x.y * f;
-          v[4 * i + 2] += x.z * f;
-          v[4 * i + 3] += x.w * f;
+        for (int j = 0; j < NPAIR; ++j) {
+          const float2 x = *reinterpret_cast<const float2*>(src + 32 * j);
+          v[j].x += x.x * f;
+          v[j].y += x.y * f;
         }
       }
     }
     const float inv = 1.f / sum;  // >= 1: the partition's largest logit contributes exp2(0)
     if (n_parts == 1) {
-      raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok +
-                  (h * a.n_rep + r) * a.out_stride_head + q * DPT;
+      raw_t* op = out_row(r) + 2 * q;
 #pragma unroll
-      for (int i = 0; i < DPT; ++i) op[i] = from_f32<DTYPE>(v[i] * inv);
+      for (int j = 0; j < NPAIR; ++j) {
+        op[32 * j] = from_f32<DTYPE>(v[j].x * inv);
+        op[32 * j + 1] = from_f32<DTYPE>(v[j].y * inv);
+      }
     } else {
       const int64_t slot = slot_base + static_cast<int64_t>(r) * a.max_parts + part;
-      uint64_t* dst = reinterpret_cast<uint64_t*>(a.ws_o + slot * D + q * DPT);
+      uint64_t* dst = reinterpret_cast<uint64_t*>(a.ws_o + slot * D + 2 * q);
 #pragma unroll
-      for (int i = 0; i < DPT / 2; ++i) store_coherent_u64(dst + i, pack_f32x2(v[2 * i] * inv, v[2 * i + 1] * inv));
+      for (int j = 0; j < NPAIR; ++j) store_coherent_u64(dst + 16 * j, pack_f32x2(v[j].x * inv, v[j].y * inv));
       if (q == 0) store_coherent_u64(reinterpret_cast<uint64_t*>(a.ws_ml) + slot, pack_f32x2(mx, sum));
     }
   }
@@ -561,56 +590,69 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   }
   __syncthreads();
   if (!s_last) return;
-  // Log-sum-exp over the partitions, kMergeRound at a time: every thread
-  // issues the (max, sum) pairs of its head and its dims of the partials
-  // of a round together (one memory round trip per round), then folds
-  // them into a running (max, sum, o) with one rescale per round.
-  constexpr int R = Tr::kMergeRound;
+  // Log-sum-exp over the partitions in rounds: every thread issues the
+  // (max, sum) pairs of its head and its dims of the partials of a round
+  // together (one memory round trip per round; the round size is the
+  // smallest of 4, 8, kMergeRound that fits, so few loads are wasted), then
+  // folds them into a running (max, sum, o) with one rescale per round.
   for (int r = threadIdx.x >> 4; r < a.n_rep; r += kWaves * 4) {
     const int64_t slot0 = slot_base + static_cast<int64_t>(r) * a.max_parts;
     float m_all = kNegInf, l_all = 0.f;
-    float acc[DPT];
+    float2 acc[NPAIR];
 #pragma unroll
-    for (int i = 0; i < DPT; ++i) acc[i] = 0.f;
-    for (int p0 = 0; p0 < n_parts; p0 += R) {
-      const int np = min(R, n_parts - p0);
+    for (int j = 0; j < NPAIR; ++j) acc[j] = make_float2(0.f, 0.f);
+    // Folds partitions [p0, p0 + np), np <= RR.
+    auto fold = [&](auto rr_c, int p0, int np) __attribute__((always_inline)) {
+      constexpr int RR = decltype(rr_c)::value;
       // Straight-line loads (entries past the last partition re-read it and
       // get weight 0), so the whole round is in flight before the first use.
-      uint64_t ml[R];
-      uint64_t ov[R][DPT / 2];
+      uint64_t ml[RR];
+      uint64_t ov[RR][NPAIR];
 #pragma unroll
-      for (int pp = 0; pp < R; ++pp) {
+      for (int pp = 0; pp < RR; ++pp) {
         const int64_t slot = slot0 + p0 + min(pp, np - 1);
         ml[pp] = load_coherent_u64(reinterpret_cast<const uint64_t*>(a.ws_ml) + slot);
-        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.ws_o + slot * D + q * DPT);
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.ws_o + slot * D + 2 * q);
 #pragma unroll
-        for (int i = 0; i < DPT / 2; ++i) ov[pp][i] = load_coherent_u64(src + i);
+        for (int j = 0; j < NPAIR; ++j) ov[pp][j] = load_coherent_u64(src + 16 * j);
       }
       float m_round = m_all;
 #pragma unroll
-      for (int pp = 0; pp < R; ++pp) m_round = fmaxf(m_round, unpack_lo(ml[pp]));
+      for (int pp = 0; pp < RR; ++pp) m_round = fmaxf(m_round, unpack_lo(ml[pp]));
       const float rescale = __builtin_amdgcn_exp2f(m_all - m_round);  // 0 on the first round
       l_all *= rescale;
 #pragma unroll
-      for (int i = 0; i < DPT; ++i) acc[i] *= rescale;
+      for (int j = 0; j < NPAIR; ++j) {
+        acc[j].x *= rescale;
+        acc[j].y *= rescale;
+      }
 #pragma unroll
-      for (int pp = 0; pp < R; ++pp) {
+      for (int pp = 0; pp < RR; ++pp) {
         const float w =
             pp < np ? unpack_hi(ml[pp]) * __builtin_amdgcn_exp2f(unpack_lo(ml[pp]) - m_round) : 0.f;
         l_all += w;
 #pragma unroll
-        for (int i = 0; i < DPT / 2; ++i) {
-          acc[2 * i] += w * unpack_lo(ov[pp][i]);
-          acc[2 * i + 1] += w * unpack_hi(ov[pp][i]);
+        for (int j = 0; j < NPAIR; ++j) {
+          acc[j].x += w * unpack_lo(ov[pp][j]);
+          acc[j].y += w * unpack_hi(ov[pp][j]);
         }
       }
       m_all = m_round;
+    };
+    constexpr int RMAX = Tr::kMergeRound;
+    for (int p0 = 0; p0 < n_parts; p0 += RMAX) {
+      const int np = min(RMAX, n_parts - p0);
+      if (np <= 4) fold(IntC<4>{}, p0, np);
+      else if (RMAX <= 8 || np <= 8) fold(IntC<(RMAX < 8 ? RMAX : 8)>{}, p0, np);
+      else fold(IntC<RMAX>{}, p0, np);
     }
     const float inv = 1.f / l_all;
-    raw_t* op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head +
-                q * DPT;
+    raw_t* op = out_row(r) + 2 * q;
 #pragma unroll
-    for (int i = 0; i < DPT; ++i) op[i] = from_f32<DTYPE>(acc[i] * inv);
+    for (int j = 0; j < NPAIR; ++j) {
+      op[32 * j] = from_f32<DTYPE>(acc[j].x * inv);
+      op[32 * j + 1] = from_f32<DTYPE>(acc[j].y * inv);
+    }
   }
   if (threadIdx.x == 0)  // ready for the next call
     __hip_atomic_store(&a.counters[b * a.num_kv_heads + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -624,9 +666,10 @@ struct PlanArgs {
   int64_t bt_stride;
   int32_t num_seqs, max_blocks, bs_log2, chunk_tokens, num_kv_heads, target_groups;
   int64_t num_blocks;
-  int32_t* kv_out;
   int32_t* work;
   int64_t work_cap;
+  int32_t* ids;
+  int64_t ids_cap;
   int32_t* counters;
   int32_t* status;
 };
@@ -653,9 +696,17 @@ __device__ int block_max(int v, int* scratch) {
   return m;
 }
 
+// Block ids stored per work item for a partition of `part_tokens` tokens:
+// it spans at most ceil(P / bs) + 1 table entries; rounded up to a multiple
+// of 4 so every item's list is 16-byte aligned.
+__host__ __device__ inline int ids_per_item(int64_t part_tokens, int bs_log2) {
+  const int64_t n = ((part_tokens + (int64_t(1) << bs_log2) - 1) >> bs_log2) + 1;
+  return static_cast<int>((n + 3) / 4 * 4);
+}
+
 // One work group: validates kv_len and the table entries each sequence
 // reads, picks the partition size, builds the (sequence, partition) list
-// and zeroes the merge counters.
+// with each item's pool blocks and zeroes the merge counters.
 template <typename KV, typename BT>
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   __shared__ int s_scan[kPlanThreads];
@@ -686,7 +737,6 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
       chunks += c;
       max_chunks = max(max_chunks, c);
     }
-    a.kv_out[b] = valid_len(kv) ? static_cast<int32_t>(kv) : 0;
   }
   const int total_chunks = block_sum(chunks, s_red);
   const int most_chunks = block_max(max_chunks, s_red);
@@ -732,8 +782,32 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     running += s_scan[kPlanThreads - 1];
     __syncthreads();
   }
+  const int64_t num_items = std::min<int64_t>(running, a.work_cap);
+  __syncthreads();  // work items written above are read back below
 
-  // pass 3: every table entry a valid sequence reads must be a pool block
+  // pass 3: each item's pool blocks, -1 past its last block (and for an
+  // entry outside the pool, which pass 4 reports)
+  const int per_item = ids_per_item(part_tokens, a.bs_log2);
+  const int64_t n_ids = num_items * per_item;
+  if (n_ids <= a.ids_cap) {
+    for (int64_t i = tid; i < n_ids; i += kPlanThreads) {
+      const int64_t it = i / per_item;
+      const int k = static_cast<int>(i - it * per_item);
+      const int4 w = reinterpret_cast<const int4*>(a.work)[it];
+      const int64_t tok_begin = static_cast<int64_t>(w.y) * part_tokens;
+      const int64_t tok_end = std::min<int64_t>(w.z, tok_begin + part_tokens);
+      const int64_t first = tok_begin >> a.bs_log2;
+      const int64_t last = (tok_end - 1) >> a.bs_log2;
+      int32_t id = -1;
+      if (first + k <= last) {
+        const int64_t blk = static_cast<int64_t>(btp[w.x * a.bt_stride + first + k]);
+        if (blk >= 0 && blk < a.num_blocks) id = static_cast<int32_t>(blk);
+      }
+      a.ids[i] = id;
+    }
+  }
+
+  // pass 4: every table entry a valid sequence reads must be a pool block
   const int64_t n = static_cast<int64_t>(a.num_seqs) * a.max_blocks;
   int bad = 0;
   for (int64_t i = tid; i < n; i += kPlanThreads) {
@@ -758,7 +832,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     a.status[MV_PLAN_MAX_PARTS] = s_cnt[3];
     a.status[MV_PLAN_MIN_KV_LEN] = a.num_seqs > 0 ? s_min_kv : 0;
     a.status[MV_PLAN_PARTITION_TOKENS] = part_tokens;
-    a.status[7] = 0;
+    a.status[MV_PLAN_IDS_PER_ITEM] = n_ids <= a.ids_cap ? per_item : -1;  // -1: list not written
   }
 }
 
@@ -782,24 +856,17 @@ template <int DTYPE, int D> struct GroupsOf { static constexpr int value = Trait
 
 int chunk_tokens(int head_dim, int dtype) { return trait_value<ChunkOf>(head_dim, dtype); }
 
-template <int DTYPE, int D, typename BT>
+template <int DTYPE, int D>
 int launch_decode(const DecodeArgs& a, int num_items, hipStream_t s) {
   const int64_t grid = static_cast<int64_t>(num_items) * a.num_kv_heads;
   if (grid > INT_MAX) return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: grid too large");
-  paged_decode_kernel<DTYPE, D, BT><<<static_cast<unsigned>(grid), kWaves * 64, 0, s>>>(a);
+  paged_decode_kernel<DTYPE, D><<<static_cast<unsigned>(grid), kWaves * 64, 0, s>>>(a);
   return check_launch("mv_paged_decode");
 }
 
-template <int DTYPE, int D>
-int launch_decode_bt(const DecodeArgs& a, bool bt64, int num_items, hipStream_t s) {
-  return bt64 ? launch_decode<DTYPE, D, int64_t>(a, num_items, s)
-              : launch_decode<DTYPE, D, int32_t>(a, num_items, s);
-}
-
 template <int DTYPE>
-int launch_decode_d(const DecodeArgs& a, int d, bool bt64, int num_items, hipStream_t s) {
-  return d == 64 ? launch_decode_bt<DTYPE, 64>(a, bt64, num_items, s)
-                 : launch_decode_bt<DTYPE, 128>(a, bt64, num_items, s);
+int launch_decode_d(const DecodeArgs& a, int d, int num_items, hipStream_t s) {
+  return d == 64 ? launch_decode<DTYPE, 64>(a, num_items, s) : launch_decode<DTYPE, 128>(a, num_items, s);
 }
 
 }  // namespace
@@ -815,6 +882,15 @@ extern "C" int mv_decode_groups_per_cu(int32_t head_dim, int32_t dtype) {
   return mv::trait_value<mv::GroupsOf>(head_dim, dtype);
 }
 
+extern "C" int64_t mv_decode_block_ids_capacity(int32_t num_seqs, int32_t max_blocks,
+                                                int64_t work_capacity) {
+  if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0) return 0;
+  // With np_b = ceil(kv_b / P) items for sequence b and ids_per_item <=
+  // ceil(P / bs) + 4: np_b * ids_per_item <= (kv_b + P - 1) / bs + 5 np_b
+  // <= max_blocks + (kIdCap - 1) + 5 np_b, since P <= (kIdCap - 1) * bs.
+  return static_cast<int64_t>(num_seqs) * (max_blocks + mv::kIdCap) + 5 * work_capacity;
+}
+
 extern "C" size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
                                                   int32_t head_dim, int32_t max_partitions) {
   if (max_partitions <= 1 || num_seqs <= 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
@@ -827,20 +903,26 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
                               int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs,
                               int32_t max_blocks, int32_t block_size, int64_t num_blocks,
                               int32_t chunk_tokens, int32_t num_kv_heads, int32_t target_groups,
-                              int32_t* kv_len_i32, int32_t* work_items, int64_t work_capacity,
-                              int32_t* counters, int32_t* status, void* stream) {
+                              int32_t* work_items, int64_t work_capacity, int32_t* block_ids,
+                              int64_t block_ids_capacity, int32_t* counters, int32_t* status,
+                              void* stream) {
   using namespace mv;
   if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null status");
-  if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0 || num_blocks < 0 || num_kv_heads <= 0)
+  if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0 || block_ids_capacity < 0 ||
+      num_blocks < 0 || num_kv_heads <= 0)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: bad sizes");
   if (chunk_tokens <= 0 || chunk_tokens % kTile)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: chunk_tokens %d", chunk_tokens);
   if (!is_pow2(block_size))
     return fail(MV_ERR_UNSUPPORTED, "mv_decode_plan: block_size %d is not a power of 2", block_size);
-  if (num_seqs > 0 && (!kv_len || !kv_len_i32 || !counters || (max_blocks > 0 && !block_table)))
+  if (num_seqs > 0 && (!kv_len || !counters || (max_blocks > 0 && !block_table)))
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null pointer");
-  if (work_capacity > 0 && !work_items)
+  if ((work_capacity > 0 && !work_items) || (block_ids_capacity > 0 && !block_ids))
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null work list");
+  if (block_ids_capacity < mv_decode_block_ids_capacity(num_seqs, max_blocks, work_capacity))
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: block_ids capacity %lld < %lld",
+                static_cast<long long>(block_ids_capacity),
+                static_cast<long long>(mv_decode_block_ids_capacity(num_seqs, max_blocks, work_capacity)));
   PlanArgs a;
   a.kv_len = kv_len;
   a.block_table = block_table;
@@ -852,9 +934,10 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
   a.num_kv_heads = num_kv_heads;
   a.target_groups = target_groups;
   a.num_blocks = num_blocks;
-  a.kv_out = kv_len_i32;
   a.work = work_items;
   a.work_cap = work_capacity;
+  a.ids = block_ids;
+  a.ids_cap = block_ids_capacity;
   a.counters = counters;
   a.status = status;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -870,15 +953,14 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
 
 extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
                                const void* key_cache, const void* value_cache,
-                               const void* block_table, int32_t bt_is_i64, int64_t bt_stride,
-                               const int32_t* kv_len_i32, const int32_t* work_items,
-                               int32_t num_work_items, int32_t partition_tokens,
-                               int32_t max_partitions, int32_t* counters, void* out,
-                               int64_t out_stride_tok, int64_t out_stride_head, float scale,
-                               int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
-                               int32_t head_dim, int32_t block_size, int64_t num_blocks,
-                               int32_t dtype, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+                               const int32_t* work_items, const int32_t* block_ids,
+                               int64_t block_ids_capacity, int32_t num_work_items,
+                               int32_t partition_tokens, int32_t max_partitions, int32_t* counters,
+                               void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                               float scale, int32_t num_seqs, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                               int64_t num_blocks, int32_t dtype, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   using namespace mv;
   const int eb = dtype_bytes(dtype);
   if (eb == 0) return fail(MV_ERR_UNSUPPORTED, "mv_paged_decode: unknown dtype %d", dtype);
@@ -894,7 +976,8 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
   if (n_rep > kMaxGroup)
     return fail(MV_ERR_UNSUPPORTED, "mv_paged_decode: %d query heads per kv head (max %d)", n_rep,
                 kMaxGroup);
-  if (num_seqs < 0 || num_work_items < 0 || num_blocks <= 0 || max_partitions < 0)
+  if (num_seqs < 0 || num_work_items < 0 || num_blocks <= 0 || max_partitions < 0 ||
+      block_ids_capacity < 0)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: bad sizes");
   const int chunk = chunk_tokens(head_dim, dtype);
   if (partition_tokens <= 0 || partition_tokens % chunk)
@@ -906,13 +989,21 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
                 "mv_paged_decode: partition_tokens %d spans more than %d blocks of %d tokens",
                 partition_tokens, kIdCap - 1, block_size);
   if (num_seqs == 0 || num_work_items == 0) return MV_OK;
-  if (!query || !key_cache || !value_cache || !block_table || !kv_len_i32 || !work_items || !out)
+  if (!query || !key_cache || !value_cache || !work_items || !block_ids || !out)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: null pointer");
-  // 16-byte loads of q rows and cache rows.
+  const int bs_log2 = ilog2_exact(block_size);
+  const int per_item = ids_per_item(partition_tokens, bs_log2);
+  if (static_cast<int64_t>(num_work_items) * per_item > block_ids_capacity)
+    return fail(MV_ERR_INVALID_ARGUMENT,
+                "mv_paged_decode: %d work items x %d block ids exceed capacity %lld",
+                num_work_items, per_item, static_cast<long long>(block_ids_capacity));
+  // 16-byte copies of q rows, cache rows and block-id lists.
   if ((reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key_cache) |
-       reinterpret_cast<uintptr_t>(value_cache)) % 16 ||
+       reinterpret_cast<uintptr_t>(value_cache) | reinterpret_cast<uintptr_t>(block_ids) |
+       reinterpret_cast<uintptr_t>(work_items)) % 16 ||
       (q_stride_tok * eb) % 16 || (q_stride_head * eb) % 16)
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: query/cache rows not 16-byte aligned");
+    return fail(MV_ERR_INVALID_ARGUMENT,
+                "mv_paged_decode: query/cache rows or plan arrays not 16-byte aligned");
   if (max_partitions > 0 && num_work_items > max_partitions * static_cast<int64_t>(num_seqs))
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: work list larger than the plan allows");
 
@@ -922,10 +1013,9 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
   a.q_stride_head = q_stride_head;
   a.k_cache = static_cast<const char*>(key_cache);
   a.v_cache = static_cast<const char*>(value_cache);
-  a.block_table = block_table;
-  a.bt_stride = bt_stride;
-  a.kv_len = kv_len_i32;
   a.work = work_items;
+  a.block_ids = block_ids;
+  a.ids_per_item = per_item;
   a.counters = counters;
   a.out = out;
   a.out_stride_tok = out_stride_tok;
@@ -934,7 +1024,7 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
   a.n_rep = n_rep;
-  a.bs_log2 = ilog2_exact(block_size);
+  a.bs_log2 = bs_log2;
   a.max_parts = max_partitions;
   a.part_tokens = partition_tokens;
   a.num_blocks = num_blocks;
@@ -954,10 +1044,9 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
     a.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((o + 255) / 256) * 256);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool bt64 = bt_is_i64 != 0;
   switch (dtype) {
-    case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, bt64, num_work_items, s);
-    case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, bt64, num_work_items, s);
-    default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, bt64, num_work_items, s);
+    case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, num_work_items, s);
+    case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, num_work_items, s);
+    default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, num_work_items, s);
   }
 }

@@ -33,6 +33,7 @@ MV_PLAN_BAD_BLOCK = 3
 MV_PLAN_MAX_PARTS = 4
 MV_PLAN_MIN_KV_LEN = 5
 MV_PLAN_PARTITION_TOKENS = 6
+MV_PLAN_IDS_PER_ITEM = 7
 MV_PLAN_WORDS = 8
 
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
@@ -62,13 +63,15 @@ SIGNATURES = {
         _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride
         _I32, _I32, _I32, _I64,    # num_seqs, max_blocks, block_size, num_blocks
         _I32, _I32, _I32,          # chunk_tokens, num_kv_heads, target_groups
-        _P, _P, _I64, _P, _P, _P,  # kv_len_i32, work_items, capacity, counters, status, stream
+        _P, _I64, _P, _I64,        # work_items, capacity, block_ids, capacity
+        _P, _P, _P,                # counters, status, stream
     ]),
+    "mv_decode_block_ids_capacity": (_I64, [_I32, _I32, _I64]),
     "mv_paged_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
     "mv_paged_decode": (ctypes.c_int, [
         _P, _I64, _I64,            # query, strides
-        _P, _P, _P, _I32, _I64,    # key_cache, value_cache, block_table, bt_is_i64, bt_stride
-        _P, _P, _I32,              # kv_len_i32, work_items, num_work_items
+        _P, _P,                    # key_cache, value_cache
+        _P, _P, _I64, _I32,        # work_items, block_ids, block_ids_capacity, num_work_items
         _I32, _I32, _P,            # partition_tokens, max_partitions, counters
         _P, _I64, _I64,            # out, strides
         _F, _I32, _I32, _I32, _I32,  # scale, num_seqs, num_q_heads, num_kv_heads, head_dim

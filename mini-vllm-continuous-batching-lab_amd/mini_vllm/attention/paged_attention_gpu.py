@@ -219,9 +219,8 @@ def hip_cache_write(
 class DecodePlan:
     """Device-side per-step decode metadata produced by ``mv_decode_plan``."""
 
-    block_table: torch.Tensor  # [num_seqs, max_blocks] int32/int64 on the device
-    kv_len_i32: torch.Tensor   # [num_seqs] int32
     work: torch.Tensor         # [4 * capacity] int32 (seq, partition, kv_len, 0)
+    block_ids: torch.Tensor    # [capacity] int32: ids_per_item pool blocks per work item
     counters: torch.Tensor     # [num_seqs * num_kv_heads] int32, zero between calls
     num_items: int
     max_parts: int
@@ -290,17 +289,18 @@ def plan_decode(
     num_seqs = kv.shape[0]
     max_blocks = bt.shape[1] if bt.dim() == 2 else 0
     cap = num_seqs * max(1, math.ceil(max_blocks * block_size / chunk))
-    kv32 = torch.empty(max(num_seqs, 1), dtype=torch.int32, device=device)
     work = torch.empty(4 * max(cap, 1), dtype=torch.int32, device=device)
+    ids_cap = lib.mv_decode_block_ids_capacity(num_seqs, max_blocks, cap)
+    block_ids = torch.empty(max(ids_cap, 4), dtype=torch.int32, device=device)
     counters = torch.empty(max(num_seqs * num_kv_heads, 1), dtype=torch.int32, device=device)
     status = torch.empty(_hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
     _hip.check(
         lib.mv_decode_plan(
             _ptr(kv), int(kv.dtype == torch.int64), _ptr(bt), int(bt.dtype == torch.int64),
             bt.stride(0) if bt.dim() == 2 else 0, num_seqs, max_blocks, block_size,
-            num_blocks, chunk, num_kv_heads, _target_groups(device, head_dim, dtype), _ptr(kv32),
-            _ptr(work),
-            cap, _ptr(counters), _ptr(status), _stream(device),
+            num_blocks, chunk, num_kv_heads, _target_groups(device, head_dim, dtype),
+            _ptr(work), cap, _ptr(block_ids), block_ids.numel(),
+            _ptr(counters), _ptr(status), _stream(device),
         ),
         "mv_decode_plan",
     )
@@ -321,9 +321,9 @@ def plan_decode(
             f"that are not pool blocks [0, {num_blocks})"
         )
     num_items = st[_hip.MV_PLAN_NUM_ITEMS]
-    if num_items > cap:
-        raise RuntimeError(f"decode plan: {num_items} work items exceed capacity {cap}")
-    plan = DecodePlan(bt, kv32, work, counters, num_items, st[_hip.MV_PLAN_MAX_PARTS],
+    if num_items > cap or st[_hip.MV_PLAN_IDS_PER_ITEM] < 0:
+        raise RuntimeError(f"decode plan: {num_items} work items exceed the plan capacity {cap}")
+    plan = DecodePlan(work, block_ids, counters, num_items, st[_hip.MV_PLAN_MAX_PARTS],
                       st[_hip.MV_PLAN_PARTITION_TOKENS])
     _cache_put("plan", (block_table, kv_len_after), extra, plan)
     return plan
@@ -385,12 +385,11 @@ def hip_decode_attention(
     lib = _hip.load()
     ws_bytes = lib.mv_paged_decode_workspace_bytes(total_decode, num_q_heads, head_dim, plan.max_parts)
     ws = _workspace(device, ws_bytes) if ws_bytes else None
-    bt = plan.block_table
     _hip.check(
         lib.mv_paged_decode(
             _ptr(query), query.stride(0), query.stride(1),
-            _ptr(key_cache), _ptr(value_cache), _ptr(bt), int(bt.dtype == torch.int64),
-            bt.stride(0), _ptr(plan.kv_len_i32), _ptr(plan.work), plan.num_items,
+            _ptr(key_cache), _ptr(value_cache),
+            _ptr(plan.work), _ptr(plan.block_ids), plan.block_ids.numel(), plan.num_items,
             plan.partition_tokens, plan.max_parts, _ptr(plan.counters),
             _ptr(output), output.stride(0), output.stride(1),
             float(head_dim ** -0.5), total_decode, num_q_heads, num_kv_heads, head_dim,
