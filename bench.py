@@ -17,6 +17,11 @@ per-sequence gather + SDPA loop) timed on this host's cores on the same
 workload in fp32.
 
     python bench.py [--steps K] [--warmup W] [--workload c2] [--no-cpu-baseline]
+    python bench.py --copy-calibration   # plain 256 MiB copies, for PMC byte scaling
+
+``roofline.traffic`` (HBM bytes per decode launch) comes from the
+rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under profiles/ for
+the workload, when there is one; otherwise it is null.
 """
 
 from __future__ import annotations
@@ -146,6 +151,37 @@ def cpu_baseline(spec, layout, layer, budget_s=12.0):
     }
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "paged_decode_kernel_{workload}_traffic.md")
+COPY_BYTES = 256 << 20
+
+
+def measured_traffic(workload):
+    """HBM bytes per decode launch from the committed PMC summary (a line
+    ``traffic_bytes_per_launch: N``), or None."""
+    path = TRAFFIC_SUMMARY.format(workload=workload)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(steps):
+    """A plain device copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES)
+    per launch: what FETCH_SIZE / WRITE_SIZE report for it scales the
+    counters of the decode kernel to bytes."""
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": COPY_BYTES, "launches": steps}), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,6 +190,7 @@ def main(argv=None) -> int:
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(SPECS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -165,6 +202,8 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        return copy_calibration(args.steps if args.steps != 200 else 10)
 
     from mini_vllm.attention import _hip
     from mini_vllm.attention.paged_attention_gpu import (
@@ -259,7 +298,7 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(dec_gbs / PEAK_HBM_GBS, 4),
             "algorithmic_bytes": dec_bytes,
-            "traffic": None,
+            "traffic": measured_traffic(spec.name),
         },
         "cpu_baseline": None,
     }

@@ -83,7 +83,7 @@ int mv_decode_groups_per_cu(int32_t head_dim, int32_t dtype);
 /*
  * KV-cache write.
  * Replaces the launch of `_cache_write_kernel` in `triton_cache_write`
- * (mini_vllm/attention/paged_attention_gpu.py:90-154, kernel :32-87) and
+ * (mini_vllm/attention/paged_attention_gpu.py:90-154, kernel :33-87) and
  * follows `write_to_paged_cache` (mini_vllm/cache/cache_write.py:25-74):
  *   for t in [0, num_tokens): s = slot_mapping[t]; s == -1 skips;
  *     key_cache[s / block_size, h, s % block_size, :] = key[t, h, :]
@@ -160,7 +160,7 @@ size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, in
 /*
  * Paged decode attention (one kernel launch).
  * Replaces the launch of `_paged_decode_kernel` in `triton_decode_attention`
- * (paged_attention_gpu.py:252-321, kernel :162-249); the math is that of
+ * (paged_attention_gpu.py:252-321, kernel :163-249); the math is that of
  * `AttentionBackendRef.decode_attention`
  * (mini_vllm/attention/paged_attention_ref.py:102-161):
  *   out[b, hq, :] = softmax(scale * q[b, hq] . K_b[hk]^T) V_b[hk],
@@ -193,7 +193,7 @@ int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_he
 /*
  * Prefix gather (prefill support).
  * Replaces the launch of `_gather_prefix_kv_kernel` in `gather_prefix_kv`
- * (mini_vllm/attention/paged_attention_gpu.py:391-446, kernel :329-388),
+ * (mini_vllm/attention/paged_attention_gpu.py:391-446, kernel :330-388),
  * semantics of `gather_paged_kv` (mini_vllm/cache/cache_read.py:19-84):
  *   out[cu_tokens[i] + p, h, :] = cache[bt[seq_rows[i], p / bs], h, p % bs, :]
  *   for p < cu_tokens[i+1] - cu_tokens[i], i < num_seqs.

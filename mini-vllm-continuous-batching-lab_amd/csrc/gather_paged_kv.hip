@@ -1,7 +1,7 @@
 // Gather of cached prefix K/V into contiguous rows (prefill support).
 //
 // Replaces the Triton `_gather_prefix_kv_kernel`
-// (mini_vllm/attention/paged_attention_gpu.py:329-388) and follows
+// (mini_vllm/attention/paged_attention_gpu.py:330-388) and follows
 // `gather_paged_kv` (mini_vllm/cache/cache_read.py:19-84): for sequence i,
 // token pos < cu_tokens[i+1] - cu_tokens[i] of table row seq_rows[i]
 //   out[cu_tokens[i] + pos, h, :] = cache[bt[row, pos / BS], h, pos % BS, :]

@@ -1,7 +1,7 @@
 // KV-cache write (scatter by slot) and slot validation for gfx950.
 //
 // Follows write_to_paged_cache (mini_vllm/cache/cache_write.py:25-74) and
-// replaces the Triton `_cache_write_kernel` (paged_attention_gpu.py:32-87).
+// replaces the Triton `_cache_write_kernel` (paged_attention_gpu.py:33-87).
 //
 // Layout of one token row: key[t, h, 0:D] sits at key + t*stride_tok +
 // h*stride_head (elements) with the D elements contiguous; its destination

@@ -14,19 +14,28 @@
 //   K/V byte is read from HBM exactly once. The work group walks its
 //   partition in chunks of kWaves 16-token tiles, one tile per wave.
 //
+// Prologue (one dependent memory round trip before the first tile):
+//   the work item (seq, partition, kv_len) and the partition's pool block
+//   ids, both addressed by blockIdx alone (the plan kernel stores each
+//   item's ids), arrive together; the ids go straight to LDS. The group's
+//   Q rows are then copied to LDS alongside the first tiles.
+//
 // Per tile (16 tokens x D) and wave, with lane = 16*g + t (g = 0..3):
 //   * HBM -> LDS without registers: global_load_lds_dwordx4 writes lane l's
 //     16 bytes to LDS slot (64c + l) of load instruction c. Each lane
 //     fetches the 16-byte piece that belongs in its slot under an XOR
 //     swizzle (slot s of row r holds piece s ^ sw(r)), so every load
 //     instruction still reads 1 KiB of contiguous HBM while the reads
-//     below are bank-conflict free with unpadded rows. Two LDS buffers per
-//     wave: the next tile streams in while the current one is computed.
+//     below are bank-conflict free with unpadded rows. kStages buffers per
+//     wave: up to kStages - 1 tiles stream in while one is computed, with
+//     exact vmcnt waits (the copies are issued through inline asm so the
+//     compiler does not drain them before every LDS access).
 //   * S^T = K Q^T on MFMA (16x16x32 for 16-bit types, 16x16x4 for fp32):
 //     A = K tile (M = tokens), row t, dims [g*D/4, (g+1)*D/4) from LDS;
-//     B = Q^T (N = query heads of the group, rows >= n_rep zero) from
-//     registers. Both operands use the same k-slot -> dim mapping, so the
-//     contraction covers all D dims whatever the hardware's k order.
+//     B = Q^T (N = query heads of the group; columns >= n_rep repeat a
+//     real head and are never stored) from registers. Both operands use
+//     the same k-slot -> dim mapping, so the contraction covers all D dims
+//     whatever the hardware's k order.
 //   * The accumulator holds S^T[token 4g+e][head t] in lane (g, t), slot e
 //     -- the A-operand layout of the P V MFMA (M = heads, K = tokens), so
 //     the probabilities never leave registers.
@@ -40,11 +49,11 @@
 // (o, max, sum) in fp32 with device-coherent stores, waits for them to
 // complete and bumps the (sequence, kv head) counter; the work group that
 // brings the counter to n_parts merges all partials with a log-sum-exp
-// reduce (device-coherent loads), writes the output and resets the counter
-// to zero. (A __threadfence() here would write back and invalidate the
-// whole L2 of the XCD in every wave, which costs ~10x the kernel.)
-// Counters are zeroed by the plan kernel, so every call that shares a plan
-// must run on one stream.
+// reduce (device-coherent loads, one round of loads per up to 16
+// partitions), writes the output and resets the counter to zero. (A
+// __threadfence() here would write back and invalidate the whole L2 of the
+// XCD in every wave, which costs ~10x the kernel.) Counters are zeroed by
+// the plan kernel, so every call that shares a plan must run on one stream.
 #include <algorithm>
 #include <climits>
 

@@ -615,13 +615,15 @@ class AttentionBackendGPU(AttentionBackend):
                 q_pos = torch.arange(c, c + ql, device=query.device)
                 k_pos = torch.arange(c + ql, device=query.device)
                 mask = k_pos.unsqueeze(0) <= q_pos.unsqueeze(1)
+                # fp32: SDPA's math path issues batched products on transposed
+                # views, which are not safe in 16-bit types on this platform.
                 out = F.scaled_dot_product_attention(
-                    query[offset:offset + ql].permute(1, 0, 2).unsqueeze(0),
-                    full_k.permute(1, 0, 2).unsqueeze(0).contiguous(),
-                    full_v.permute(1, 0, 2).unsqueeze(0).contiguous(),
+                    query[offset:offset + ql].permute(1, 0, 2).unsqueeze(0).float().contiguous(),
+                    full_k.permute(1, 0, 2).unsqueeze(0).float().contiguous(),
+                    full_v.permute(1, 0, 2).unsqueeze(0).float().contiguous(),
                     attn_mask=mask, is_causal=False, scale=scale,
                 )
-                outputs.append(out.squeeze(0).permute(1, 0, 2))
+                outputs.append(out.squeeze(0).permute(1, 0, 2).to(query.dtype))
                 offset += ql
         if not outputs:
             return query

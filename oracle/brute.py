@@ -63,3 +63,34 @@ def decode(q, key_cache, value_cache, block_table, kv_len, block_size, scale=Non
             p = np.exp(logits - m)
             out[b, h] = (p[:, None] * v).sum(axis=0) / p.sum()
     return out
+
+
+def prefill(q, key_cache, value_cache, block_tables, seq_indices, cached_len_before, query_len,
+            block_size, scale=None):
+    """float64 chunked prefill: query token t of sequence i sits at position
+    cached_len_before[i] + t and attends key positions 0 .. that position
+    (mini_vllm/attention/paged_attention_ref.py:167-244). ``q`` is the
+    concatenation [sum(query_len), Hq, D] in sequence order."""
+    q = np.asarray(q, dtype=np.float64)
+    kc = np.asarray(key_cache, dtype=np.float64)
+    vc = np.asarray(value_cache, dtype=np.float64)
+    bt = np.asarray(block_tables)
+    hq, d = q.shape[1], q.shape[2]
+    n_rep = hq // kc.shape[1]
+    if scale is None:
+        scale = d ** -0.5
+    out = np.zeros_like(q)
+    off = 0
+    for i, s in enumerate(seq_indices):
+        c, ql = int(cached_len_before[i]), int(query_len[i])
+        blk, pos = token_rows(bt[int(s)], c + ql, block_size)
+        for t in range(ql):
+            n = c + t + 1  # causal: positions 0 .. c + t
+            for h in range(hq):
+                k = kc[blk[:n], h // n_rep, pos[:n], :]
+                v = vc[blk[:n], h // n_rep, pos[:n], :]
+                logits = (k @ q[off + t, h]) * scale
+                p = np.exp(logits - logits.max())
+                out[off + t, h] = (p[:, None] * v).sum(axis=0) / p.sum()
+        off += ql
+    return out
