@@ -289,7 +289,7 @@ def main(argv=None) -> int:
         "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "plan_us_per_step": round(plan_us, 1),
         "partition_tokens": plan.partition_tokens,
-        "work_groups": plan.num_items * spec.num_kv_heads,
+        "work_groups": plan.num_groups,
         "roofline": {
             "bound": "hbm",
             "kernel": "paged_decode_kernel (one launch, partition merge fused)",

@@ -55,14 +55,14 @@ extern "C" {
 #define MV_SLOTS_DUPLICATES 1   /* # (i < j) pairs with slot[i] == slot[j] >= 0 */
 
 /* Status words written by mv_decode_plan (int32[8], device memory). */
-#define MV_PLAN_NUM_ITEMS 0     /* number of (sequence, partition) work items */
+#define MV_PLAN_NUM_ITEMS 0     /* number of work groups (launch grid) */
 #define MV_PLAN_BAD_KV_LEN 1    /* # sequences with kv_len < 1 */
 #define MV_PLAN_INSUFFICIENT 2  /* # sequences whose table row cannot cover kv_len */
 #define MV_PLAN_BAD_BLOCK 3     /* # table entries used by kv_len outside [0, num_blocks) */
-#define MV_PLAN_MAX_PARTS 4     /* max partitions of any sequence */
+#define MV_PLAN_MAX_PARTS 4     /* max pieces of any sequence */
 #define MV_PLAN_MIN_KV_LEN 5    /* min kv_len (clamped to int32) */
-#define MV_PLAN_PARTITION_TOKENS 6 /* tokens per partition chosen for this step */
-#define MV_PLAN_IDS_PER_ITEM 7  /* block ids stored per work item (-1: capacity exceeded) */
+#define MV_PLAN_PARTITION_TOKENS 6 /* piece bound P chosen for this step */
+#define MV_PLAN_IDS_PER_ITEM 7  /* block ids stored per work group (-1: capacity exceeded) */
 #define MV_PLAN_WORDS 8
 
 /* Version of this ABI (MVATTN_ABI_VERSION of the built library). */
@@ -77,7 +77,7 @@ int mv_decode_chunk_tokens(int32_t head_dim, int32_t dtype);
 
 /* Decode work groups one compute unit holds at once for (head_dim, dtype)
  * (LDS-limited); times the CU count it is the work-group count that runs in
- * a single dispatch round, the natural target_groups of mv_decode_plan. */
+ * a single dispatch round (the groups_per_cu of mv_decode_plan). */
 int mv_decode_groups_per_cu(int32_t head_dim, int32_t dtype);
 
 /*
@@ -113,7 +113,7 @@ int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t t
                       int32_t* status, void* stream);
 
 /*
- * Per-step decode metadata: validation, partition size, work list.
+ * Per-step decode metadata: validation, work split, work list.
  * Replaces the per-layer `kv_len_after.clone().to(int32)` of
  * `AttentionBackendGPU.decode_attention` (paged_attention_gpu.py:560-562)
  * and the `(kv_len_after < 1).any()` check of `triton_decode_attention`
@@ -122,35 +122,43 @@ int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t t
  *   kv_len      [num_seqs] int64 (kv_len_is_i64=1) or int32
  *   block_table [num_seqs, max_blocks] (row stride bt_stride), int64
  *               (bt_is_i64=1) or int32, -1 padded
- * Chooses the partition size P: the smallest multiple of chunk_tokens
- * (mv_decode_chunk_tokens) that keeps the number of (sequence, kv head,
- * partition) work groups within target_groups (aiming at no more than 128
- * partitions per sequence), capped so that a partition spans at most 511
- * table entries. Outputs:
- *   work_items  int32 quadruples (seq, partition, kv_len, 0), 16-byte
- *               aligned, capacity work_capacity quadruples
- *               (num_seqs * ceil(max_blocks * block_size / chunk_tokens)
- *               always suffices);
- *   block_ids   for work item i, int32 [i * n, (i + 1) * n) with
- *               n = status[MV_PLAN_IDS_PER_ITEM]: the pool blocks of table
- *               entries P*p/bs .. of its sequence, -1 past its last block;
+ * Cuts every sequence into pieces of equal 16-token tile counts, at most P
+ * tokens each, P the smallest multiple of 16 that keeps the (sequence, kv
+ * head, piece) work groups within groups_per_cu * cu_count
+ * (mv_decode_groups_per_cu: one dispatch round) -- unless that takes
+ * pieces over twice the slots' fair share, then about the fair share in
+ * several rounds -- aiming at no more than 128 pieces per sequence and
+ * spanning at most 511 table entries. When the groups fit one round they
+ * are dealt to launch slots by size so the compute units carry near-equal
+ * bytes. Outputs:
+ *   work_items  per work group (launch slot), int32[8]: (seq, kv head,
+ *               piece, pieces of the sequence, first token, end token, 0,
+ *               0); 32-byte aligned, capacity work_capacity groups
+ *               (num_seqs * num_kv_heads * ceil(max_blocks * block_size /
+ *               16) always suffices);
+ *   block_ids   for slot s, int32 [s * n, (s + 1) * n) with
+ *               n = status[MV_PLAN_IDS_PER_ITEM]: the pool blocks of the
+ *               table entries its tokens lie in, -1 past the last;
  *               16-byte aligned, block_ids_capacity >=
  *               mv_decode_block_ids_capacity(num_seqs, max_blocks,
- *               work_capacity) ints;
+ *               num_kv_heads, work_capacity) ints;
  *   counters    [num_seqs * num_kv_heads] set to zero;
- *   status      [MV_PLAN_WORDS].
+ *   status      [MV_PLAN_WORDS] (MV_PLAN_NUM_ITEMS = work groups to launch,
+ *               MV_PLAN_PARTITION_TOKENS = P, MV_PLAN_MAX_PARTS = most pieces
+ *               of one sequence).
  * One work group; enqueue only.
  */
 int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                    int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs, int32_t max_blocks,
-                   int32_t block_size, int64_t num_blocks, int32_t chunk_tokens,
-                   int32_t num_kv_heads, int32_t target_groups, int32_t* work_items,
-                   int64_t work_capacity, int32_t* block_ids, int64_t block_ids_capacity,
-                   int32_t* counters, int32_t* status, void* stream);
+                   int32_t block_size, int64_t num_blocks, int32_t num_kv_heads,
+                   int32_t groups_per_cu, int32_t cu_count,
+                   int32_t* work_items, int64_t work_capacity, int32_t* block_ids,
+                   int64_t block_ids_capacity, int32_t* counters, int32_t* status, void* stream);
 
 /* Ints of block_ids storage mv_decode_plan needs (an upper bound for any
- * kv_len and partition size). */
-int64_t mv_decode_block_ids_capacity(int32_t num_seqs, int32_t max_blocks, int64_t work_capacity);
+ * kv_len and piece size). */
+int64_t mv_decode_block_ids_capacity(int32_t num_seqs, int32_t max_blocks, int32_t num_kv_heads,
+                                     int64_t work_capacity);
 
 /* Bytes of fp32 workspace mv_paged_decode needs for `max_partitions`
  * partitions per sequence (0 when max_partitions <= 1). */
@@ -167,9 +175,9 @@ size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, in
  *   hk = hq / (num_q_heads / num_kv_heads), over kv_len[b] tokens whose
  *   token j lives at block block_table[b, j / block_size], offset
  *   j % block_size.
- * The sequences, lengths and blocks come from mv_decode_plan on the same
- * metadata: work_items, block_ids, counters, num_work_items =
- * status[MV_PLAN_NUM_ITEMS], partition_tokens =
+ * The sequences, token ranges and blocks come from mv_decode_plan on the
+ * same metadata: work_items, block_ids, counters, num_work_groups =
+ * status[MV_PLAN_NUM_ITEMS] (one work group each), partition_tokens =
  * status[MV_PLAN_PARTITION_TOKENS], max_partitions =
  * status[MV_PLAN_MAX_PARTS]; the block table itself is not read.
  * Sequences split into several partitions are merged inside the same
@@ -183,7 +191,7 @@ size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, in
  */
 int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
                     const void* key_cache, const void* value_cache, const int32_t* work_items,
-                    const int32_t* block_ids, int64_t block_ids_capacity, int32_t num_work_items,
+                    const int32_t* block_ids, int64_t block_ids_capacity, int32_t num_work_groups,
                     int32_t partition_tokens, int32_t max_partitions, int32_t* counters, void* out,
                     int64_t out_stride_tok, int64_t out_stride_head, float scale,
                     int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,

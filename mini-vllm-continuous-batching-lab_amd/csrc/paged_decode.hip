@@ -102,7 +102,10 @@ struct Traits {
   static constexpr int kQOffset = kIdsOffset + kIdCap * 4;  // Q rows of the group (16 x D)
   static constexpr int kQLoads = kTile * kRowBytes / 1024;  // 1 KiB copies of the Q rows
   static constexpr int kTilesEnd = kQOffset + kTile * kRowBytes;
-  static constexpr int kWaveOBytes = kWaves * kMaxGroup * D * 4;     // wave merge o
+  // Wave merge o rows, padded by 4 floats: the accumulator rows 4g+e that
+  // one store instruction writes then start 16 banks apart.
+  static constexpr int kORowStride = D + 4;
+  static constexpr int kWaveOBytes = kWaves * kMaxGroup * kORowStride * 4;
   static constexpr int kStatsOffset = kWaveOBytes;                    // s_max, s_sum
   static constexpr int kFlagOffset = kStatsOffset + 2 * kWaves * kMaxGroup * 4;
   static constexpr int kMergeEnd = kFlagOffset + 16;
@@ -132,14 +135,14 @@ __device__ __forceinline__ int piece_swizzle(int r) {
 // Kernel arguments; the fields the prologue needs come first, so a couple
 // of wide scalar loads fetch them together.
 struct DecodeArgs {
-  const int32_t* work;       // (seq, partition, kv_len, 0) quadruples
-  const int32_t* block_ids;  // [work item][ids_per_item]: the partition's pool blocks, -1 padded
+  const int32_t* work;       // per work group: (seq, kv head, piece, pieces, token begin, end, 0, 0)
+  const int32_t* block_ids;  // [work group][ids_per_item]: the piece's pool blocks, -1 padded
   const void* q;
   const char* k_cache;
   const char* v_cache;
   int64_t q_stride_tok, q_stride_head;  // elements
   int32_t ids_per_item;                 // multiple of 4, <= kIdCap
-  int32_t num_kv_heads, n_rep, bs_log2, part_tokens;
+  int32_t num_kv_heads, n_rep, bs_log2;
   float scale_log2;                     // scale * log2(e)
   int32_t num_q_heads, max_parts;
   int64_t num_blocks;
@@ -312,9 +315,8 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   // costs several scalar memory round trips before the first copy.
   asm volatile("" ::"s"(a.work), "s"(a.block_ids), "s"(a.ids_per_item), "s"(a.num_kv_heads),
                "s"(a.q), "s"(a.q_stride_tok), "s"(a.q_stride_head), "s"(a.n_rep), "s"(a.k_cache),
-               "s"(a.v_cache), "s"(a.bs_log2), "s"(a.part_tokens));
-  const int item = blockIdx.x / a.num_kv_heads;
-  const int h = blockIdx.x - item * a.num_kv_heads;
+               "s"(a.v_cache), "s"(a.bs_log2));
+  const int item = blockIdx.x;
   const uint32_t lds0 = lds_address(s_lds);
   int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
 
@@ -330,15 +332,16 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
                     __builtin_amdgcn_readfirstlane(lds0 + Tr::kIdsOffset + wave * 1024));
   }
   asm volatile("" ::: "memory");
-  const int4 wi = reinterpret_cast<const int4*>(a.work)[item];  // (seq, partition, kv_len, -)
+  const int4 w0 = reinterpret_cast<const int4*>(a.work + 8 * static_cast<int64_t>(item))[0];
+  const int4 w1 = reinterpret_cast<const int4*>(a.work + 8 * static_cast<int64_t>(item))[1];
   wait_vmcnt<0>();
   asm volatile("" ::: "memory");
-  const int b = wi.x;
-  const int part = wi.y;
-  const int kv = wi.z;
-  const int n_parts = (kv + a.part_tokens - 1) / a.part_tokens;
-  const int tok_begin = part * a.part_tokens;
-  const int tok_end = min(kv, tok_begin + a.part_tokens);
+  const int b = w0.x;        // sequence
+  const int h = w0.y;        // kv head
+  const int part = w0.z;     // piece of the sequence
+  const int n_parts = w0.w;  // pieces of the sequence
+  const int tok_begin = w1.x;
+  const int tok_end = w1.y;
   const int n_chunks = (tok_end - tok_begin + Tr::kChunk - 1) / Tr::kChunk;
   const int bs_mask = (1 << a.bs_log2) - 1;
   const int first_blk = tok_begin >> a.bs_log2;  // s_ids[i] = pool block of table entry first_blk + i
@@ -526,7 +529,8 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   // load or store instruction then covers 128 contiguous bytes per head.
   constexpr int NPAIR = Tr::kPairsPerThread;
   __syncthreads();  // every wave is done with its tiles (s_lds is reused)
-  float* s_o = reinterpret_cast<float*>(s_lds);  // [kWaves][kMaxGroup][D]
+  constexpr int OS = Tr::kORowStride;
+  float* s_o = reinterpret_cast<float*>(s_lds);  // [kWaves][kMaxGroup][OS]
   if (g == 0) {
     s_max[wave][t] = m_run;
     s_sum[wave][t] = l_run;
@@ -536,7 +540,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = 4 * g + e;  // accumulator row = query head of the group
-      if (row < a.n_rep) s_o[(wave * kMaxGroup + row) * D + 16 * c + t] = o[c][e];
+      if (row < a.n_rep) s_o[(wave * kMaxGroup + row) * OS + 16 * c + t] = o[c][e];
     }
   }
   __syncthreads();
@@ -552,19 +556,19 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     float2 v[NPAIR];
 #pragma unroll
     for (int j = 0; j < NPAIR; ++j) v[j] = make_float2(0.f, 0.f);
+    // Straight-line LDS reads (one round trip): a wave with no token of the
+    // partition has max -inf, sum 0 and o 0, and gets weight 0.
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       const float mw = s_max[w][r];
-      if (mw != kNegInf) {  // a wave with no token of the partition holds nothing
-        const float f = __builtin_amdgcn_exp2f(mw - mx);
-        sum += s_sum[w][r] * f;
-        const float* src = s_o + (w * kMaxGroup + r) * D + 2 * q;
+      const float f = mw == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
+      sum += s_sum[w][r] * f;
+      const float* src = s_o + (w * kMaxGroup + r) * OS + 2 * q;
 #pragma unroll
-        for (int j = 0; j < NPAIR; ++j) {
-          const float2 x = *reinterpret_cast<const float2*>(src + 32 * j);
-          v[j].x += x.x * f;
-          v[j].y += x.y * f;
-        }
+      for (int j = 0; j < NPAIR; ++j) {
+        const float2 x = *reinterpret_cast<const float2*>(src + 32 * j);
+        v[j].x += x.x * f;
+        v[j].y += x.y * f;
       }
     }
     const float inv = 1.f / sum;  // >= 1: the partition's largest logit contributes exp2(0)
@@ -673,10 +677,10 @@ struct PlanArgs {
   const void* kv_len;
   const void* block_table;
   int64_t bt_stride;
-  int32_t num_seqs, max_blocks, bs_log2, chunk_tokens, num_kv_heads, target_groups;
+  int32_t num_seqs, max_blocks, bs_log2, num_kv_heads, groups_per_cu, cu_count;
   int64_t num_blocks;
-  int32_t* work;
-  int64_t work_cap;
+  int32_t* work;      // [work_cap][8]: one entry per work group (launch slot)
+  int64_t work_cap;   // entries
   int32_t* ids;
   int64_t ids_cap;
   int32_t* counters;
@@ -684,6 +688,7 @@ struct PlanArgs {
 };
 
 constexpr int kPlanThreads = 1024;
+constexpr int kDealMax = 1024;  // work groups sorted and dealt to CUs in shared memory
 
 __device__ int block_sum(int v, int* scratch) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -692,6 +697,7 @@ __device__ int block_sum(int v, int* scratch) {
   __syncthreads();
   int total = 0;
   for (int w = 0; w < kPlanThreads / 64; ++w) total += scratch[w];
+  __syncthreads();  // scratch is reused by the next call
   return total;
 }
 
@@ -702,26 +708,52 @@ __device__ int block_max(int v, int* scratch) {
   __syncthreads();
   int m = 0;
   for (int w = 0; w < kPlanThreads / 64; ++w) m = max(m, scratch[w]);
+  __syncthreads();
   return m;
 }
 
-// Block ids stored per work item for a partition of `part_tokens` tokens:
-// it spans at most ceil(P / bs) + 1 table entries; rounded up to a multiple
-// of 4 so every item's list is 16-byte aligned.
+// Block ids stored per work group for pieces of at most `part_tokens`
+// tokens: a piece spans at most ceil(P / bs) + 1 table entries; rounded up
+// to a multiple of 4 so every list is 16-byte aligned.
 __host__ __device__ inline int ids_per_item(int64_t part_tokens, int bs_log2) {
   const int64_t n = ((part_tokens + (int64_t(1) << bs_log2) - 1) >> bs_log2) + 1;
   return static_cast<int>((n + 3) / 4 * 4);
 }
 
-// One work group: validates kv_len and the table entries each sequence
-// reads, picks the partition size, builds the (sequence, partition) list
-// with each item's pool blocks and zeroes the merge counters.
+// Token range of piece j of a sequence of kv tokens cut into np pieces:
+// equal shares of its 16-token tiles.
+__device__ inline int2 piece_range(int kv, int np, int j) {
+  const int tiles = (kv + kTile - 1) / kTile;
+  const int t0 = static_cast<int>(static_cast<int64_t>(j) * tiles / np) * kTile;
+  const int t1 = static_cast<int>(static_cast<int64_t>(j + 1) * tiles / np) * kTile;
+  return make_int2(t0, min(kv, t1));
+}
+
+// One work group builds the per-step decode plan:
+//   1. validates kv_len and every table entry a sequence reads;
+//   2. picks the piece bound L (16-token tiles): the smallest that keeps
+//      the (sequence, kv head, piece) work groups within one dispatch round
+//      (groups_per_cu x cu_count), so every group is resident at once --
+//      unless that needs pieces over twice the fair share of the slots (a
+//      few very long sequences): then pieces of about the fair share run in
+//      several rounds and the dispatcher balances them;
+//   3. cuts each sequence into ceil(tiles / L) pieces of equal tile counts;
+//   4. when the groups fit one round, sorts them by size and deals them to
+//      launch slots in snake order over the CUs: work group i of a resident
+//      grid runs on the same CU as group i + cu_count (dispatch is
+//      round-robin), so slot s lands on CU "s mod cu_count" and the CUs
+//      carry near-equal bytes (a CU streams at a bounded rate, so the most
+//      loaded one sets the kernel time);
+//   5. stores each slot's entry (seq, kv head, piece, pieces, token range)
+//      and pool block ids, and zeroes the merge counters.
 template <typename KV, typename BT>
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   __shared__ int s_scan[kPlanThreads];
   __shared__ int s_red[kPlanThreads / 64];
-  __shared__ int s_cnt[4];  // bad kv_len, insufficient table, bad block id, max partitions
+  __shared__ int s_cnt[4];  // bad kv_len, insufficient table, bad block id, max pieces
   __shared__ int s_min_kv;
+  __shared__ uint32_t s_key[kDealMax];                    // sort keys of the work groups
+  __shared__ int s_item_b[kDealMax], s_item_j[kDealMax];  // items (sequence, piece) when dealt
   const int tid = threadIdx.x;
   if (tid < 4) s_cnt[tid] = 0;
   if (tid == 0) s_min_kv = INT_MAX;
@@ -730,49 +762,75 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const KV* kvp = static_cast<const KV*>(a.kv_len);
   const BT* btp = static_cast<const BT*>(a.block_table);
   const int64_t bs = int64_t(1) << a.bs_log2;
+  const int hkv = a.num_kv_heads;
   auto valid_len = [&](int64_t kv) {
     return kv >= 1 && (kv + bs - 1) / bs <= a.max_blocks && kv <= INT_MAX / 2;
   };
+  auto tiles_of = [&](int b) -> int {
+    const int64_t kv = static_cast<int64_t>(kvp[b]);
+    return valid_len(kv) ? static_cast<int>((kv + kTile - 1) / kTile) : 0;
+  };
 
-  // pass 1: validate lengths, count chunks
-  int chunks = 0, max_chunks = 0;
+  // ---- 1. lengths
+  int tiles = 0, max_tiles = 0, seqs = 0;
   for (int b = tid; b < a.num_seqs; b += kPlanThreads) {
     const int64_t kv = static_cast<int64_t>(kvp[b]);
     atomicMin(&s_min_kv, static_cast<int>(std::max<int64_t>(std::min<int64_t>(kv, INT_MAX), INT_MIN)));
     if (kv < 1) atomicAdd(&s_cnt[0], 1);
     else if (!valid_len(kv)) atomicAdd(&s_cnt[1], 1);
-    else {
-      const int c = static_cast<int>((kv + a.chunk_tokens - 1) / a.chunk_tokens);
-      chunks += c;
-      max_chunks = max(max_chunks, c);
-    }
+    const int t = tiles_of(b);
+    tiles += t;
+    max_tiles = max(max_tiles, t);
+    seqs += t > 0;
   }
-  const int total_chunks = block_sum(chunks, s_red);
-  const int most_chunks = block_max(max_chunks, s_red);
-  const int64_t groups = static_cast<int64_t>(total_chunks) * a.num_kv_heads;
-  // enough work groups for the device, at most kMaxParts partitions per sequence
-  const int64_t target = std::max(1, a.target_groups);
-  // A partition spans at most kIdCap table entries (they are staged in LDS):
-  // P <= (kIdCap - 1) * block_size covers a partition that starts mid-block.
-  const int64_t id_cap_chunks = std::max<int64_t>(
-      1, ((static_cast<int64_t>(kIdCap - 1)) << a.bs_log2) / a.chunk_tokens);
-  const int per_part = static_cast<int>(std::min<int64_t>(
-      id_cap_chunks, std::max<int64_t>(std::max<int64_t>(1, (groups + target - 1) / target),
-                                       (most_chunks + kMaxParts - 1) / kMaxParts)));
-  const int part_tokens = per_part * a.chunk_tokens;
+  const int64_t total_tiles = block_sum(tiles, s_red);
+  const int most_tiles = block_max(max_tiles, s_red);
+  const int64_t units = static_cast<int64_t>(block_sum(seqs, s_red)) * hkv;  // (sequence, kv head) pairs
 
-  // pass 2: work list
+  // ---- 2. piece bound L (tiles)
+  // Resident slots to fill: all a CU holds, or 2 per CU when there is at
+  // most one (sequence, kv head) unit per CU -- fewer, longer pieces per CU
+  // stream at a steadier rate per CU than three (measured on c2/c3-like
+  // batches), and the split-K merge has fewer partials.
+  const int per_cu = units <= a.cu_count ? std::min(2, std::max(1, a.groups_per_cu))
+                                         : std::max(1, a.groups_per_cu);
+  const int64_t target = static_cast<int64_t>(per_cu) * std::max(1, a.cu_count);
+  // hard: a piece spans at most kIdCap table entries (they are staged in LDS)
+  const int l_cap = static_cast<int>(std::max<int64_t>(
+      1, std::min<int64_t>(INT_MAX / 32, ((static_cast<int64_t>(kIdCap - 1)) << a.bs_log2) / kTile)));
+  // soft: at least one tile per wave per piece, at most kMaxParts pieces per sequence
+  const int l_min = std::min(l_cap, std::max(kWaves, (most_tiles + kMaxParts - 1) / kMaxParts));
+  const int l_top = std::min(l_cap, std::max(l_min, most_tiles));
+  const int l_fair = static_cast<int>(std::min<int64_t>(
+      l_cap, std::max<int64_t>(l_min, (total_tiles * hkv + target - 1) / target)));
+  auto groups_at = [&](int l) -> int64_t {  // uniform call: every thread
+    int n = 0;
+    for (int b = tid; b < a.num_seqs; b += kPlanThreads) n += (tiles_of(b) + l - 1) / l;
+    return static_cast<int64_t>(block_sum(n, s_red)) * hkv;
+  };
+  int lb;
+  if (groups_at(l_top) > target) {
+    lb = l_fair;  // more sequences than resident slots: several rounds anyway
+  } else {
+    int lo = l_min, hi = l_top;  // smallest l in [lo, hi] with groups_at(l) <= target
+    while (lo < hi) {
+      const int mid = lo + (hi - lo) / 2;
+      if (groups_at(mid) <= target) hi = mid;
+      else lo = mid + 1;
+    }
+    lb = lo > 2 * l_fair ? std::max(l_min, std::min(l_cap, 2 * l_fair)) : lo;
+  }
+  const int part_tokens = lb * kTile;
+
+  // ---- 3. items (sequence, piece) in sequence order
+  const int64_t num_groups = groups_at(lb);
+  const bool deal = num_groups <= kDealMax && num_groups <= target && a.cu_count > 0;
+  const int64_t used_groups = std::min<int64_t>(num_groups, a.work_cap);
   int64_t running = 0;
   for (int base = 0; base < a.num_seqs; base += kPlanThreads) {
     const int b = base + tid;
-    int np = 0;
-    if (b < a.num_seqs) {
-      const int64_t kv = static_cast<int64_t>(kvp[b]);
-      if (valid_len(kv)) {
-        np = static_cast<int>((kv + part_tokens - 1) / part_tokens);
-        atomicMax(&s_cnt[3], np);
-      }
-    }
+    const int np = b < a.num_seqs ? (tiles_of(b) + lb - 1) / lb : 0;
+    if (np > 0) atomicMax(&s_cnt[3], np);
     s_scan[tid] = np;
     __syncthreads();
     for (int off = 1; off < kPlanThreads; off <<= 1) {
@@ -782,41 +840,103 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
       __syncthreads();
     }
     const int64_t start = running + s_scan[tid] - np;
-    for (int p = 0; p < np; ++p) {
-      const int64_t idx = start + p;
-      if (idx < a.work_cap) {
-        reinterpret_cast<int4*>(a.work)[idx] = make_int4(b, p, static_cast<int>(kvp[b]), 0);
+    for (int j = 0; j < np; ++j) {
+      const int64_t item = start + j;
+      if (deal) {
+        s_item_b[item] = b;
+        s_item_j[item] = j;
+      } else {
+        const int2 r = piece_range(static_cast<int>(kvp[b]), np, j);
+        for (int h = 0; h < hkv; ++h) {
+          const int64_t slot = item * hkv + h;
+          if (slot < a.work_cap) {
+            int4* w = reinterpret_cast<int4*>(a.work + 8 * slot);
+            w[0] = make_int4(b, h, j, np);
+            w[1] = make_int4(r.x, r.y, 0, 0);
+          }
+        }
       }
     }
     running += s_scan[kPlanThreads - 1];
     __syncthreads();
   }
-  const int64_t num_items = std::min<int64_t>(running, a.work_cap);
-  __syncthreads();  // work items written above are read back below
 
-  // pass 3: each item's pool blocks, -1 past its last block (and for an
-  // entry outside the pool, which pass 4 reports)
+  // ---- 4. deal: sort groups by size (descending, then index) and place
+  // sorted position j in slot r * cu_count + c (round r = j / cu_count),
+  // forward or backward over c by round parity, ending forward so the last
+  // partial round fills slots [r * cu_count, r * cu_count + rem).
+  if (deal) {
+    const int g = tid;
+    uint32_t key = 0xFFFFFFFFu;
+    if (g < num_groups) {
+      const int item = g / hkv;
+      const int b = s_item_b[item];
+      const int np = (tiles_of(b) + lb - 1) / lb;
+      const int2 r = piece_range(static_cast<int>(kvp[b]), np, s_item_j[item]);
+      const uint32_t t = static_cast<uint32_t>(std::min((r.y - r.x + kTile - 1) / kTile, 0xFFFFF));
+      key = ((0xFFFFFu - t) << 11) | static_cast<uint32_t>(g);
+    }
+    s_key[tid] = key;
+    __syncthreads();
+    // bitonic sort of kDealMax keys, ascending
+    for (int k = 2; k <= kDealMax; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const int ixj = tid ^ j;
+        if (ixj > tid) {
+          const uint32_t x = s_key[tid], y = s_key[ixj];
+          const bool up = (tid & k) == 0;
+          if ((x > y) == up) {
+            s_key[tid] = y;
+            s_key[ixj] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (tid < num_groups) {
+      const int gs = static_cast<int>(s_key[tid] & 2047u);
+      const int item = gs / hkv;
+      const int h = gs - item * hkv;
+      const int b = s_item_b[item];
+      const int j = s_item_j[item];
+      const int np = (tiles_of(b) + lb - 1) / lb;
+      const int2 r = piece_range(static_cast<int>(kvp[b]), np, j);
+      const int cus = a.cu_count;
+      const int rounds = static_cast<int>((num_groups + cus - 1) / cus);
+      const int rd = tid / cus, c = tid - rd * cus;
+      const bool forward = ((rounds - 1 - rd) & 1) == 0;
+      const int64_t slot = static_cast<int64_t>(rd) * cus + (forward ? c : cus - 1 - c);
+      if (slot < a.work_cap) {
+        int4* w = reinterpret_cast<int4*>(a.work + 8 * slot);
+        w[0] = make_int4(b, h, j, np);
+        w[1] = make_int4(r.x, r.y, 0, 0);
+      }
+    }
+  }
+  __syncthreads();  // work entries written above are read back below
+
+  // ---- 5. each slot's pool blocks, -1 past its last block (and for an
+  // entry outside the pool, which the check below reports)
   const int per_item = ids_per_item(part_tokens, a.bs_log2);
-  const int64_t n_ids = num_items * per_item;
+  const int64_t n_ids = used_groups * per_item;
   if (n_ids <= a.ids_cap) {
     for (int64_t i = tid; i < n_ids; i += kPlanThreads) {
-      const int64_t it = i / per_item;
-      const int k = static_cast<int>(i - it * per_item);
-      const int4 w = reinterpret_cast<const int4*>(a.work)[it];
-      const int64_t tok_begin = static_cast<int64_t>(w.y) * part_tokens;
-      const int64_t tok_end = std::min<int64_t>(w.z, tok_begin + part_tokens);
-      const int64_t first = tok_begin >> a.bs_log2;
-      const int64_t last = (tok_end - 1) >> a.bs_log2;
+      const int64_t slot = i / per_item;
+      const int k = static_cast<int>(i - slot * per_item);
+      const int4 w0 = reinterpret_cast<const int4*>(a.work + 8 * slot)[0];
+      const int4 w1 = reinterpret_cast<const int4*>(a.work + 8 * slot)[1];
+      const int64_t first = static_cast<int64_t>(w1.x) >> a.bs_log2;
+      const int64_t last = (static_cast<int64_t>(w1.y) - 1) >> a.bs_log2;
       int32_t id = -1;
       if (first + k <= last) {
-        const int64_t blk = static_cast<int64_t>(btp[w.x * a.bt_stride + first + k]);
+        const int64_t blk = static_cast<int64_t>(btp[w0.x * a.bt_stride + first + k]);
         if (blk >= 0 && blk < a.num_blocks) id = static_cast<int32_t>(blk);
       }
       a.ids[i] = id;
     }
   }
 
-  // pass 4: every table entry a valid sequence reads must be a pool block
+  // every table entry a valid sequence reads must be a pool block
   const int64_t n = static_cast<int64_t>(a.num_seqs) * a.max_blocks;
   int bad = 0;
   for (int64_t i = tid; i < n; i += kPlanThreads) {
@@ -830,11 +950,11 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     }
   }
   if (bad) atomicAdd(&s_cnt[2], bad);
-  const int64_t nc = static_cast<int64_t>(a.num_seqs) * a.num_kv_heads;
+  const int64_t nc = static_cast<int64_t>(a.num_seqs) * hkv;
   for (int64_t i = tid; i < nc; i += kPlanThreads) a.counters[i] = 0;
   __syncthreads();
   if (tid == 0) {
-    a.status[MV_PLAN_NUM_ITEMS] = static_cast<int32_t>(std::min<int64_t>(running, INT_MAX));
+    a.status[MV_PLAN_NUM_ITEMS] = static_cast<int32_t>(std::min<int64_t>(num_groups, INT_MAX));
     a.status[MV_PLAN_BAD_KV_LEN] = s_cnt[0];
     a.status[MV_PLAN_INSUFFICIENT] = s_cnt[1];
     a.status[MV_PLAN_BAD_BLOCK] = s_cnt[2];
@@ -866,16 +986,14 @@ template <int DTYPE, int D> struct GroupsOf { static constexpr int value = Trait
 int chunk_tokens(int head_dim, int dtype) { return trait_value<ChunkOf>(head_dim, dtype); }
 
 template <int DTYPE, int D>
-int launch_decode(const DecodeArgs& a, int num_items, hipStream_t s) {
-  const int64_t grid = static_cast<int64_t>(num_items) * a.num_kv_heads;
-  if (grid > INT_MAX) return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: grid too large");
-  paged_decode_kernel<DTYPE, D><<<static_cast<unsigned>(grid), kWaves * 64, 0, s>>>(a);
+int launch_decode(const DecodeArgs& a, int num_groups, hipStream_t s) {
+  paged_decode_kernel<DTYPE, D><<<static_cast<unsigned>(num_groups), kWaves * 64, 0, s>>>(a);
   return check_launch("mv_paged_decode");
 }
 
 template <int DTYPE>
-int launch_decode_d(const DecodeArgs& a, int d, int num_items, hipStream_t s) {
-  return d == 64 ? launch_decode<DTYPE, 64>(a, num_items, s) : launch_decode<DTYPE, 128>(a, num_items, s);
+int launch_decode_d(const DecodeArgs& a, int d, int num_groups, hipStream_t s) {
+  return d == 64 ? launch_decode<DTYPE, 64>(a, num_groups, s) : launch_decode<DTYPE, 128>(a, num_groups, s);
 }
 
 }  // namespace
@@ -892,12 +1010,15 @@ extern "C" int mv_decode_groups_per_cu(int32_t head_dim, int32_t dtype) {
 }
 
 extern "C" int64_t mv_decode_block_ids_capacity(int32_t num_seqs, int32_t max_blocks,
-                                                int64_t work_capacity) {
-  if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0) return 0;
-  // With np_b = ceil(kv_b / P) items for sequence b and ids_per_item <=
-  // ceil(P / bs) + 4: np_b * ids_per_item <= (kv_b + P - 1) / bs + 5 np_b
-  // <= max_blocks + (kIdCap - 1) + 5 np_b, since P <= (kIdCap - 1) * bs.
-  return static_cast<int64_t>(num_seqs) * (max_blocks + mv::kIdCap) + 5 * work_capacity;
+                                                int32_t num_kv_heads, int64_t work_capacity) {
+  if (num_seqs < 0 || max_blocks < 0 || num_kv_heads < 0 || work_capacity < 0) return 0;
+  // Sequence b (T_b tiles) is cut into np_b = ceil(T_b / L) pieces of at
+  // most P = 16 L tokens, and ids_per_item <= ceil(P / bs) + 4. np_b * P <
+  // 16 T_b + P <= kv_b + 15 + P, so np_b * ids_per_item <= (kv_b + 15 + P)
+  // / bs + 5 np_b <= max_blocks + 15 + kIdCap + 5 np_b (P <= (kIdCap - 1)
+  // * bs); per kv head.
+  return static_cast<int64_t>(num_kv_heads) * num_seqs * (max_blocks + mv::kIdCap + 16) +
+         5 * work_capacity;
 }
 
 extern "C" size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
@@ -911,8 +1032,9 @@ extern "C" size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_
 extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                               int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs,
                               int32_t max_blocks, int32_t block_size, int64_t num_blocks,
-                              int32_t chunk_tokens, int32_t num_kv_heads, int32_t target_groups,
-                              int32_t* work_items, int64_t work_capacity, int32_t* block_ids,
+                              int32_t num_kv_heads, int32_t groups_per_cu,
+                              int32_t cu_count, int32_t* work_items, int64_t work_capacity,
+                              int32_t* block_ids,
                               int64_t block_ids_capacity, int32_t* counters, int32_t* status,
                               void* stream) {
   using namespace mv;
@@ -920,18 +1042,17 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
   if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0 || block_ids_capacity < 0 ||
       num_blocks < 0 || num_kv_heads <= 0)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: bad sizes");
-  if (chunk_tokens <= 0 || chunk_tokens % kTile)
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: chunk_tokens %d", chunk_tokens);
   if (!is_pow2(block_size))
     return fail(MV_ERR_UNSUPPORTED, "mv_decode_plan: block_size %d is not a power of 2", block_size);
   if (num_seqs > 0 && (!kv_len || !counters || (max_blocks > 0 && !block_table)))
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null pointer");
   if ((work_capacity > 0 && !work_items) || (block_ids_capacity > 0 && !block_ids))
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null work list");
-  if (block_ids_capacity < mv_decode_block_ids_capacity(num_seqs, max_blocks, work_capacity))
+  const int64_t ids_need =
+      mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, work_capacity);
+  if (block_ids_capacity < ids_need)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: block_ids capacity %lld < %lld",
-                static_cast<long long>(block_ids_capacity),
-                static_cast<long long>(mv_decode_block_ids_capacity(num_seqs, max_blocks, work_capacity)));
+                static_cast<long long>(block_ids_capacity), static_cast<long long>(ids_need));
   PlanArgs a;
   a.kv_len = kv_len;
   a.block_table = block_table;
@@ -939,9 +1060,9 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
   a.num_seqs = num_seqs;
   a.max_blocks = max_blocks;
   a.bs_log2 = ilog2_exact(block_size);
-  a.chunk_tokens = chunk_tokens;
   a.num_kv_heads = num_kv_heads;
-  a.target_groups = target_groups;
+  a.groups_per_cu = groups_per_cu;
+  a.cu_count = cu_count;
   a.num_blocks = num_blocks;
   a.work = work_items;
   a.work_cap = work_capacity;
@@ -963,7 +1084,7 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
 extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
                                const void* key_cache, const void* value_cache,
                                const int32_t* work_items, const int32_t* block_ids,
-                               int64_t block_ids_capacity, int32_t num_work_items,
+                               int64_t block_ids_capacity, int32_t num_work_groups,
                                int32_t partition_tokens, int32_t max_partitions, int32_t* counters,
                                void* out, int64_t out_stride_tok, int64_t out_stride_head,
                                float scale, int32_t num_seqs, int32_t num_q_heads,
@@ -985,27 +1106,26 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
   if (n_rep > kMaxGroup)
     return fail(MV_ERR_UNSUPPORTED, "mv_paged_decode: %d query heads per kv head (max %d)", n_rep,
                 kMaxGroup);
-  if (num_seqs < 0 || num_work_items < 0 || num_blocks <= 0 || max_partitions < 0 ||
+  if (num_seqs < 0 || num_work_groups < 0 || num_blocks <= 0 || max_partitions < 0 ||
       block_ids_capacity < 0)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: bad sizes");
-  const int chunk = chunk_tokens(head_dim, dtype);
-  if (partition_tokens <= 0 || partition_tokens % chunk)
+  if (partition_tokens <= 0 || partition_tokens % kTile)
     return fail(MV_ERR_INVALID_ARGUMENT,
                 "mv_paged_decode: partition_tokens %d is not a positive multiple of %d",
-                partition_tokens, chunk);
+                partition_tokens, kTile);
   if ((static_cast<int64_t>(partition_tokens) + block_size - 1) / block_size + 1 > kIdCap)
     return fail(MV_ERR_INVALID_ARGUMENT,
                 "mv_paged_decode: partition_tokens %d spans more than %d blocks of %d tokens",
                 partition_tokens, kIdCap - 1, block_size);
-  if (num_seqs == 0 || num_work_items == 0) return MV_OK;
+  if (num_seqs == 0 || num_work_groups == 0) return MV_OK;
   if (!query || !key_cache || !value_cache || !work_items || !block_ids || !out)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: null pointer");
   const int bs_log2 = ilog2_exact(block_size);
   const int per_item = ids_per_item(partition_tokens, bs_log2);
-  if (static_cast<int64_t>(num_work_items) * per_item > block_ids_capacity)
+  if (static_cast<int64_t>(num_work_groups) * per_item > block_ids_capacity)
     return fail(MV_ERR_INVALID_ARGUMENT,
-                "mv_paged_decode: %d work items x %d block ids exceed capacity %lld",
-                num_work_items, per_item, static_cast<long long>(block_ids_capacity));
+                "mv_paged_decode: %d work groups x %d block ids exceed capacity %lld",
+                num_work_groups, per_item, static_cast<long long>(block_ids_capacity));
   // 16-byte copies of q rows, cache rows and block-id lists.
   if ((reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key_cache) |
        reinterpret_cast<uintptr_t>(value_cache) | reinterpret_cast<uintptr_t>(block_ids) |
@@ -1013,7 +1133,8 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
       (q_stride_tok * eb) % 16 || (q_stride_head * eb) % 16)
     return fail(MV_ERR_INVALID_ARGUMENT,
                 "mv_paged_decode: query/cache rows or plan arrays not 16-byte aligned");
-  if (max_partitions > 0 && num_work_items > max_partitions * static_cast<int64_t>(num_seqs))
+  if (max_partitions > 0 &&
+      num_work_groups > static_cast<int64_t>(max_partitions) * num_seqs * num_kv_heads)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode: work list larger than the plan allows");
 
   DecodeArgs a;
@@ -1035,7 +1156,6 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
   a.n_rep = n_rep;
   a.bs_log2 = bs_log2;
   a.max_parts = max_partitions;
-  a.part_tokens = partition_tokens;
   a.num_blocks = num_blocks;
   a.ws_o = nullptr;
   a.ws_ml = nullptr;
@@ -1054,8 +1174,8 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, num_work_items, s);
-    case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, num_work_items, s);
-    default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, num_work_items, s);
+    case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, num_work_groups, s);
+    case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, num_work_groups, s);
+    default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, num_work_groups, s);
   }
 }

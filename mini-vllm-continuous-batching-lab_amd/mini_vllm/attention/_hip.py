@@ -62,16 +62,16 @@ SIGNATURES = {
     "mv_decode_plan": (ctypes.c_int, [
         _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride
         _I32, _I32, _I32, _I64,    # num_seqs, max_blocks, block_size, num_blocks
-        _I32, _I32, _I32,          # chunk_tokens, num_kv_heads, target_groups
+        _I32, _I32, _I32,          # num_kv_heads, groups_per_cu, cu_count
         _P, _I64, _P, _I64,        # work_items, capacity, block_ids, capacity
         _P, _P, _P,                # counters, status, stream
     ]),
-    "mv_decode_block_ids_capacity": (_I64, [_I32, _I32, _I64]),
+    "mv_decode_block_ids_capacity": (_I64, [_I32, _I32, _I32, _I64]),
     "mv_paged_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
     "mv_paged_decode": (ctypes.c_int, [
         _P, _I64, _I64,            # query, strides
         _P, _P,                    # key_cache, value_cache
-        _P, _P, _I64, _I32,        # work_items, block_ids, block_ids_capacity, num_work_items
+        _P, _P, _I64, _I32,        # work_items, block_ids, block_ids_capacity, num_work_groups
         _I32, _I32, _P,            # partition_tokens, max_partitions, counters
         _P, _I64, _I64,            # out, strides
         _F, _I32, _I32, _I32, _I32,  # scale, num_seqs, num_q_heads, num_kv_heads, head_dim

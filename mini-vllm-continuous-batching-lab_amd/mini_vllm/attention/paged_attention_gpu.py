@@ -219,28 +219,29 @@ def hip_cache_write(
 class DecodePlan:
     """Device-side per-step decode metadata produced by ``mv_decode_plan``."""
 
-    work: torch.Tensor         # [4 * capacity] int32 (seq, partition, kv_len, 0)
-    block_ids: torch.Tensor    # [capacity] int32: ids_per_item pool blocks per work item
+    work: torch.Tensor         # [8 * capacity] int32: one entry per work group
+    block_ids: torch.Tensor    # int32: ids_per_item pool blocks per work group
     counters: torch.Tensor     # [num_seqs * num_kv_heads] int32, zero between calls
-    num_items: int
+    num_groups: int
     max_parts: int
     partition_tokens: int
 
 
-# The partition size aims for as many work groups as the device holds at
-# once (work groups per CU from the library, times the CU count), so the
-# whole grid runs in one dispatch round. MVATTN_GROUPS_PER_CU overrides the
-# per-CU figure.
+# The plan aims for as many work groups as the device holds at once (work
+# groups per CU from the library, times the CU count), so the whole grid
+# runs in one dispatch round and can be balanced over the CUs.
+# MVATTN_GROUPS_PER_CU overrides the per-CU figure.
 _CU_COUNT: dict = {}
 
 
-def _target_groups(device: torch.device, head_dim: int, dtype: torch.dtype) -> int:
+def _groups_per_cu(device: torch.device, head_dim: int, dtype: torch.dtype) -> Tuple[int, int]:
+    """(work groups per CU, CU count) for the decode plan."""
     if device not in _CU_COUNT:
         _CU_COUNT[device] = torch.cuda.get_device_properties(device).multi_processor_count
     per_cu = os.environ.get("MVATTN_GROUPS_PER_CU")
     if per_cu is None:
         per_cu = _hip.load().mv_decode_groups_per_cu(head_dim, _hip.MV_DTYPE[dtype])
-    return max(1, int(per_cu)) * _CU_COUNT[device]
+    return max(1, int(per_cu)), _CU_COUNT[device]
 
 
 def plan_decode(
@@ -265,8 +266,8 @@ def plan_decode(
     unmodified tensors (the other layers of the step) reuse the plan.
     """
     lib = _hip.load()
-    chunk = lib.mv_decode_chunk_tokens(head_dim, _hip.MV_DTYPE[dtype])
-    extra = (block_size, num_blocks, device, chunk, num_kv_heads)
+    split = _groups_per_cu(device, head_dim, dtype)
+    extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads, split)
     cached = _cache_get("plan", (block_table, kv_len_after), extra)
     if cached is not None:
         return cached
@@ -288,9 +289,9 @@ def plan_decode(
 
     num_seqs = kv.shape[0]
     max_blocks = bt.shape[1] if bt.dim() == 2 else 0
-    cap = num_seqs * max(1, math.ceil(max_blocks * block_size / chunk))
-    work = torch.empty(4 * max(cap, 1), dtype=torch.int32, device=device)
-    ids_cap = lib.mv_decode_block_ids_capacity(num_seqs, max_blocks, cap)
+    cap = num_seqs * num_kv_heads * max(1, math.ceil(max_blocks * block_size / 16))
+    work = torch.empty(8 * max(cap, 1), dtype=torch.int32, device=device)
+    ids_cap = lib.mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, cap)
     block_ids = torch.empty(max(ids_cap, 4), dtype=torch.int32, device=device)
     counters = torch.empty(max(num_seqs * num_kv_heads, 1), dtype=torch.int32, device=device)
     status = torch.empty(_hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
@@ -298,7 +299,7 @@ def plan_decode(
         lib.mv_decode_plan(
             _ptr(kv), int(kv.dtype == torch.int64), _ptr(bt), int(bt.dtype == torch.int64),
             bt.stride(0) if bt.dim() == 2 else 0, num_seqs, max_blocks, block_size,
-            num_blocks, chunk, num_kv_heads, _target_groups(device, head_dim, dtype),
+            num_blocks, num_kv_heads, *split,
             _ptr(work), cap, _ptr(block_ids), block_ids.numel(),
             _ptr(counters), _ptr(status), _stream(device),
         ),
@@ -320,10 +321,10 @@ def plan_decode(
             f"block_table has {st[_hip.MV_PLAN_BAD_BLOCK]} entr(ies) within kv_len_after "
             f"that are not pool blocks [0, {num_blocks})"
         )
-    num_items = st[_hip.MV_PLAN_NUM_ITEMS]
-    if num_items > cap or st[_hip.MV_PLAN_IDS_PER_ITEM] < 0:
-        raise RuntimeError(f"decode plan: {num_items} work items exceed the plan capacity {cap}")
-    plan = DecodePlan(work, block_ids, counters, num_items, st[_hip.MV_PLAN_MAX_PARTS],
+    num_groups = st[_hip.MV_PLAN_NUM_ITEMS]
+    if num_groups > cap or st[_hip.MV_PLAN_IDS_PER_ITEM] < 0:
+        raise RuntimeError(f"decode plan: {num_groups} work groups exceed the plan capacity {cap}")
+    plan = DecodePlan(work, block_ids, counters, num_groups, st[_hip.MV_PLAN_MAX_PARTS],
                       st[_hip.MV_PLAN_PARTITION_TOKENS])
     _cache_put("plan", (block_table, kv_len_after), extra, plan)
     return plan
@@ -376,7 +377,7 @@ def hip_decode_attention(
     plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
                        query.dtype, num_kv_heads)
     output = torch.empty(query.shape, dtype=query.dtype, device=device)
-    if total_decode == 0 or plan.num_items == 0:
+    if total_decode == 0 or plan.num_groups == 0:
         return output
     if query.stride(2) != 1 or (query.stride(1) * query.element_size()) % 16 or (
         query.stride(0) * query.element_size()
@@ -389,7 +390,7 @@ def hip_decode_attention(
         lib.mv_paged_decode(
             _ptr(query), query.stride(0), query.stride(1),
             _ptr(key_cache), _ptr(value_cache),
-            _ptr(plan.work), _ptr(plan.block_ids), plan.block_ids.numel(), plan.num_items,
+            _ptr(plan.work), _ptr(plan.block_ids), plan.block_ids.numel(), plan.num_groups,
             plan.partition_tokens, plan.max_parts, _ptr(plan.counters),
             _ptr(output), output.stride(0), output.stride(1),
             float(head_dim ** -0.5), total_decode, num_q_heads, num_kv_heads, head_dim,

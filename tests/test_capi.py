@@ -76,7 +76,7 @@ def test_workspace_bytes(lib):
 
 DECODE_PARAMS = [
     "query", "q_stride_tok", "q_stride_head", "key_cache", "value_cache", "work_items",
-    "block_ids", "block_ids_capacity", "num_work_items", "partition_tokens",
+    "block_ids", "block_ids_capacity", "num_work_groups", "partition_tokens",
     "max_partitions", "counters", "out", "out_stride_tok", "out_stride_head", "scale",
     "num_seqs", "num_q_heads", "num_kv_heads", "head_dim", "block_size", "num_blocks", "dtype",
     "workspace", "workspace_bytes", "stream",
@@ -86,7 +86,7 @@ DECODE_PARAMS = [
 def _decode_args(**kw):
     base = dict(query=None, q_stride_tok=0, q_stride_head=0, key_cache=None, value_cache=None,
                 work_items=None, block_ids=None, block_ids_capacity=1024,
-                num_work_items=1, partition_tokens=64, max_partitions=1, counters=None, out=None,
+                num_work_groups=1, partition_tokens=64, max_partitions=1, counters=None, out=None,
                 out_stride_tok=0, out_stride_head=0, scale=0.125, num_seqs=1, num_q_heads=14,
                 num_kv_heads=2, head_dim=64, block_size=16, num_blocks=10, dtype=2,
                 workspace=None, workspace_bytes=0, stream=None)
@@ -95,15 +95,15 @@ def _decode_args(**kw):
 
 
 def test_block_ids_capacity(lib):
-    # num_seqs * (max_blocks + 512) + 5 * work_capacity (an upper bound for any partition size)
-    assert lib.mv_decode_block_ids_capacity(64, 128, 2048) == 64 * (128 + 512) + 5 * 2048
-    assert lib.mv_decode_block_ids_capacity(0, 0, 0) == 0
-    assert lib.mv_decode_block_ids_capacity(-1, 4, 4) == 0
+    # kv_heads * num_seqs * (max_blocks + 512 + 16) + 5 * work_capacity (a bound for any piece size)
+    assert lib.mv_decode_block_ids_capacity(64, 128, 2, 4096) == 2 * 64 * (128 + 512 + 16) + 5 * 4096
+    assert lib.mv_decode_block_ids_capacity(0, 0, 2, 0) == 0
+    assert lib.mv_decode_block_ids_capacity(-1, 4, 2, 4) == 0
 
 
 def test_plan_rejects_small_block_ids_buffer_on_host(lib):
     # dummy addresses: the call fails on the capacity before anything is launched
-    rc = lib.mv_decode_plan(16, 1, 16, 1, 8, 4, 8, 16, 100, 64, 2, 512,
+    rc = lib.mv_decode_plan(16, 1, 16, 1, 8, 4, 8, 16, 100, 2, 3, 256,
                             16, 8, 16, 10, 16, 16, None)
     assert rc == _hip.MV_ERR_INVALID_ARGUMENT
     assert b"block_ids capacity" in lib.mv_last_error()
@@ -127,14 +127,14 @@ def test_decode_rejects_unsupported_shapes_on_host(lib):
         _hip.MV_ERR_INVALID_ARGUMENT
     assert b"spans more than 511 blocks" in lib.mv_last_error()
     assert lib.mv_paged_decode(*_decode_args(block_size=1, partition_tokens=448,
-                                             num_work_items=0)) == _hip.MV_OK
+                                             num_work_groups=0)) == _hip.MV_OK
     # the block-id lists of the work items must fit the given capacity
     assert lib.mv_paged_decode(*_decode_args(query=16, key_cache=16, value_cache=16, work_items=16,
-                                             block_ids=16, out=16, num_work_items=300,
+                                             block_ids=16, out=16, num_work_groups=300,
                                              block_ids_capacity=1000)) == _hip.MV_ERR_INVALID_ARGUMENT
     assert b"exceed capacity" in lib.mv_last_error()
     # nothing to do is not an error
-    assert lib.mv_paged_decode(*_decode_args(num_work_items=0)) == _hip.MV_OK
+    assert lib.mv_paged_decode(*_decode_args(num_work_groups=0)) == _hip.MV_OK
     # work to do but null pointers
     assert lib.mv_paged_decode(*_decode_args()) == _hip.MV_ERR_INVALID_ARGUMENT
 
