@@ -22,6 +22,20 @@ template <> struct Chunk<8> { using type = uint2; };
 template <> struct Chunk<4> { using type = uint32_t; };
 template <> struct Chunk<2> { using type = uint16_t; };
 
+// Uses a loaded chunk in an empty asm (with a memory clobber, so loads
+// issued before it stay before it): the compiler can then no longer sink
+// the load below the slot check that guards the store.
+__device__ __forceinline__ void keep_loaded(const uint4& v) {
+  asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w) : "memory");
+}
+__device__ __forceinline__ void keep_loaded(const uint2& v) {
+  asm volatile("" ::"v"(v.x), "v"(v.y) : "memory");
+}
+__device__ __forceinline__ void keep_loaded(uint32_t v) { asm volatile("" ::"v"(v) : "memory"); }
+__device__ __forceinline__ void keep_loaded(uint16_t v) {
+  asm volatile("" ::"v"(static_cast<uint32_t>(v)) : "memory");
+}
+
 struct WriteArgs {
   const char* key;
   const char* value;
@@ -35,34 +49,39 @@ struct WriteArgs {
   int32_t num_kv_heads;
   int32_t row_bytes;  // head_dim * element bytes
   int32_t block_size;
+  int32_t bs_log2;    // log2(block_size) when it is a power of two, else -1
 };
 
 template <int VEC>
 __global__ __launch_bounds__(256) void kv_cache_write_kernel(WriteArgs a) {
   using C = typename Chunk<VEC>::type;
+  // 32-bit index math (the host guarantees 2 * rows * chunks < 2^31)
   const int chunks_per_row = a.row_bytes / VEC;
-  const int64_t rows = a.num_tokens * a.num_kv_heads;
-  const int64_t per_tensor = rows * chunks_per_row;
-  const int64_t total = 2 * per_tensor;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
+  const int rows = static_cast<int>(a.num_tokens) * a.num_kv_heads;
+  const int per_tensor = rows * chunks_per_row;
+  const int total = 2 * per_tensor;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
     const bool is_v = i >= per_tensor;
-    const int64_t r = is_v ? i - per_tensor : i;
-    const int64_t row = r / chunks_per_row;
-    const int chunk = static_cast<int>(r - row * chunks_per_row);
-    const int64_t t = row / a.num_kv_heads;
-    const int h = static_cast<int>(row - t * a.num_kv_heads);
+    const int r = is_v ? i - per_tensor : i;
+    const int row = r / chunks_per_row;
+    const int chunk = r - row * chunks_per_row;
+    const int t = row / a.num_kv_heads;
+    const int h = row - t * a.num_kv_heads;
+    // The source chunk and the slot are loaded together: the source address
+    // does not depend on the slot, so the copy costs one memory round trip.
+    const char* src = is_v ? a.value + t * a.value_stride_tok + h * a.value_stride_head
+                           : a.key + t * a.key_stride_tok + h * a.key_stride_head;
+    const C v = reinterpret_cast<const C*>(src)[chunk];
     const int64_t slot = a.slots[t];
+    keep_loaded(v);
     // -1 skips (prefix-cache hit); anything else outside the pool is
     // reported by the slot check and never written.
     if (slot < 0 || slot >= a.total_slots) continue;
-    const int64_t blk = slot / a.block_size;
+    const int64_t blk = a.bs_log2 >= 0 ? slot >> a.bs_log2 : slot / a.block_size;
     const int64_t off = slot - blk * a.block_size;
-    const char* src = is_v ? a.value + t * a.value_stride_tok + h * a.value_stride_head
-                           : a.key + t * a.key_stride_tok + h * a.key_stride_head;
     char* dst = (is_v ? a.value_cache : a.key_cache) +
                 ((blk * a.num_kv_heads + h) * a.block_size + off) * a.row_bytes;
-    reinterpret_cast<C*>(dst)[chunk] = reinterpret_cast<const C*>(src)[chunk];
+    reinterpret_cast<C*>(dst)[chunk] = v;
   }
 }
 
@@ -153,6 +172,7 @@ extern "C" int mv_kv_cache_write(const void* key, int64_t key_stride_tok, int64_
   a.num_kv_heads = num_kv_heads;
   a.row_bytes = head_dim * eb;
   a.block_size = block_size;
+  a.bs_log2 = is_pow2(block_size) ? ilog2_exact(block_size) : -1;
 
   const int vec = pick_vec(a.row_bytes,
                            {(int64_t)(uintptr_t)key, (int64_t)(uintptr_t)value,
@@ -163,6 +183,9 @@ extern "C" int mv_kv_cache_write(const void* key, int64_t key_stride_tok, int64_
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_kv_cache_write: addresses not 2-byte aligned");
 
   const int64_t work = 2 * num_tokens * num_kv_heads * (a.row_bytes / vec);
+  if (work >= INT_MAX)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_kv_cache_write: %lld tokens x %d heads is too many",
+                (long long)num_tokens, num_kv_heads);
   const int threads = 256;
   const int64_t blocks = std::min<int64_t>((work + threads - 1) / threads, 65536);
   hipStream_t s = static_cast<hipStream_t>(stream);
