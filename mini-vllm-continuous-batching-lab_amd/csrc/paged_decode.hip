@@ -96,8 +96,8 @@ struct Traits {
   // LDS is one union, laid out per phase:
   //   tile loop: [kWaves][kStages][K, V][kTileBytes], then the partition's
   //              block ids (int32, kIdCap), then the group's 16 Q rows;
-  //   merges:    [0, kWaveOBytes) the waves' o, then their (max, sum)
-  //              and the last-group flag.
+  //   epilogue:  each wave's o rows and (max, sum) in its own tile buffers;
+  //              the last-group flag where the block ids were.
   static constexpr int kIdsOffset = kWaves * kWaveLds;
   static constexpr int kQOffset = kIdsOffset + kIdCap * 4;  // Q rows of the group (16 x D)
   static constexpr int kQLoads = kTile * kRowBytes / 1024;  // 1 KiB copies of the Q rows
@@ -105,11 +105,10 @@ struct Traits {
   // Wave merge o rows, padded by 4 floats: the accumulator rows 4g+e that
   // one store instruction writes then start 16 banks apart.
   static constexpr int kORowStride = D + 4;
-  static constexpr int kWaveOBytes = kWaves * kMaxGroup * kORowStride * 4;
-  static constexpr int kStatsOffset = kWaveOBytes;                    // s_max, s_sum
-  static constexpr int kFlagOffset = kStatsOffset + 2 * kWaves * kMaxGroup * 4;
-  static constexpr int kMergeEnd = kFlagOffset + 16;
-  static constexpr int kLdsBytes = kTilesEnd > kMergeEnd ? kTilesEnd : kMergeEnd;
+  static constexpr int kWaveEpilogueBytes = (kMaxGroup * kORowStride + 2 * kMaxGroup) * 4;
+  static constexpr int kFlagOffset = kIdsOffset;
+  static constexpr int kLdsBytes = kTilesEnd;
+  static_assert(kWaveEpilogueBytes <= kWaveLds, "a wave's epilogue fits its tile buffers");
   static_assert(kStages >= 2 && kStages <= 4, "tile stages");
   // Work groups one CU holds (160 KiB of LDS on gfx950), and the matching
   // register budget: waves per SIMD = groups * kWaves / 4 (at least 1).
@@ -301,8 +300,6 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   constexpr int QP = Tr::kLanePieces;
 
   __shared__ __attribute__((aligned(16))) char s_lds[Tr::kLdsBytes];
-  float (*s_max)[kMaxGroup] = reinterpret_cast<float (*)[kMaxGroup]>(s_lds + Tr::kStatsOffset);
-  float (*s_sum)[kMaxGroup] = s_max + kWaves;
   int& s_last = *reinterpret_cast<int*>(s_lds + Tr::kFlagOffset);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -527,20 +524,25 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   // From here on thread (r, q) = (tid / 16, tid % 16) owns the dim pairs
   // (32j + 2q, 32j + 2q + 1), j < D/32, of query head r of the group: each
   // load or store instruction then covers 128 contiguous bytes per head.
+  // Each wave parks its o rows and (max, sum) in its own tile buffers, free
+  // once its loop is done (its copies and LDS reads have all completed), so
+  // one barrier suffices and no wave waits for the others before writing.
   constexpr int NPAIR = Tr::kPairsPerThread;
-  __syncthreads();  // every wave is done with its tiles (s_lds is reused)
   constexpr int OS = Tr::kORowStride;
-  float* s_o = reinterpret_cast<float*>(s_lds);  // [kWaves][kMaxGroup][OS]
-  if (g == 0) {
-    s_max[wave][t] = m_run;
-    s_sum[wave][t] = l_run;
-  }
+  auto wave_o = [&](int w) { return reinterpret_cast<float*>(s_lds + w * Tr::kWaveLds); };  // [kMaxGroup][OS]
+  auto wave_ms = [&](int w) { return wave_o(w) + kMaxGroup * OS; };  // max [kMaxGroup], sum [kMaxGroup]
+  {
+    float* my_o = wave_o(wave);
+    if (g == 0) {
+      wave_ms(wave)[t] = m_run;
+      wave_ms(wave)[kMaxGroup + t] = l_run;
+    }
+    // all 16 accumulator rows (= query heads of the group; rows >= n_rep
+    // are never read): unconditional, conflict-free stores
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c) {
+    for (int c = 0; c < D / 16; ++c) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = 4 * g + e;  // accumulator row = query head of the group
-      if (row < a.n_rep) s_o[(wave * kMaxGroup + row) * OS + 16 * c + t] = o[c][e];
+      for (int e = 0; e < 4; ++e) my_o[(4 * g + e) * OS + 16 * c + t] = o[c][e];
     }
   }
   __syncthreads();
@@ -551,7 +553,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   for (int r = threadIdx.x >> 4; r < a.n_rep; r += kWaves * 4) {
     float mx = kNegInf;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_max[w][r]);
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wave_ms(w)[r]);
     float sum = 0.f;
     float2 v[NPAIR];
 #pragma unroll
@@ -560,10 +562,10 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     // partition has max -inf, sum 0 and o 0, and gets weight 0.
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float mw = s_max[w][r];
+      const float mw = wave_ms(w)[r];
       const float f = mw == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
-      sum += s_sum[w][r] * f;
-      const float* src = s_o + (w * kMaxGroup + r) * OS + 2 * q;
+      sum += wave_ms(w)[kMaxGroup + r] * f;
+      const float* src = wave_o(w) + r * OS + 2 * q;
 #pragma unroll
       for (int j = 0; j < NPAIR; ++j) {
         const float2 x = *reinterpret_cast<const float2*>(src + 32 * j);
