@@ -1,0 +1,141 @@
+"""The per-step decode plan (mv_decode_plan) on the GPU.
+
+* Structure, read back from the device: every (sequence, kv head) unit is
+  cut into pieces that tile [0, kv_len) exactly once, in order; the launch
+  slots form a complete list; each slot's block ids are its table entries
+  (-1 past its last block); pieces respect the reported bounds.
+* Parity on the plan's three paths: groups dealt over the CUs (one
+  dispatch round), more groups than can be dealt (natural order), and a
+  skewed batch whose one-round split would need oversized pieces (fair
+  pieces in several rounds).
+"""
+
+import pytest
+import torch
+
+from benchmarks.paged_decode_workloads import WorkloadSpec, make_case
+from gpu_util import DEV, TOL, oracle_step, say, to_device
+from mini_vllm.attention.paged_attention_gpu import hip_cache_write, hip_decode_attention, plan_decode
+
+pytestmark = pytest.mark.gpu
+
+
+def _cus():
+    return torch.cuda.get_device_properties(DEV).multi_processor_count
+
+
+def _check_plan(case):
+    spec = case.layout.spec
+    bt = case.block_table.to(DEV)
+    kv = case.kv_len.to(DEV)
+    plan = plan_decode(bt, kv, spec.block_size, case.layout.num_blocks, DEV, spec.head_dim,
+                       spec.dtype, spec.num_kv_heads)
+    torch.cuda.synchronize()
+    g = plan.num_groups
+    work = plan.work[: 8 * g].view(g, 8).cpu().tolist()
+    bs = spec.block_size
+    kv_l = case.kv_len.tolist()
+    table = case.block_table.tolist()
+    pieces = {}
+    for slot, (b, h, j, np_, t0, t1, z0, z1) in enumerate(work):
+        assert 0 <= b < len(kv_l) and 0 <= h < spec.num_kv_heads and 0 <= j < np_, (slot, b, h, j, np_)
+        assert (z0, z1) == (0, 0)
+        assert 0 <= t0 < t1 <= kv_l[b], (slot, t0, t1, kv_l[b])
+        assert t0 % 16 == 0
+        assert t1 - t0 <= plan.partition_tokens
+        assert np_ <= plan.max_parts
+        pieces.setdefault((b, h), {})[j] = (np_, t0, t1, slot)
+    for b, n in enumerate(kv_l):
+        for h in range(spec.num_kv_heads):
+            ps = pieces[(b, h)]
+            np_ = next(iter(ps.values()))[0]
+            assert sorted(ps) == list(range(np_)), (b, h, sorted(ps))
+            pos = 0
+            for j in range(np_):
+                assert ps[j][0] == np_
+                assert ps[j][1] == pos, (b, h, j, ps[j], pos)
+                pos = ps[j][2]
+            assert pos == n
+    assert len(work) == sum(len(v) for v in pieces.values())
+    # block ids per slot
+    ids = plan.block_ids.cpu()
+    stride = None
+    for slot, (b, h, j, np_, t0, t1, _, _) in enumerate(work):
+        first, last = t0 // bs, (t1 - 1) // bs
+        if stride is None:
+            # the stride is at least the span of the widest piece, a multiple of 4
+            stride = ((plan.partition_tokens + bs - 1) // bs + 1 + 3) // 4 * 4
+            assert stride * g <= ids.numel()
+        row = ids[slot * stride:(slot + 1) * stride].tolist()
+        want = [table[b][first + k] if first + k <= last else -1 for k in range(stride)]
+        assert row == want, (slot, row[:8], want[:8])
+    return plan
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+def test_plan_structure_on_workloads(name):
+    say("plan structure", name)
+    case = make_case(name, seed=0)
+    plan = _check_plan(case)
+    spec = case.layout.spec
+    units = len(case.layout.kv_lens) * spec.num_kv_heads
+    assert plan.num_groups >= units
+
+
+def _run_and_check(spec, seed=0):
+    case = make_case(spec, seed=seed, nan_fill=True)
+    plan = _check_plan(case)
+    d = to_device(case)
+    bs = spec.block_size
+    hip_cache_write(d.new_key, d.new_value, d.key_cache, d.value_cache, d.slot_mapping, bs)
+    out = hip_decode_attention(d.query, d.key_cache, d.value_cache, d.block_table, d.kv_len, bs)
+    torch.cuda.synchronize()
+    ref, _, _ = oracle_step(case)
+    out = out.float().cpu()
+    assert not torch.isnan(out).any()
+    err = (out - ref).abs().max().item()
+    assert err <= TOL[spec.dtype], err
+    return plan, err
+
+
+def test_many_units_are_not_dealt():
+    """700 sequences x 2 kv heads: more work groups than one sort holds."""
+    lens = [1 + (7 * i) % 40 for i in range(700)]
+    spec = WorkloadSpec("many", 14, 2, 64, 16, torch.bfloat16, len(lens), ("fixed", lens))
+    say("plan: many units", len(lens))
+    plan, err = _run_and_check(spec)
+    assert plan.num_groups > 1024
+    say(f"  groups {plan.num_groups} max abs err {err:.3g}")
+
+
+def test_skewed_batch_uses_fair_pieces():
+    """382 one-tile sequences and one of 16000 tokens (766 units of 768 slots
+    at 3 per CU): fitting one dispatch round would leave the long sequence
+    two pieces of 500 tiles, far over twice the fair share, so the plan cuts
+    fair pieces and runs more groups than resident slots."""
+    from mini_vllm.attention import _hip
+
+    lens = [16] * 382 + [16000]
+    spec = WorkloadSpec("skew", 14, 2, 64, 16, torch.bfloat16, len(lens), ("fixed", lens))
+    say("plan: skewed batch")
+    plan, err = _run_and_check(spec)
+    per_cu = _hip.load().mv_decode_groups_per_cu(64, _hip.MV_DTYPE[torch.bfloat16])
+    assert plan.num_groups > per_cu * _cus()
+    say(f"  groups {plan.num_groups} P {plan.partition_tokens} max abs err {err:.3g}")
+
+
+def test_dealt_plan_fills_slots_round_robin():
+    """A batch that fits one round is dealt: sizes never increase within
+    the first round of slots (biggest pieces first)."""
+    case = make_case("c2", seed=1)
+    plan = _check_plan(case)
+    cus = _cus()
+    g = plan.num_groups
+    assert g <= 2 * cus
+    work = plan.work[: 8 * g].view(g, 8).cpu()
+    sizes = ((work[:, 5] - work[:, 4] + 15) // 16).tolist()  # the plan sorts by 16-token tiles
+    first_round = sorted(sizes[:min(g, cus)], reverse=True)
+    second = sizes[cus:]
+    # every piece of the first round is at least as big as every later one
+    if second:
+        assert min(first_round) >= max(second)
