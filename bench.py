@@ -110,6 +110,20 @@ def wall_loop(fn, n):
     return (time.perf_counter() - t0) * 1e6 / n
 
 
+def plan_step_us(bt, kv, bs, num_blocks, dev, spec, plan_decode, reps=20):
+    """Host time of one step's decode plan in steady state (median): the
+    plan kernel plus the read-back of its status. Fresh copies of the
+    metadata defeat the per-step plan cache, as a new engine step would."""
+    times = []
+    for _ in range(reps):
+        b2, k2 = bt.clone(), kv.clone()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        plan_decode(b2, k2, bs, num_blocks, dev, spec.head_dim, spec.dtype, spec.num_kv_heads)
+        times.append((time.perf_counter() - t0) * 1e6)
+    return statistics.median(times)
+
+
 def cpu_baseline(spec, layout, layer, budget_s=12.0):
     """The oracle's CPU path (reference loops, fp32) on a bounded sample:
     whole layer calls (write + decode of the full batch) repeated until
@@ -227,10 +241,9 @@ def main(argv=None) -> int:
     stream = torch.cuda.current_stream(dev)
 
     # per-step validation/planning (once per engine step, shared by all layers)
-    t0 = time.perf_counter()
     plan = plan_decode(bt, kv, bs, layout.num_blocks, dev, spec.head_dim, spec.dtype,
                        spec.num_kv_heads)
-    plan_us = (time.perf_counter() - t0) * 1e6
+    plan_us = plan_step_us(bt, kv, bs, layout.num_blocks, dev, spec, plan_decode)
 
     def layer_call(i):
         L = layers[i % n_layers]

@@ -690,28 +690,98 @@ struct PlanArgs {
 };
 
 constexpr int kPlanThreads = 1024;
-constexpr int kDealMax = 1024;  // work groups sorted and dealt to CUs in shared memory
+constexpr int kPlanWaves = kPlanThreads / 64;
+constexpr int kDealMax = 1024;       // work groups sorted and dealt to CUs in shared memory
+constexpr int kPlanSeqCache = 4096;  // kv lengths held in shared memory
+constexpr int kWaveSearchSeqs = 256; // one wave runs the piece-bound search up to this batch
+constexpr int kIdsThreads = 256;     // block-id kernel: threads per work group
+constexpr int kIdsQuads = 4;         // block-id kernel: 4-id quads per thread per pass
+constexpr int kIdsPerPass = kIdsThreads * kIdsQuads * 4;
+static_assert(kPlanThreads == kDealMax, "the sort holds one key per thread");
 
-__device__ int block_sum(int v, int* scratch) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-  __syncthreads();
-  int total = 0;
-  for (int w = 0; w < kPlanThreads / 64; ++w) total += scratch[w];
-  __syncthreads();  // scratch is reused by the next call
-  return total;
+// Value-returning min / max: std::min / std::max return a reference, and
+// a reference to one of two temporaries makes the compiler keep both on
+// the stack to select an address.
+template <typename T> __device__ inline T vmin(T x, T y) { return y < x ? y : x; }
+template <typename T> __device__ inline T vmax(T x, T y) { return x < y ? y : x; }
+
+// Wave-wide scans on DPP lane moves (a few cycles each, against an LDS
+// round trip for a shuffle). DPP controls: row_shr:n (0x110 + n) reads lane
+// i - n of the same 16-lane row, row_shl:n (0x100 + n) lane i + n, row_ror:n
+// (0x120 + n) rotates the row, quad_perm (0x00-0xFF) permutes within 4
+// lanes, row_bcast:15 (0x142) / row_bcast:31 (0x143) read lane 15 of the
+// previous row / lane 31. A lane whose source lies outside its row, or
+// whose row is masked off, gets `fill`.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline int dpp(int fill, int v) {
+  return __builtin_amdgcn_update_dpp(fill, v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline int64_t dpp64(int64_t v) {
+  const int lo = dpp<CTRL, ROW_MASK>(0, static_cast<int>(v));
+  const int hi = dpp<CTRL, ROW_MASK>(0, static_cast<int>(v >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                              static_cast<uint32_t>(lo));
+}
+// Inclusive scan over the 64 lanes (all active): within each row by
+// shifts 1, 2, 4, 8, then row totals carried by the two broadcasts.
+template <typename Op>
+__device__ inline int wave_scan(int v, int identity, Op op) {
+  v = op(v, dpp<0x111>(identity, v));
+  v = op(v, dpp<0x112>(identity, v));
+  v = op(v, dpp<0x114>(identity, v));
+  v = op(v, dpp<0x118>(identity, v));
+  v = op(v, dpp<0x142, 0xA>(identity, v));
+  v = op(v, dpp<0x143, 0xC>(identity, v));
+  return v;
+}
+__device__ inline int wave_scan_sum(int v) {
+  return wave_scan(v, 0, [](int x, int y) { return x + y; });
+}
+__device__ inline int wave_sum(int v) { return __builtin_amdgcn_readlane(wave_scan_sum(v), 63); }
+__device__ inline int wave_max(int v) {
+  return __builtin_amdgcn_readlane(wave_scan(v, INT_MIN, [](int x, int y) { return max(x, y); }), 63);
+}
+__device__ inline int wave_min(int v) {
+  return __builtin_amdgcn_readlane(wave_scan(v, INT_MAX, [](int x, int y) { return min(x, y); }), 63);
+}
+__device__ inline int64_t wave_sum64(int64_t v) {
+  v += dpp64<0x111>(v);
+  v += dpp64<0x112>(v);
+  v += dpp64<0x114>(v);
+  v += dpp64<0x118>(v);
+  v += dpp64<0x142, 0xA>(v);
+  v += dpp64<0x143, 0xC>(v);
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v), 63);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), 63);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+// The partner's key in a bitonic compare-exchange at distance j < 64.
+__device__ inline uint32_t xor_partner(uint32_t x, int j, int lane) {
+  const int v = static_cast<int>(x);
+  switch (j) {
+    case 1: return static_cast<uint32_t>(dpp<0xB1>(v, v));  // quad_perm [1,0,3,2]
+    case 2: return static_cast<uint32_t>(dpp<0x4E>(v, v));  // quad_perm [2,3,0,1]
+    case 4: {
+      const int up = dpp<0x104>(v, v), down = dpp<0x114>(v, v);  // lane i+4, lane i-4
+      return static_cast<uint32_t>((lane & 4) ? down : up);
+    }
+    case 8: return static_cast<uint32_t>(dpp<0x128>(v, v));  // row_ror:8 = lane i ^ 8
+    default: return static_cast<uint32_t>(__shfl_xor(v, j));
+  }
 }
 
-__device__ int block_max(int v, int* scratch) {
-  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off));
-  __syncthreads();
+// Work-group sum of one value per thread. The trailing barrier lets the
+// next call reuse the scratch.
+__device__ int64_t block_sum64(int64_t v, int64_t* scratch) {
+  v = wave_sum64(v);
   if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
   __syncthreads();
-  int m = 0;
-  for (int w = 0; w < kPlanThreads / 64; ++w) m = max(m, scratch[w]);
+  int64_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanWaves; ++w) total += scratch[w];
   __syncthreads();
-  return m;
+  return total;
 }
 
 // Block ids stored per work group for pieces of at most `part_tokens`
@@ -732,7 +802,8 @@ __device__ inline int2 piece_range(int kv, int np, int j) {
 }
 
 // One work group builds the per-step decode plan:
-//   1. validates kv_len and every table entry a sequence reads;
+//   1. validates kv_len (and, with the block ids of step 5, every table
+//      entry a sequence reads);
 //   2. picks the piece bound L (16-token tiles): the smallest that keeps
 //      the (sequence, kv head, piece) work groups within one dispatch round
 //      (groups_per_cu x cu_count), so every group is resident at once --
@@ -746,109 +817,177 @@ __device__ inline int2 piece_range(int kv, int np, int j) {
 //      round-robin), so slot s lands on CU "s mod cu_count" and the CUs
 //      carry near-equal bytes (a CU streams at a bounded rate, so the most
 //      loaded one sets the kernel time);
-//   5. stores each slot's entry (seq, kv head, piece, pieces, token range)
-//      and pool block ids, and zeroes the merge counters.
+//   5. stores each slot's entry (seq, kv head, piece, pieces, token range),
+//      zeroes the merge counters, and publishes the ids per slot for
+//      decode_ids_kernel (or checks the table itself when the list does
+//      not fit: the plan is then unusable and says so).
+// It runs once per engine step, so its latency is what counts: the kv
+// lengths stay in shared memory and the search and scans use wave
+// shuffles. The block ids (step 5) are written by decode_ids_kernel, which
+// spreads them over many CUs (one CU streams only ~20 GB/s).
 template <typename KV, typename BT>
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
-  __shared__ int s_scan[kPlanThreads];
-  __shared__ int s_red[kPlanThreads / 64];
-  __shared__ int s_cnt[4];  // bad kv_len, insufficient table, bad block id, max pieces
-  __shared__ int s_min_kv;
-  __shared__ uint32_t s_key[kDealMax];                    // sort keys of the work groups
+  __shared__ int s_kv[kPlanSeqCache];     // kv_len, or 0 for an invalid length
+  __shared__ int64_t s_red[kPlanWaves];
+  __shared__ int64_t s_tiles[kPlanWaves];
+  __shared__ int s_red5[5][kPlanWaves];  // live sequences, most tiles, least kv, bad kv, short table
+  __shared__ int s_wsum[2][kPlanWaves];
+  __shared__ int s_max_parts;
+  __shared__ int s_lb;
+  __shared__ int64_t s_groups;
+  __shared__ uint32_t s_key[2][kDealMax];                 // bitonic exchange buffers
   __shared__ int s_item_b[kDealMax], s_item_j[kDealMax];  // items (sequence, piece) when dealt
   const int tid = threadIdx.x;
-  if (tid < 4) s_cnt[tid] = 0;
-  if (tid == 0) s_min_kv = INT_MAX;
-  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) s_max_parts = 0;
 
   const KV* kvp = static_cast<const KV*>(a.kv_len);
   const BT* btp = static_cast<const BT*>(a.block_table);
   const int64_t bs = int64_t(1) << a.bs_log2;
   const int hkv = a.num_kv_heads;
-  auto valid_len = [&](int64_t kv) {
-    return kv >= 1 && (kv + bs - 1) / bs <= a.max_blocks && kv <= INT_MAX / 2;
+  const bool cached = a.num_seqs <= kPlanSeqCache;
+  auto clean_len = [&](int64_t kv) -> int {  // 0 for a length no piece reads
+    const bool ok = kv >= 1 && (kv + bs - 1) / bs <= a.max_blocks && kv <= INT_MAX / 2;
+    return ok ? static_cast<int>(kv) : 0;
   };
-  auto tiles_of = [&](int b) -> int {
-    const int64_t kv = static_cast<int64_t>(kvp[b]);
-    return valid_len(kv) ? static_cast<int>((kv + kTile - 1) / kTile) : 0;
+  auto kv_of = [&](int b) -> int {
+    return cached ? s_kv[b] : clean_len(static_cast<int64_t>(kvp[b]));
   };
+  auto tiles_of = [&](int b) -> int { return (kv_of(b) + kTile - 1) / kTile; };
 
   // ---- 1. lengths
-  int tiles = 0, max_tiles = 0, seqs = 0;
-  for (int b = tid; b < a.num_seqs; b += kPlanThreads) {
-    const int64_t kv = static_cast<int64_t>(kvp[b]);
-    atomicMin(&s_min_kv, static_cast<int>(std::max<int64_t>(std::min<int64_t>(kv, INT_MAX), INT_MIN)));
-    if (kv < 1) atomicAdd(&s_cnt[0], 1);
-    else if (!valid_len(kv)) atomicAdd(&s_cnt[1], 1);
-    const int t = tiles_of(b);
-    tiles += t;
-    max_tiles = max(max_tiles, t);
-    seqs += t > 0;
+  {
+    int64_t tiles = 0;
+    int seqs = 0, max_tiles = 0, min_kv = INT_MAX, bad_kv = 0, short_table = 0;
+    for (int b = tid; b < a.num_seqs; b += kPlanThreads) {
+      const int64_t kv = static_cast<int64_t>(kvp[b]);
+      min_kv = min(min_kv, static_cast<int>(vmax<int64_t>(vmin<int64_t>(kv, INT_MAX), INT_MIN)));
+      const int c = clean_len(kv);
+      bad_kv += kv < 1;
+      short_table += kv >= 1 && c == 0;
+      if (cached) s_kv[b] = c;
+      const int t = (c + kTile - 1) / kTile;
+      tiles += t;
+      max_tiles = max(max_tiles, t);
+      seqs += c > 0;
+    }
+    tiles = wave_sum64(tiles);
+    seqs = wave_sum(seqs);
+    max_tiles = wave_max(max_tiles);
+    min_kv = wave_min(min_kv);
+    bad_kv = wave_sum(bad_kv);
+    short_table = wave_sum(short_table);
+    if (lane == 0) {
+      s_tiles[wave] = tiles;
+      s_red5[0][wave] = seqs;
+      s_red5[1][wave] = max_tiles;
+      s_red5[2][wave] = min_kv;
+      s_red5[3][wave] = bad_kv;
+      s_red5[4][wave] = short_table;
+    }
   }
-  const int64_t total_tiles = block_sum(tiles, s_red);
-  const int most_tiles = block_max(max_tiles, s_red);
-  const int64_t units = static_cast<int64_t>(block_sum(seqs, s_red)) * hkv;  // (sequence, kv head) pairs
+  __syncthreads();
+  int64_t total_tiles = 0, live_seqs = 0;
+  int most_tiles = 0, least_kv = INT_MAX, bad_kv = 0, short_table = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanWaves; ++w) {
+    total_tiles += s_tiles[w];
+    live_seqs += s_red5[0][w];
+    most_tiles = max(most_tiles, s_red5[1][w]);
+    least_kv = min(least_kv, s_red5[2][w]);
+    bad_kv += s_red5[3][w];
+    short_table += s_red5[4][w];
+  }
+  const int64_t units = live_seqs * hkv;  // (sequence, kv head) pairs
 
   // ---- 2. piece bound L (tiles)
   // Resident slots to fill: all a CU holds, or 2 per CU when there is at
   // most one (sequence, kv head) unit per CU -- fewer, longer pieces per CU
   // stream at a steadier rate per CU than three (measured on c2/c3-like
   // batches), and the split-K merge has fewer partials.
-  const int per_cu = units <= a.cu_count ? std::min(2, std::max(1, a.groups_per_cu))
-                                         : std::max(1, a.groups_per_cu);
-  const int64_t target = static_cast<int64_t>(per_cu) * std::max(1, a.cu_count);
+  const int per_cu = units <= a.cu_count ? vmin(2, vmax(1, a.groups_per_cu))
+                                         : vmax(1, a.groups_per_cu);
+  const int64_t target = static_cast<int64_t>(per_cu) * vmax(1, a.cu_count);
   // hard: a piece spans at most kIdCap table entries (they are staged in LDS)
-  const int l_cap = static_cast<int>(std::max<int64_t>(
-      1, std::min<int64_t>(INT_MAX / 32, ((static_cast<int64_t>(kIdCap - 1)) << a.bs_log2) / kTile)));
+  const int l_cap = static_cast<int>(vmax<int64_t>(
+      1, vmin<int64_t>(INT_MAX / 32, ((static_cast<int64_t>(kIdCap - 1)) << a.bs_log2) / kTile)));
   // soft: at least one tile per wave per piece, at most kMaxParts pieces per sequence
-  const int l_min = std::min(l_cap, std::max(kWaves, (most_tiles + kMaxParts - 1) / kMaxParts));
-  const int l_top = std::min(l_cap, std::max(l_min, most_tiles));
-  const int l_fair = static_cast<int>(std::min<int64_t>(
-      l_cap, std::max<int64_t>(l_min, (total_tiles * hkv + target - 1) / target)));
-  auto groups_at = [&](int l) -> int64_t {  // uniform call: every thread
-    int n = 0;
-    for (int b = tid; b < a.num_seqs; b += kPlanThreads) n += (tiles_of(b) + l - 1) / l;
-    return static_cast<int64_t>(block_sum(n, s_red)) * hkv;
-  };
-  int lb;
-  if (groups_at(l_top) > target) {
-    lb = l_fair;  // more sequences than resident slots: several rounds anyway
-  } else {
-    int lo = l_min, hi = l_top;  // smallest l in [lo, hi] with groups_at(l) <= target
+  const int l_min = vmin(l_cap, vmax(kWaves, (most_tiles + kMaxParts - 1) / kMaxParts));
+  const int l_top = vmin(l_cap, vmax(l_min, most_tiles));
+  const int l_fair = static_cast<int>(vmin<int64_t>(
+      l_cap, vmax<int64_t>(l_min, (total_tiles * hkv + target - 1) / target)));
+  // smallest l in [l_min, l_top] whose groups fit the target (see above)
+  auto pick = [&](auto&& groups_at) -> int {
+    if (groups_at(l_top) > target) return l_fair;  // more sequences than slots: several rounds
+    int lo = l_min, hi = l_top;
     while (lo < hi) {
       const int mid = lo + (hi - lo) / 2;
       if (groups_at(mid) <= target) hi = mid;
       else lo = mid + 1;
     }
-    lb = lo > 2 * l_fair ? std::max(l_min, std::min(l_cap, 2 * l_fair)) : lo;
+    return lo > 2 * l_fair ? vmax(l_min, vmin(l_cap, 2 * l_fair)) : lo;
+  };
+  int lb;
+  int64_t num_groups;
+  if (cached && a.num_seqs <= kWaveSearchSeqs) {
+    // one wave, lengths from shared memory, no barriers in the search
+    if (wave == 0) {
+      auto groups_wave = [&](int l) -> int64_t {
+        int64_t n = 0;
+        for (int b = lane; b < a.num_seqs; b += 64) n += (tiles_of(b) + l - 1) / l;
+        return wave_sum64(n) * hkv;
+      };
+      const int l = pick(groups_wave);
+      const int64_t g = groups_wave(l);
+      if (lane == 0) {
+        s_lb = l;
+        s_groups = g;
+      }
+    }
+    __syncthreads();
+    lb = s_lb;
+    num_groups = s_groups;
+  } else {
+    auto groups_block = [&](int l) -> int64_t {  // uniform call: every thread
+      int64_t n = 0;
+      for (int b = tid; b < a.num_seqs; b += kPlanThreads) n += (tiles_of(b) + l - 1) / l;
+      return block_sum64(n, s_red) * hkv;
+    };
+    lb = pick(groups_block);
+    num_groups = groups_block(lb);
   }
   const int part_tokens = lb * kTile;
 
   // ---- 3. items (sequence, piece) in sequence order
-  const int64_t num_groups = groups_at(lb);
   const bool deal = num_groups <= kDealMax && num_groups <= target && a.cu_count > 0;
-  const int64_t used_groups = std::min<int64_t>(num_groups, a.work_cap);
+  const int64_t used_groups = vmin<int64_t>(num_groups, a.work_cap);
   int64_t running = 0;
-  for (int base = 0; base < a.num_seqs; base += kPlanThreads) {
+  int parity = 0;
+  for (int base = 0; base < a.num_seqs; base += kPlanThreads, parity ^= 1) {
     const int b = base + tid;
     const int np = b < a.num_seqs ? (tiles_of(b) + lb - 1) / lb : 0;
-    if (np > 0) atomicMax(&s_cnt[3], np);
-    s_scan[tid] = np;
-    __syncthreads();
-    for (int off = 1; off < kPlanThreads; off <<= 1) {
-      const int v = tid >= off ? s_scan[tid - off] : 0;
-      __syncthreads();
-      s_scan[tid] += v;
-      __syncthreads();
+    const int most = wave_max(np);
+    if (lane == 0 && most > 0) atomicMax(&s_max_parts, most);
+    // exclusive scan of np: inclusive within the wave, then wave totals
+    const int incl = wave_scan_sum(np);
+    if (lane == 63) s_wsum[parity][wave] = incl;
+    __syncthreads();  // alternate buffers: the next chunk writes the other one
+    int before = 0, chunk = 0;
+#pragma unroll
+    for (int w = 0; w < kPlanWaves; ++w) {
+      const int t = s_wsum[parity][w];
+      before += w < wave ? t : 0;
+      chunk += t;
     }
-    const int64_t start = running + s_scan[tid] - np;
+    const int64_t start = running + before + incl - np;
     for (int j = 0; j < np; ++j) {
       const int64_t item = start + j;
       if (deal) {
+        if (item >= kDealMax) break;  // cannot happen: items <= num_groups <= kDealMax
         s_item_b[item] = b;
         s_item_j[item] = j;
       } else {
-        const int2 r = piece_range(static_cast<int>(kvp[b]), np, j);
+        const int2 r = piece_range(kv_of(b), np, j);
         for (int h = 0; h < hkv; ++h) {
           const int64_t slot = item * hkv + h;
           if (slot < a.work_cap) {
@@ -859,55 +998,58 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
         }
       }
     }
-    running += s_scan[kPlanThreads - 1];
-    __syncthreads();
+    running += chunk;
   }
+  __syncthreads();  // items complete
 
   // ---- 4. deal: sort groups by size (descending, then index) and place
   // sorted position j in slot r * cu_count + c (round r = j / cu_count),
   // forward or backward over c by round parity, ending forward so the last
   // partial round fills slots [r * cu_count, r * cu_count + rem).
   if (deal) {
-    const int g = tid;
-    uint32_t key = 0xFFFFFFFFu;
-    if (g < num_groups) {
-      const int item = g / hkv;
+    uint32_t x = 0xFFFFFFFFu;
+    if (tid < num_groups) {
+      const int item = tid / hkv;
       const int b = s_item_b[item];
       const int np = (tiles_of(b) + lb - 1) / lb;
-      const int2 r = piece_range(static_cast<int>(kvp[b]), np, s_item_j[item]);
-      const uint32_t t = static_cast<uint32_t>(std::min((r.y - r.x + kTile - 1) / kTile, 0xFFFFF));
-      key = ((0xFFFFFu - t) << 11) | static_cast<uint32_t>(g);
+      const int2 r = piece_range(kv_of(b), np, s_item_j[item]);
+      const uint32_t t = static_cast<uint32_t>(vmin((r.y - r.x + kTile - 1) / kTile, 0xFFFFF));
+      x = ((0xFFFFFu - t) << 11) | static_cast<uint32_t>(tid);
     }
-    s_key[tid] = key;
-    __syncthreads();
-    // bitonic sort of kDealMax keys, ascending
+    // bitonic sort of kDealMax keys, ascending, one key per thread:
+    // partners in the same wave exchange by DPP or shuffle, farther ones
+    // through alternating shared buffers (one barrier per exchange)
+    int buf = 0;
+#pragma unroll
     for (int k = 2; k <= kDealMax; k <<= 1) {
+#pragma unroll
       for (int j = k >> 1; j > 0; j >>= 1) {
-        const int ixj = tid ^ j;
-        if (ixj > tid) {
-          const uint32_t x = s_key[tid], y = s_key[ixj];
-          const bool up = (tid & k) == 0;
-          if ((x > y) == up) {
-            s_key[tid] = y;
-            s_key[ixj] = x;
-          }
+        uint32_t y;
+        if (j >= 64) {
+          s_key[buf][tid] = x;
+          __syncthreads();
+          y = s_key[buf][tid ^ j];
+          buf ^= 1;
+        } else {
+          y = xor_partner(x, j, lane);
         }
-        __syncthreads();
+        const bool up = (tid & k) == 0, lower = (tid & j) == 0;
+        x = (lower == up) ? min(x, y) : max(x, y);
       }
     }
-    if (tid < num_groups) {
-      const int gs = static_cast<int>(s_key[tid] & 2047u);
+    const int gs = static_cast<int>(x & 2047u);
+    if (tid < num_groups && gs < num_groups) {  // gs < num_groups: always, for a sorted list
       const int item = gs / hkv;
       const int h = gs - item * hkv;
       const int b = s_item_b[item];
       const int j = s_item_j[item];
       const int np = (tiles_of(b) + lb - 1) / lb;
-      const int2 r = piece_range(static_cast<int>(kvp[b]), np, j);
+      const int2 r = piece_range(kv_of(b), np, j);
       const int cus = a.cu_count;
       const int rounds = static_cast<int>((num_groups + cus - 1) / cus);
       const int rd = tid / cus, c = tid - rd * cus;
       const bool forward = ((rounds - 1 - rd) & 1) == 0;
-      const int64_t slot = static_cast<int64_t>(rd) * cus + (forward ? c : cus - 1 - c);
+      const int slot = rd * cus + (forward ? c : cus - 1 - c);
       if (slot < a.work_cap) {
         int4* w = reinterpret_cast<int4*>(a.work + 8 * slot);
         w[0] = make_int4(b, h, j, np);
@@ -915,56 +1057,106 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
       }
     }
   }
-  __syncthreads();  // work entries written above are read back below
 
-  // ---- 5. each slot's pool blocks, -1 past its last block (and for an
-  // entry outside the pool, which the check below reports)
+  // ---- 5. block ids per slot: decode_ids_kernel, when the list fits
   const int per_item = ids_per_item(part_tokens, a.bs_log2);
   const int64_t n_ids = used_groups * per_item;
-  if (n_ids <= a.ids_cap) {
-    for (int64_t i = tid; i < n_ids; i += kPlanThreads) {
-      const int64_t slot = i / per_item;
-      const int k = static_cast<int>(i - slot * per_item);
-      const int4 w0 = reinterpret_cast<const int4*>(a.work + 8 * slot)[0];
-      const int4 w1 = reinterpret_cast<const int4*>(a.work + 8 * slot)[1];
-      const int64_t first = static_cast<int64_t>(w1.x) >> a.bs_log2;
-      const int64_t last = (static_cast<int64_t>(w1.y) - 1) >> a.bs_log2;
-      int32_t id = -1;
-      if (first + k <= last) {
-        const int64_t blk = static_cast<int64_t>(btp[w0.x * a.bt_stride + first + k]);
-        if (blk >= 0 && blk < a.num_blocks) id = static_cast<int32_t>(blk);
+  const bool listed = used_groups == num_groups && n_ids <= a.ids_cap &&
+                      n_ids <= INT_MAX - kIdsPerPass;
+  int64_t bad = 0;
+  if (!listed) {  // uniform
+    const int64_t n = static_cast<int64_t>(a.num_seqs) * a.max_blocks;
+    for (int64_t i = tid; i < n; i += kPlanThreads) {
+      const int64_t b = i / a.max_blocks;
+      const int64_t j = i - b * a.max_blocks;
+      if (j < (kv_of(static_cast<int>(b)) + bs - 1) / bs) {
+        const int64_t blk = static_cast<int64_t>(btp[b * a.bt_stride + j]);
+        bad += (blk < 0 || blk >= a.num_blocks);
       }
-      a.ids[i] = id;
     }
+    bad = block_sum64(bad, s_red);
   }
-
-  // every table entry a valid sequence reads must be a pool block
-  const int64_t n = static_cast<int64_t>(a.num_seqs) * a.max_blocks;
-  int bad = 0;
-  for (int64_t i = tid; i < n; i += kPlanThreads) {
-    const int64_t b = i / a.max_blocks;
-    const int64_t j = i - b * a.max_blocks;
-    const int64_t kv = static_cast<int64_t>(kvp[b]);
-    if (!valid_len(kv)) continue;
-    if (j < (kv + bs - 1) / bs) {
-      const int64_t blk = static_cast<int64_t>(btp[b * a.bt_stride + j]);
-      bad += (blk < 0 || blk >= a.num_blocks);
-    }
-  }
-  if (bad) atomicAdd(&s_cnt[2], bad);
   const int64_t nc = static_cast<int64_t>(a.num_seqs) * hkv;
   for (int64_t i = tid; i < nc; i += kPlanThreads) a.counters[i] = 0;
   __syncthreads();
   if (tid == 0) {
-    a.status[MV_PLAN_NUM_ITEMS] = static_cast<int32_t>(std::min<int64_t>(num_groups, INT_MAX));
-    a.status[MV_PLAN_BAD_KV_LEN] = s_cnt[0];
-    a.status[MV_PLAN_INSUFFICIENT] = s_cnt[1];
-    a.status[MV_PLAN_BAD_BLOCK] = s_cnt[2];
-    a.status[MV_PLAN_MAX_PARTS] = s_cnt[3];
-    a.status[MV_PLAN_MIN_KV_LEN] = a.num_seqs > 0 ? s_min_kv : 0;
+    a.status[MV_PLAN_NUM_ITEMS] = static_cast<int32_t>(vmin<int64_t>(num_groups, INT_MAX));
+    a.status[MV_PLAN_BAD_KV_LEN] = bad_kv;
+    a.status[MV_PLAN_INSUFFICIENT] = short_table;
+    a.status[MV_PLAN_BAD_BLOCK] = static_cast<int32_t>(vmin<int64_t>(bad, INT_MAX));  // the id kernel adds its count
+    a.status[MV_PLAN_MAX_PARTS] = s_max_parts;
+    a.status[MV_PLAN_MIN_KV_LEN] = a.num_seqs > 0 ? least_kv : 0;
     a.status[MV_PLAN_PARTITION_TOKENS] = part_tokens;
-    a.status[MV_PLAN_IDS_PER_ITEM] = n_ids <= a.ids_cap ? per_item : -1;  // -1: list not written
+    a.status[MV_PLAN_IDS_PER_ITEM] = listed ? per_item : -1;  // -1: no list this step
   }
+}
+
+struct IdsArgs {
+  const void* block_table;
+  int64_t bt_stride;
+  int32_t num_seqs, max_blocks;
+  const int32_t* work;
+  int32_t* ids;
+  int32_t* status;
+  int64_t num_blocks;
+  int32_t bs_log2;
+};
+
+// Step 5 of the plan, over many CUs: slot s's list ids[s * n, (s + 1) * n)
+// (n = status[MV_PLAN_IDS_PER_ITEM], a multiple of 4) holds the pool blocks
+// of its piece, -1 past its last block and for an entry outside the pool.
+// One thread writes 4 ids of one slot at a time. The pieces of kv head 0
+// read every block of every valid sequence, and a block belongs to the one
+// piece that holds its first token: counting the bad entries among those
+// reads checks each table entry a sequence needs exactly once.
+template <typename BT>
+__global__ __launch_bounds__(kIdsThreads) void decode_ids_kernel(IdsArgs a) {
+  const int per_item = a.status[MV_PLAN_IDS_PER_ITEM];  // -1: no list this step
+  const int groups = a.status[MV_PLAN_NUM_ITEMS];
+  if (per_item <= 0 || groups <= 0) return;
+  const int quads = groups * (per_item / 4);  // the plan bounds groups * per_item
+  const int quads_per_slot = per_item / 4;
+  const BT* btp = static_cast<const BT*>(a.block_table);
+  int bad = 0;
+  for (int base = blockIdx.x * kIdsThreads * kIdsQuads; base < quads;
+       base += gridDim.x * kIdsThreads * kIdsQuads) {
+    int64_t blk[kIdsQuads][4];
+    bool own[kIdsQuads][4];
+#pragma unroll
+    for (int u = 0; u < kIdsQuads; ++u) {
+      const int q = base + u * kIdsThreads + threadIdx.x;
+      const bool live = q < quads;
+      const int slot = live ? q / quads_per_slot : 0;
+      const int k0 = live ? 4 * (q - slot * quads_per_slot) : 0;
+      const int4 w0 = reinterpret_cast<const int4*>(a.work + 8 * static_cast<int64_t>(slot))[0];
+      const int4 w1 = reinterpret_cast<const int4*>(a.work + 8 * static_cast<int64_t>(slot))[1];
+      const int first = w1.x >> a.bs_log2;
+      const int last = (w1.y - 1) >> a.bs_log2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = first + k0 + e;
+        // the bounds hold for every entry the plan writes
+        const bool read = live && m <= last && m >= 0 && m < a.max_blocks && w0.x >= 0 &&
+                          w0.x < a.num_seqs;
+        own[u][e] = read && w0.y == 0 && (static_cast<int64_t>(m) << a.bs_log2) >= w1.x;
+        blk[u][e] = read ? static_cast<int64_t>(btp[w0.x * a.bt_stride + m]) : -1;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kIdsQuads; ++u) {
+      const int q = base + u * kIdsThreads + threadIdx.x;
+      int32_t v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool in_pool = blk[u][e] >= 0 && blk[u][e] < a.num_blocks;
+        bad += own[u][e] && !in_pool;
+        v[e] = in_pool ? static_cast<int32_t>(blk[u][e]) : -1;
+      }
+      if (q < quads)
+        reinterpret_cast<int4*>(a.ids)[q] = make_int4(v[0], v[1], v[2], v[3]);
+    }
+  }
+  if (bad) atomicAdd(&a.status[MV_PLAN_BAD_BLOCK], bad);
 }
 
 // ------------------------------------------------------------- dispatch ---
@@ -1079,6 +1271,24 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
   } else {
     if (bt_is_i64) decode_plan_kernel<int32_t, int64_t><<<1, kPlanThreads, 0, s>>>(a);
     else decode_plan_kernel<int32_t, int32_t><<<1, kPlanThreads, 0, s>>>(a);
+  }
+  if (const int rc = check_launch("mv_decode_plan")) return rc;
+  if (num_seqs > 0 && block_ids_capacity > 0) {
+    IdsArgs d;
+    d.block_table = block_table;
+    d.bt_stride = bt_stride;
+    d.num_seqs = num_seqs;
+    d.max_blocks = max_blocks;
+    d.work = work_items;
+    d.ids = block_ids;
+    d.status = status;
+    d.num_blocks = num_blocks;
+    d.bs_log2 = a.bs_log2;
+    // enough work groups for the largest list the capacity admits, in one pass
+    const int grid = static_cast<int>(std::min<int64_t>(
+        1024, std::max<int64_t>(1, (block_ids_capacity + kIdsPerPass - 1) / kIdsPerPass)));
+    if (bt_is_i64) decode_ids_kernel<int64_t><<<grid, kIdsThreads, 0, s>>>(d);
+    else decode_ids_kernel<int32_t><<<grid, kIdsThreads, 0, s>>>(d);
   }
   return check_launch("mv_decode_plan");
 }
