@@ -85,13 +85,14 @@ def _hold_gpu(stream, ms):
     torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS * ms))
 
 
-def time_loop(fn, n, stream):
+def time_loop(fn, n, stream, host_us=60.0):
     """GPU time per iteration: the launches run back to back on the GPU
-    (host overhead hidden behind a held GPU), bracketed by HIP events."""
+    (host overhead, up to ``host_us`` per iteration, hidden behind a held
+    GPU), bracketed by HIP events."""
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    _hold_gpu(stream, 5 + 0.06 * n)
+    _hold_gpu(stream, 5 + host_us * 1e-3 * n)
     start.record(stream)
     for i in range(n):
         fn(i)
@@ -108,6 +109,23 @@ def wall_loop(fn, n):
         fn(i)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) * 1e6 / n
+
+
+def rope_tables(head_dim, theta, max_pos, dtype, device):
+    """cos / sin tables of the model's rotary embedding (RotaryEmbedding,
+    mini_vllm/model/rotary.py:16-35), built on the device."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim))
+    emb = torch.outer(torch.arange(max_pos, dtype=torch.float32, device=device), inv)
+    emb = torch.cat((emb, emb), dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def torch_rope(x, pos, cos, sin):
+    """The reference's eager rotary (rotary.py:44-82): the unfused sequence
+    the fused kernel replaces, timed beside it."""
+    c, s = cos[pos].unsqueeze(-2), sin[pos].unsqueeze(-2)
+    h = x.shape[-1] // 2
+    return x * c + torch.cat((-x[..., h:], x[..., :h]), dim=-1) * s
 
 
 def plan_step_us(bt, kv, bs, num_blocks, dev, spec, plan_decode, reps=20):
@@ -221,7 +239,7 @@ def main(argv=None) -> int:
 
     from mini_vllm.attention import _hip
     from mini_vllm.attention.paged_attention_gpu import (
-        hip_cache_write, hip_decode_attention, plan_decode)
+        hip_cache_write, hip_decode_attention, hip_rope_kv_cache_write, plan_decode)
 
     _hip.load()
     dev = torch.device("cuda", 0)
@@ -268,6 +286,32 @@ def main(argv=None) -> int:
     us_wall = wall_loop(layer_call, args.steps)
     log(f"[bench] layer call {us_step:.2f} us, decode {us_decode:.2f} us, write {us_write:.2f} us")
 
+    # RoPE of the step's q and new k + KV write: fused kernel against the
+    # reference's sequence (two eager rotaries, then the cache write)
+    cos, sin = rope_tables(spec.head_dim, 1000000.0, 32768, spec.dtype, dev)
+    pos = kv - 1  # the new token's position in each sequence
+
+    def rope_fused(i):
+        L = layers[i % n_layers]
+        hip_rope_kv_cache_write(L["q"], L["nk"], L["nv"], pos, cos, sin, L["k"], L["v"], slots, bs,
+                                return_key=False)
+
+    def rope_unfused(i):
+        L = layers[i % n_layers]
+        torch_rope(L["q"], pos, cos, sin)
+        k = torch_rope(L["nk"], pos, cos, sin)
+        hip_cache_write(k, L["nv"], L["k"], L["v"], slots, bs)
+
+    for i in range(args.warmup):
+        rope_fused(i)
+        rope_unfused(i)
+    us_rope = time_loop(rope_fused, args.steps, stream)
+    us_rope_unfused = time_loop(rope_unfused, args.steps, stream, host_us=200.0)
+    us_rope_wall = wall_loop(rope_fused, args.steps)
+    us_rope_unfused_wall = wall_loop(rope_unfused, args.steps)
+    log(f"[bench] rope+write fused {us_rope:.2f} us (host-incl {us_rope_wall:.1f}), "
+        f"unfused {us_rope_unfused:.2f} us (host-incl {us_rope_unfused_wall:.1f})")
+
     dec_bytes = decode_bytes(layout, spec.dtype)
     wr_bytes = write_bytes(layout, spec.dtype)
     gbs = (dec_bytes + wr_bytes) / us_step / 1e3
@@ -301,6 +345,13 @@ def main(argv=None) -> int:
         "host_inclusive_us_per_layer_call": round(us_wall, 3),
         "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "plan_us_per_step": round(plan_us, 1),
+        "rope_write": {
+            "what": "RoPE of the step's q and new k + KV write (qwen_runner.py:164-170)",
+            "fused_us": round(us_rope, 3),
+            "unfused_us": round(us_rope_unfused, 3),
+            "fused_host_inclusive_us": round(us_rope_wall, 2),
+            "unfused_host_inclusive_us": round(us_rope_unfused_wall, 2),
+        },
         "partition_tokens": plan.partition_tokens,
         "work_groups": plan.num_groups,
         "roofline": {

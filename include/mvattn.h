@@ -216,6 +216,48 @@ int mv_gather_paged_kv(const void* key_cache, const void* value_cache, const voi
                        void* out_key, void* out_value, int32_t num_kv_heads, int32_t head_dim,
                        int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream);
 
+/*
+ * Fused rotary embedding + KV-cache write of one step's new tokens.
+ * Replaces, in `QwenModelRunner.execute_model`
+ * (mini_vllm/model_runner/qwen_runner.py:164-170), the three calls
+ *   q = rope(q, positions); k = rope(k, positions);
+ *   write_kv_cache(layer, k, v, slot_mapping)
+ * with `RotaryEmbedding.__call__` / `_rotate_half`
+ * (mini_vllm/model/rotary.py:44-82):
+ *   x_rot = x * cos[pos] + [-x[D/2:], x[:D/2]] * sin[pos]
+ * for every query head (-> query_out; may equal query) and key head
+ * (-> key_cache at slot_mapping[t], as mv_kv_cache_write; also -> key_out
+ * when key_out is not null), and the bitwise copy of value into
+ * value_cache. Each product and the sum are rounded to the storage dtype,
+ * as the reference's eager ops do: the results are bit-identical.
+ *   cos_table, sin_table  [max_positions, >= head_dim] rows of
+ *                         table_stride elements, the tensors' dtype
+ *   positions             [num_tokens] int64, checked by mv_positions_check
+ * key_cache == NULL skips the cache write (value, value_cache and
+ * slot_mapping are then ignored): a plain rotary on query / key.
+ * Pointers and strides (in elements) must give 16-byte aligned rows, and
+ * head_dim must be a multiple of 32 bytes' worth of elements.
+ */
+int mv_rope_kv_cache_write(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                           void* query_out, int64_t qo_stride_tok, int64_t qo_stride_head,
+                           const void* key, int64_t k_stride_tok, int64_t k_stride_head,
+                           void* key_out, int64_t ko_stride_tok, int64_t ko_stride_head,
+                           const void* value, int64_t v_stride_tok, int64_t v_stride_head,
+                           void* key_cache, void* value_cache, const int64_t* slot_mapping,
+                           const int64_t* positions, const void* cos_table, const void* sin_table,
+                           int64_t table_stride, int64_t max_positions, int64_t num_tokens,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream);
+
+/*
+ * Position validation for mv_rope_kv_cache_write: status[0] (int32,
+ * device) = number of positions outside [0, max_positions). Replaces the
+ * bounds check of the reference's table lookup `self._cos[positions]`
+ * (mini_vllm/model/rotary.py:64-65), which raises IndexError.
+ */
+int mv_positions_check(const int64_t* positions, int64_t num_tokens, int64_t max_positions,
+                       int32_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,18 @@ SIGNATURES = {
         _P, _P, _I32, _I32, _I32,  # out_key, out_value, num_kv_heads, head_dim, block_size
         _I64, _I32, _P,            # num_blocks, dtype, stream
     ]),
+    "mv_rope_kv_cache_write": (ctypes.c_int, [
+        _P, _I64, _I64,            # query, strides
+        _P, _I64, _I64,            # query_out, strides
+        _P, _I64, _I64,            # key, strides
+        _P, _I64, _I64,            # key_out, strides
+        _P, _I64, _I64,            # value, strides
+        _P, _P, _P,                # key_cache, value_cache, slot_mapping
+        _P, _P, _P, _I64, _I64,    # positions, cos, sin, table_stride, max_positions
+        _I64, _I32, _I32, _I32,    # num_tokens, num_q_heads, num_kv_heads, head_dim
+        _I32, _I64, _I32, _P,      # block_size, num_blocks, dtype, stream
+    ]),
+    "mv_positions_check": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -48,6 +48,8 @@ __all__ = [
     "gather_prefix_kv",
     "hip_cache_write",
     "hip_decode_attention",
+    "hip_rope_kv_cache_write",
+    "hip_rotary",
     "plan_decode",
     "triton_cache_write",
     "triton_decode_attention",
@@ -58,8 +60,17 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def _stream(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+# torch's raw current-stream accessor costs ~0.1 us per call against ~2 us
+# for torch.cuda.current_stream(device).cuda_stream.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as an address (hipStream_t)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def _is_pow2(v: int) -> bool:
@@ -231,17 +242,20 @@ class DecodePlan:
 # groups per CU from the library, times the CU count), so the whole grid
 # runs in one dispatch round and can be balanced over the CUs.
 # MVATTN_GROUPS_PER_CU overrides the per-CU figure.
-_CU_COUNT: dict = {}
+_SPLIT: dict = {}
 
 
 def _groups_per_cu(device: torch.device, head_dim: int, dtype: torch.dtype) -> Tuple[int, int]:
     """(work groups per CU, CU count) for the decode plan."""
-    if device not in _CU_COUNT:
-        _CU_COUNT[device] = torch.cuda.get_device_properties(device).multi_processor_count
-    per_cu = os.environ.get("MVATTN_GROUPS_PER_CU")
-    if per_cu is None:
-        per_cu = _hip.load().mv_decode_groups_per_cu(head_dim, _hip.MV_DTYPE[dtype])
-    return max(1, int(per_cu)), _CU_COUNT[device]
+    key = (device, head_dim, dtype)
+    split = _SPLIT.get(key)
+    if split is None:
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        per_cu = os.environ.get("MVATTN_GROUPS_PER_CU")
+        if per_cu is None:
+            per_cu = _hip.load().mv_decode_groups_per_cu(head_dim, _hip.MV_DTYPE[dtype])
+        split = _SPLIT[key] = (max(1, int(per_cu)), cus)
+    return split
 
 
 def plan_decode(
@@ -376,7 +390,7 @@ def hip_decode_attention(
     num_blocks = key_cache.shape[0]
     plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
                        query.dtype, num_kv_heads)
-    output = torch.empty(query.shape, dtype=query.dtype, device=device)
+    output = torch.empty_like(query, memory_format=torch.contiguous_format)
     if total_decode == 0 or plan.num_groups == 0:
         return output
     if query.stride(2) != 1 or (query.stride(1) * query.element_size()) % 16 or (
@@ -405,6 +419,165 @@ def hip_decode_attention(
 # The reference's tests and benchmarks import these names.
 triton_cache_write = hip_cache_write
 triton_decode_attention = hip_decode_attention
+
+
+# ============================================================================
+# Rotary embedding (+ KV write)
+# ============================================================================
+
+
+def _check_positions(positions: torch.Tensor, max_positions: int) -> None:
+    """``IndexError`` for a position outside the cos / sin tables, as the
+    reference's lookup ``self._cos[positions]`` raises
+    (mini_vllm/model/rotary.py:64-65). One device check per distinct
+    positions tensor (the layers of a step share it)."""
+    extra = (max_positions,)
+    if _cache_get("positions", (positions,), extra) is not None:
+        return
+    lib = _hip.load()
+    device = positions.device
+    status = torch.empty(1, dtype=torch.int32, device=device)
+    _hip.check(
+        lib.mv_positions_check(_ptr(positions), positions.numel(), max_positions, _ptr(status),
+                               _stream(device)),
+        "mv_positions_check",
+    )
+    bad = status.item()
+    if bad:
+        raise IndexError(
+            f"{bad} position(s) outside the rotary tables [0, {max_positions})"
+        )
+    _cache_put("positions", (positions,), extra, True)
+
+
+def _rope_operand(x: torch.Tensor) -> torch.Tensor:
+    """x with 16-byte aligned, head_dim-contiguous rows (a copy only if not)."""
+    eb = x.element_size()
+    if (x.stride(2) != 1 or (x.stride(0) * eb) % 16 or (x.stride(1) * eb) % 16
+            or x.data_ptr() % 16):
+        x = x.contiguous()
+    return x
+
+
+def hip_rope_kv_cache_write(
+    query: Optional[torch.Tensor],
+    key: torch.Tensor,
+    value: Optional[torch.Tensor],
+    positions: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    key_cache: Optional[torch.Tensor] = None,
+    value_cache: Optional[torch.Tensor] = None,
+    slot_mapping: Optional[torch.Tensor] = None,
+    block_size: int = 0,
+    *,
+    return_key: bool = True,
+    inplace: bool = False,
+) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """Fused ``q = rope(q, positions); k = rope(k, positions);
+    write_kv_cache(k, v, slot_mapping)`` in one launch.
+
+    Replaces the runner's three calls (reference qwen_runner.py:164-170):
+    ``RotaryEmbedding.__call__`` (rotary.py:44-82, tables ``rope.cos`` /
+    ``rope.sin`` of ``[max_seq_len, head_dim]`` in the model dtype) on
+    ``query`` ``[T, Hq, D]`` and ``key`` ``[T, Hkv, D]``, then
+    ``triton_cache_write`` (paged_attention_gpu.py:90-154) of the rotated
+    key and of ``value``. Results are bit-identical to the reference's
+    eager ops (each product and the sum rounded to the dtype).
+
+    Returns ``(query_rot, key_rot)``: ``query_rot`` is a new tensor, or
+    ``query`` itself with ``inplace=True`` (None without a query);
+    ``key_rot`` is materialised only with ``return_key=True`` (prefill
+    attention reads it), else None. Without ``key_cache`` nothing is
+    written to a cache (a plain rotary of query and key). Errors as the
+    reference: ``AssertionError`` (shapes, dtypes, duplicate slots),
+    ``IndexError`` (slot or position out of range).
+    """
+    num_tokens, num_kv_heads, head_dim = key.shape
+    dtype, device = key.dtype, key.device
+    assert device.type == "cuda", f"key.device must be cuda, got {device}"
+    assert dtype in SUPPORTED_DTYPES, f"dtype {dtype} not supported"
+    assert positions.shape == (num_tokens,), f"positions {tuple(positions.shape)} != ({num_tokens},)"
+    assert cos.dim() == 2 and cos.shape == sin.shape and cos.shape[1] >= head_dim, (
+        f"rotary tables {tuple(cos.shape)} / {tuple(sin.shape)} do not cover head_dim {head_dim}"
+    )
+    assert cos.dtype == dtype and sin.dtype == dtype, f"rotary tables {cos.dtype} != {dtype}"
+    assert cos.device == device and sin.device == device
+    num_q_heads = 0
+    if query is not None:
+        assert query.dim() == 3 and query.shape[0] == num_tokens and query.shape[2] == head_dim, (
+            f"query {tuple(query.shape)} does not match key {tuple(key.shape)}"
+        )
+        assert query.dtype == dtype and query.device == device
+        num_q_heads = query.shape[1]
+    write = key_cache is not None
+    num_blocks = 0
+    if write:
+        assert value is not None and value_cache is not None and slot_mapping is not None
+        assert key.shape == value.shape, f"key {key.shape} != value {value.shape}"
+        assert key_cache.shape == value_cache.shape
+        assert value.dtype == dtype and key_cache.dtype == dtype and value_cache.dtype == dtype
+        assert key_cache.device == device and value_cache.device == device
+        assert slot_mapping.shape == (num_tokens,)
+        assert block_size == key_cache.shape[2], f"block_size {block_size} != cache dim2 {key_cache.shape[2]}"
+        assert _is_pow2(block_size), f"block_size {block_size} must be a power of 2"
+        assert key_cache.shape[1] == num_kv_heads and key_cache.shape[3] == head_dim
+        assert key_cache.is_contiguous() and value_cache.is_contiguous(), "cache must be contiguous"
+        if slot_mapping.device != device:
+            slot_mapping = slot_mapping.to(device)
+        if slot_mapping.dtype != torch.int64:
+            slot_mapping = slot_mapping.to(torch.int64)
+        slot_mapping = slot_mapping.contiguous()
+        num_blocks = key_cache.shape[0]
+        _check_slots(slot_mapping, num_blocks * block_size)
+    if positions.device != device:
+        positions = positions.to(device)
+    if positions.dtype != torch.int64:
+        positions = positions.to(torch.int64)
+    positions = positions.contiguous()
+    _check_positions(positions, cos.shape[0])
+
+    q_out = None
+    if query is not None:
+        query = _rope_operand(query)
+        q_out = query if inplace else torch.empty_like(query, memory_format=torch.contiguous_format)
+    k_out = torch.empty_like(key, memory_format=torch.contiguous_format) if return_key else None
+    if num_tokens == 0:
+        return q_out, k_out
+    key = _rope_operand(key)
+    if write:
+        value = _rope_operand(value)
+    if cos.stride(1) != 1 or sin.stride(1) != 1 or cos.stride(0) != sin.stride(0):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    lib = _hip.load()
+    _hip.check(
+        lib.mv_rope_kv_cache_write(
+            _ptr(query), query.stride(0) if query is not None else 0,
+            query.stride(1) if query is not None else 0,
+            _ptr(q_out), q_out.stride(0) if q_out is not None else 0,
+            q_out.stride(1) if q_out is not None else 0,
+            _ptr(key), key.stride(0), key.stride(1),
+            _ptr(k_out), k_out.stride(0) if k_out is not None else 0,
+            k_out.stride(1) if k_out is not None else 0,
+            _ptr(value) if write else None, value.stride(0) if write else 0,
+            value.stride(1) if write else 0,
+            _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping) if write else None,
+            _ptr(positions), _ptr(cos), _ptr(sin), cos.stride(0), cos.shape[0],
+            num_tokens, num_q_heads, num_kv_heads, head_dim, block_size if write else 0,
+            num_blocks, _hip.MV_DTYPE[dtype], _stream(device),
+        ),
+        "mv_rope_kv_cache_write",
+    )
+    return q_out, k_out
+
+
+def hip_rotary(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+               sin: torch.Tensor) -> torch.Tensor:
+    """``RotaryEmbedding.__call__`` (reference rotary.py:44-66) on the GPU:
+    ``x`` ``[T, H, D]`` rotated at ``positions`` with tables ``cos`` /
+    ``sin``; a new tensor, bit-identical to the reference's eager ops."""
+    _, out = hip_rope_kv_cache_write(None, x, None, positions, cos, sin, return_key=True)
+    return out
 
 
 # ============================================================================
@@ -550,6 +723,31 @@ class AttentionBackendGPU(AttentionBackend):
         hip_cache_write(
             key, value, pool.key_caches[layer_idx], pool.value_caches[layer_idx],
             slot_mapping, pool.block_size,
+        )
+
+    def rope_write_kv_cache(
+        self,
+        layer_idx: int,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        positions: torch.Tensor,
+        rope: Any,
+        slot_mapping: torch.Tensor,
+        return_key: bool = False,
+    ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """Fused replacement of the runner's ``q = rope(q, positions);
+        k = rope(k, positions); write_kv_cache(layer, k, v, slot_mapping)``
+        (reference qwen_runner.py:164-170). ``rope`` is the runner's
+        ``RotaryEmbedding`` (its ``cos`` / ``sin`` tables). Returns the
+        rotated query and, with ``return_key``, the rotated key (the prefill
+        chunk's attention reads it)."""
+        pool = self._pool
+        assert pool is not None, "allocate_pool must be called first"
+        return hip_rope_kv_cache_write(
+            query, key, value, positions, rope.cos, rope.sin,
+            pool.key_caches[layer_idx], pool.value_caches[layer_idx], slot_mapping,
+            pool.block_size, return_key=return_key,
         )
 
     def decode_attention(

@@ -94,3 +94,17 @@ def prefill(q, key_cache, value_cache, block_tables, seq_indices, cached_len_bef
                 out[off + t, h] = (p[:, None] * v).sum(axis=0) / p.sum()
         off += ql
     return out
+
+
+def rotary_complex(x, positions, head_dim, theta):
+    """RoPE as the complex product of RoFormer: pair (x_i, x_{i+D/2}) is the
+    complex number z_i, rotated by angle pos * theta**(-2i/D) (float64
+    angles, no tables), i.e. the map the reference's rotate_half form
+    (mini_vllm/model/rotary.py:44-82) implements. x: [T, H, D]."""
+    x = np.asarray(x, dtype=np.float64)
+    half = head_dim // 2
+    inv = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / head_dim)
+    ang = np.asarray(positions, dtype=np.float64)[:, None] * inv[None, :]  # [T, half]
+    rot = np.exp(1j * ang)[:, None, :]                                      # [T, 1, half]
+    z = (x[..., :half] + 1j * x[..., half:]) * rot
+    return np.concatenate([z.real, z.imag], axis=-1)
