@@ -286,6 +286,27 @@ def main(argv=None) -> int:
     us_wall = wall_loop(layer_call, args.steps)
     log(f"[bench] layer call {us_step:.2f} us, decode {us_decode:.2f} us, write {us_write:.2f} us")
 
+    # A whole decode step captured into one HIP graph: the plan (replanned
+    # from the static metadata at every replay) and Qwen2-0.5B's 24 layer
+    # calls; no host work per layer.
+    from mini_vllm.attention.paged_attention_gpu import check_deferred, clear_deferred
+    graph_layers = 24
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(graph_layers):
+            layer_call(i)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    check_deferred()
+    g_steps = max(5, args.steps // graph_layers)
+    us_graph = time_loop(lambda i: graph.replay(), g_steps, stream, host_us=100.0)
+    us_graph_wall = wall_loop(lambda i: graph.replay(), g_steps)
+    del graph
+    clear_deferred()
+    log(f"[bench] captured step ({graph_layers} layers + plan): {us_graph:.1f} us GPU, "
+        f"{us_graph_wall:.1f} us host-inclusive")
+
     # RoPE of the step's q and new k + KV write: fused kernel against the
     # reference's sequence (two eager rotaries, then the cache write)
     cos, sin = rope_tables(spec.head_dim, 1000000.0, 32768, spec.dtype, dev)
@@ -345,6 +366,13 @@ def main(argv=None) -> int:
         "host_inclusive_us_per_layer_call": round(us_wall, 3),
         "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "plan_us_per_step": round(plan_us, 1),
+        "graph_step": {
+            "what": "one HIP graph: decode plan + 24 layer calls (KV write + decode)",
+            "layers": graph_layers,
+            "us_per_step": round(us_graph, 2),
+            "us_per_layer_call": round(us_graph / graph_layers, 3),
+            "host_inclusive_us_per_step": round(us_graph_wall, 2),
+        },
         "rope_write": {
             "what": "RoPE of the step's q and new k + KV write (qwen_runner.py:164-170)",
             "fused_us": round(us_rope, 3),

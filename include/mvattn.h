@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define MVATTN_ABI_VERSION 1
+#define MVATTN_ABI_VERSION 2
 
 /* Element types of query / key / value / cache / output. */
 #define MV_DTYPE_F32 0
@@ -146,14 +146,35 @@ int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t t
  *   status      [MV_PLAN_WORDS] (MV_PLAN_NUM_ITEMS = work groups to launch,
  *               MV_PLAN_PARTITION_TOKENS = P, MV_PLAN_MAX_PARTS = most pieces
  *               of one sequence).
- * One work group; enqueue only.
+ * fixed_partition_tokens = 0 sizes the id lists for this step's P (the
+ * host reads the status back before launching the decode). A value > 0
+ * (from mv_decode_graph_bounds) is for a launch of fixed size that never
+ * reads the status on the host, e.g. inside a captured HIP graph: the
+ * lists take that bound's stride, and the work_items slots from
+ * status[MV_PLAN_NUM_ITEMS] up to work_capacity get sequence -1, which the
+ * decode kernel skips. Enqueues the plan (one work group) and the block-id
+ * list (many work groups); never synchronises.
  */
 int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                    int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs, int32_t max_blocks,
                    int32_t block_size, int64_t num_blocks, int32_t num_kv_heads,
-                   int32_t groups_per_cu, int32_t cu_count,
+                   int32_t groups_per_cu, int32_t cu_count, int32_t fixed_partition_tokens,
                    int32_t* work_items, int64_t work_capacity, int32_t* block_ids,
                    int64_t block_ids_capacity, int32_t* counters, int32_t* status, void* stream);
+
+/*
+ * Sizes of a decode launch of fixed size, for batches of at most num_seqs
+ * sequences and max_blocks table entries each (no counterpart in the
+ * reference: it lets a caller launch the decode without reading the plan's
+ * status back, as a captured graph must). out[0] = work groups to launch
+ * (the plan never makes more; unused slots are marked and exit at once),
+ * out[1] = fixed_partition_tokens for mv_decode_plan and partition_tokens
+ * for mv_paged_decode, out[2] = max_partitions for mv_paged_decode and
+ * its workspace.
+ */
+int mv_decode_graph_bounds(int32_t num_seqs, int32_t max_blocks, int32_t block_size,
+                           int32_t num_kv_heads, int32_t groups_per_cu, int32_t cu_count,
+                           int64_t* out);
 
 /* Ints of block_ids storage mv_decode_plan needs (an upper bound for any
  * kv_len and piece size). */

@@ -144,7 +144,8 @@ struct DecodeArgs {
   int32_t num_kv_heads, n_rep, bs_log2;
   float scale_log2;                     // scale * log2(e)
   int32_t num_q_heads, max_parts;
-  int64_t num_blocks;
+  uint32_t num_blocks_u32;  // pool blocks (at most 2^31): ids at or above are not read
+  uint32_t unused;
   int32_t* counters;  // [num_seqs * num_kv_heads], zero at rest
   void* out;
   int64_t out_stride_tok, out_stride_head;  // elements
@@ -333,6 +334,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const int4 w1 = reinterpret_cast<const int4*>(a.work + 8 * static_cast<int64_t>(item))[1];
   wait_vmcnt<0>();
   asm volatile("" ::: "memory");
+  if (w0.x < 0) return;      // an unused slot of a fixed-size launch (no copy in flight)
   const int b = w0.x;        // sequence
   const int h = w0.y;        // kv head
   const int part = w0.z;     // piece of the sequence
@@ -387,7 +389,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       const int j = tile_tok + slot_row[c];
       const int jj = min(j, tok_end - 1);
       const int id = s_ids[min((jj >> a.bs_log2) - first_blk, kIdCap - 1)];  // -1: not a pool block
-      const bool ok = j < tok_end && id >= 0;
+      const bool ok = j < tok_end && static_cast<uint32_t>(id) < a.num_blocks_u32;  // -1 and stale ids fail
       off[c] = ok ? (((static_cast<int64_t>(id) * a.num_kv_heads + h) << a.bs_log2) + (jj & bs_mask)) *
                             Tr::kRowBytes +
                         slot_piece[c] * 16
@@ -680,6 +682,7 @@ struct PlanArgs {
   const void* block_table;
   int64_t bt_stride;
   int32_t num_seqs, max_blocks, bs_log2, num_kv_heads, groups_per_cu, cu_count;
+  int32_t fixed_part_tokens;  // > 0: ids stride for this piece bound, unused slots marked
   int64_t num_blocks;
   int32_t* work;      // [work_cap][8]: one entry per work group (launch slot)
   int64_t work_cap;   // entries
@@ -1058,11 +1061,24 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     }
   }
 
-  // ---- 5. block ids per slot: decode_ids_kernel, when the list fits
-  const int per_item = ids_per_item(part_tokens, a.bs_log2);
+  // ---- 5. block ids per slot: decode_ids_kernel, when the list fits.
+  // With a fixed piece bound (a launch of fixed size, e.g. in a captured
+  // graph) the id lists have that bound's stride, and the slots past the
+  // last work group get an entry with sequence -1, which the decode kernel
+  // skips.
+  const bool fixed = a.fixed_part_tokens > 0;
+  const int per_item = ids_per_item(fixed ? a.fixed_part_tokens : part_tokens, a.bs_log2);
   const int64_t n_ids = used_groups * per_item;
   const bool listed = used_groups == num_groups && n_ids <= a.ids_cap &&
-                      n_ids <= INT_MAX - kIdsPerPass;
+                      n_ids <= INT_MAX - kIdsPerPass &&
+                      (!fixed || part_tokens <= a.fixed_part_tokens);
+  if (fixed) {
+    for (int64_t slot = used_groups + tid; slot < a.work_cap; slot += kPlanThreads) {
+      int4* w = reinterpret_cast<int4*>(a.work + 8 * slot);
+      w[0] = make_int4(-1, 0, 0, 0);
+      w[1] = make_int4(0, 0, 0, 0);
+    }
+  }
   int64_t bad = 0;
   if (!listed) {  // uniform
     const int64_t n = static_cast<int64_t>(a.num_seqs) * a.max_blocks;
@@ -1203,6 +1219,38 @@ extern "C" int mv_decode_groups_per_cu(int32_t head_dim, int32_t dtype) {
   return mv::trait_value<mv::GroupsOf>(head_dim, dtype);
 }
 
+extern "C" int mv_decode_graph_bounds(int32_t num_seqs, int32_t max_blocks, int32_t block_size,
+                                      int32_t num_kv_heads, int32_t groups_per_cu,
+                                      int32_t cu_count, int64_t* out) {
+  using namespace mv;
+  if (!out) return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_graph_bounds: null out");
+  if (num_seqs <= 0 || max_blocks <= 0 || num_kv_heads <= 0 || cu_count <= 0)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_graph_bounds: bad sizes");
+  if (!is_pow2(block_size))
+    return fail(MV_ERR_UNSUPPORTED, "mv_decode_graph_bounds: block_size %d is not a power of 2",
+                block_size);
+  // The plan's piece bound L never exceeds l_cap, and never falls below
+  // min(l_cap, kWaves) (l_cap >= 31 here); its groups number at most the
+  // resident target when L comes from the search, else (L >= the fair
+  // share, or L = l_cap) at most units + total tiles / L.
+  const int bs_log2 = ilog2_exact(block_size);
+  const int64_t l_cap = std::max<int64_t>(
+      1, std::min<int64_t>(INT_MAX / 32, (static_cast<int64_t>(kIdCap - 1) << bs_log2) / kTile));
+  const int64_t max_tiles = (static_cast<int64_t>(max_blocks) * block_size + kTile - 1) / kTile;
+  const int64_t max_parts =
+      std::max<int64_t>(1, std::min<int64_t>(kMaxParts, (max_tiles + kWaves - 1) / kWaves));
+  const int64_t units = static_cast<int64_t>(num_kv_heads) * num_seqs;
+  const int64_t target = static_cast<int64_t>(std::max(2, groups_per_cu)) * cu_count;
+  const int64_t by_fair = units + std::max<int64_t>(target, (units * max_tiles + l_cap - 1) / l_cap);
+  const int64_t groups = std::min<int64_t>(by_fair, units * max_parts);
+  if (groups > INT_MAX / 8)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_graph_bounds: batch too large");
+  out[0] = groups;
+  out[1] = l_cap * kTile;
+  out[2] = max_parts;
+  return MV_OK;
+}
+
 extern "C" int64_t mv_decode_block_ids_capacity(int32_t num_seqs, int32_t max_blocks,
                                                 int32_t num_kv_heads, int64_t work_capacity) {
   if (num_seqs < 0 || max_blocks < 0 || num_kv_heads < 0 || work_capacity < 0) return 0;
@@ -1227,7 +1275,8 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
                               int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs,
                               int32_t max_blocks, int32_t block_size, int64_t num_blocks,
                               int32_t num_kv_heads, int32_t groups_per_cu,
-                              int32_t cu_count, int32_t* work_items, int64_t work_capacity,
+                              int32_t cu_count, int32_t fixed_partition_tokens,
+                              int32_t* work_items, int64_t work_capacity,
                               int32_t* block_ids,
                               int64_t block_ids_capacity, int32_t* counters, int32_t* status,
                               void* stream) {
@@ -1257,6 +1306,7 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
   a.num_kv_heads = num_kv_heads;
   a.groups_per_cu = groups_per_cu;
   a.cu_count = cu_count;
+  a.fixed_part_tokens = fixed_partition_tokens;
   a.num_blocks = num_blocks;
   a.work = work_items;
   a.work_cap = work_capacity;
@@ -1368,7 +1418,8 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
   a.n_rep = n_rep;
   a.bs_log2 = bs_log2;
   a.max_parts = max_partitions;
-  a.num_blocks = num_blocks;
+  a.num_blocks_u32 = static_cast<uint32_t>(std::min<int64_t>(num_blocks, int64_t(1) << 31));
+  a.unused = 0;
   a.ws_o = nullptr;
   a.ws_ml = nullptr;
   if (max_partitions > 1) {

@@ -14,7 +14,7 @@ import threading
 
 import torch  # noqa: F401  (must be loaded before the kernel library)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MV_OK = 0
 MV_ERR_INVALID_ARGUMENT = -1
@@ -62,10 +62,11 @@ SIGNATURES = {
     "mv_decode_plan": (ctypes.c_int, [
         _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride
         _I32, _I32, _I32, _I64,    # num_seqs, max_blocks, block_size, num_blocks
-        _I32, _I32, _I32,          # num_kv_heads, groups_per_cu, cu_count
+        _I32, _I32, _I32, _I32,    # num_kv_heads, groups_per_cu, cu_count, fixed_partition_tokens
         _P, _I64, _P, _I64,        # work_items, capacity, block_ids, capacity
         _P, _P, _P,                # counters, status, stream
     ]),
+    "mv_decode_graph_bounds": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _I32, _P]),
     "mv_decode_block_ids_capacity": (_I64, [_I32, _I32, _I32, _I64]),
     "mv_paged_decode_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
     "mv_paged_decode": (ctypes.c_int, [

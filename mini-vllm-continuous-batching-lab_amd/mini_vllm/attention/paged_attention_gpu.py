@@ -45,6 +45,8 @@ SUPPORTED_DTYPES = tuple(_hip.MV_DTYPE)
 __all__ = [
     "AttentionBackendGPU",
     "DecodePlan",
+    "check_deferred",
+    "clear_deferred",
     "gather_prefix_kv",
     "hip_cache_write",
     "hip_decode_attention",
@@ -121,6 +123,47 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+# ----------------------------------------------------------------------------
+# Checks inside a captured graph
+#
+# While a stream is being captured into a HIP graph nothing may wait for the
+# device, so the slot, position and plan checks cannot read their status
+# words back. They are captured like every other kernel; each records its
+# status tensor here, and check_deferred() reads them after a replay.
+# ----------------------------------------------------------------------------
+
+
+def _capturing() -> bool:
+    return torch.cuda.is_current_stream_capturing()
+
+
+def _defer(raise_fn, status: torch.Tensor) -> None:
+    deferred = getattr(_state, "deferred", None)
+    if deferred is None:
+        deferred = _state.deferred = []
+    deferred.append((raise_fn, status))
+
+
+def check_deferred() -> None:
+    """Raise the first error found by the checks captured into a graph.
+
+    Call after replaying a captured step (it synchronises once): the same
+    exceptions as the eager calls (``IndexError`` / ``AssertionError`` for
+    slots, ``IndexError`` for positions, ``ValueError`` / ``IndexError`` /
+    ``RuntimeError`` for the decode metadata) describe the data of the last
+    replay. The kernels themselves skip what the checks report (slots and
+    block ids outside the pool, sequences without a valid length), so a bad
+    replay produces wrong rows, never an out-of-bounds access.
+    """
+    for raise_fn, status in getattr(_state, "deferred", None) or []:
+        raise_fn(status.tolist())
+
+
+def clear_deferred() -> None:
+    """Forget the recorded checks (e.g. when a captured graph is dropped)."""
+    _state.deferred = []
+
+
 # ============================================================================
 # KV-cache write
 # ============================================================================
@@ -134,8 +177,10 @@ def _check_slots(slot_mapping: torch.Tensor, total_slots: int) -> None:
     non-(-1) slots: ``AssertionError`` with "Duplicate" (reference
     paged_attention_gpu.py:126-135). Both checks run in one device kernel.
     """
+    capturing = _capturing()
+    name = "slots_graph" if capturing else "slots"
     extra = (total_slots,)
-    if _cache_get("slots", (slot_mapping,), extra) is not None:
+    if _cache_get(name, (slot_mapping,), extra) is not None:
         return
     lib = _hip.load()
     device = slot_mapping.device
@@ -146,18 +191,25 @@ def _check_slots(slot_mapping: torch.Tensor, total_slots: int) -> None:
         ),
         "mv_kv_slots_check",
     )
-    bad, dups = status.tolist()
-    if bad:
-        raise IndexError(
-            f"slot_mapping has {bad} slot(s) out of range [0, {total_slots}) "
-            f"(-1 marks a skipped token)"
-        )
-    if dups:
-        raise AssertionError(
-            f"Duplicate slots in slot_mapping: {dups} duplicate pair(s). "
-            f"The HIP cache write forbids duplicate slots."
-        )
-    _cache_put("slots", (slot_mapping,), extra, True)
+
+    def raise_slots(st) -> None:
+        bad, dups = st
+        if bad:
+            raise IndexError(
+                f"slot_mapping has {bad} slot(s) out of range [0, {total_slots}) "
+                f"(-1 marks a skipped token)"
+            )
+        if dups:
+            raise AssertionError(
+                f"Duplicate slots in slot_mapping: {dups} duplicate pair(s). "
+                f"The HIP cache write forbids duplicate slots."
+            )
+
+    if capturing:
+        _defer(raise_slots, status)
+    else:
+        raise_slots(status.tolist())
+    _cache_put(name, (slot_mapping,), extra, True)
 
 
 def hip_cache_write(
@@ -278,11 +330,18 @@ def plan_decode(
     kernel silently skips -1 entries). One host synchronisation per
     distinct (block_table, kv_len_after) pair; later calls with the same,
     unmodified tensors (the other layers of the step) reuse the plan.
+
+    While the current stream is being captured into a graph the plan
+    cannot be read back: it is enqueued for a launch of fixed size
+    (``mv_decode_graph_bounds``), and its checks raise from
+    ``check_deferred()`` after a replay instead.
     """
     lib = _hip.load()
     split = _groups_per_cu(device, head_dim, dtype)
+    capturing = _capturing()
+    name = "plan_graph" if capturing else "plan"
     extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads, split)
-    cached = _cache_get("plan", (block_table, kv_len_after), extra)
+    cached = _cache_get(name, (block_table, kv_len_after), extra)
     if cached is not None:
         return cached
     bt = block_table
@@ -303,9 +362,19 @@ def plan_decode(
 
     num_seqs = kv.shape[0]
     max_blocks = bt.shape[1] if bt.dim() == 2 else 0
-    cap = num_seqs * num_kv_heads * max(1, math.ceil(max_blocks * block_size / 16))
+    fixed = 0
+    if capturing and num_seqs > 0 and max_blocks > 0:
+        bounds = (ctypes.c_int64 * 3)()
+        _hip.check(lib.mv_decode_graph_bounds(num_seqs, max_blocks, block_size, num_kv_heads,
+                                              *split, bounds), "mv_decode_graph_bounds")
+        cap, fixed, fixed_parts = bounds
+        per_item = ((fixed + block_size - 1) // block_size + 1 + 3) // 4 * 4
+        ids_cap = max(lib.mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, cap),
+                      cap * per_item)
+    else:
+        cap = num_seqs * num_kv_heads * max(1, math.ceil(max_blocks * block_size / 16))
+        ids_cap = lib.mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, cap)
     work = torch.empty(8 * max(cap, 1), dtype=torch.int32, device=device)
-    ids_cap = lib.mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, cap)
     block_ids = torch.empty(max(ids_cap, 4), dtype=torch.int32, device=device)
     counters = torch.empty(max(num_seqs * num_kv_heads, 1), dtype=torch.int32, device=device)
     status = torch.empty(_hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
@@ -313,34 +382,45 @@ def plan_decode(
         lib.mv_decode_plan(
             _ptr(kv), int(kv.dtype == torch.int64), _ptr(bt), int(bt.dtype == torch.int64),
             bt.stride(0) if bt.dim() == 2 else 0, num_seqs, max_blocks, block_size,
-            num_blocks, num_kv_heads, *split,
+            num_blocks, num_kv_heads, *split, fixed,
             _ptr(work), cap, _ptr(block_ids), block_ids.numel(),
             _ptr(counters), _ptr(status), _stream(device),
         ),
         "mv_decode_plan",
     )
-    st = status.tolist()
-    if st[_hip.MV_PLAN_BAD_KV_LEN]:
-        raise ValueError(
-            f"kv_len_after must be >= 1 for all decode sequences, "
-            f"got min={st[_hip.MV_PLAN_MIN_KV_LEN]}"
-        )
-    if st[_hip.MV_PLAN_INSUFFICIENT]:
-        raise IndexError(
-            f"block_table with {max_blocks} blocks per row (block_size={block_size}) is "
-            f"insufficient to cover kv_len_after for {st[_hip.MV_PLAN_INSUFFICIENT]} sequence(s)"
-        )
-    if st[_hip.MV_PLAN_BAD_BLOCK]:
-        raise IndexError(
-            f"block_table has {st[_hip.MV_PLAN_BAD_BLOCK]} entr(ies) within kv_len_after "
-            f"that are not pool blocks [0, {num_blocks})"
-        )
-    num_groups = st[_hip.MV_PLAN_NUM_ITEMS]
-    if num_groups > cap or st[_hip.MV_PLAN_IDS_PER_ITEM] < 0:
-        raise RuntimeError(f"decode plan: {num_groups} work groups exceed the plan capacity {cap}")
-    plan = DecodePlan(work, block_ids, counters, num_groups, st[_hip.MV_PLAN_MAX_PARTS],
-                      st[_hip.MV_PLAN_PARTITION_TOKENS])
-    _cache_put("plan", (block_table, kv_len_after), extra, plan)
+
+    def raise_plan(st) -> None:
+        if st[_hip.MV_PLAN_BAD_KV_LEN]:
+            raise ValueError(
+                f"kv_len_after must be >= 1 for all decode sequences, "
+                f"got min={st[_hip.MV_PLAN_MIN_KV_LEN]}"
+            )
+        if st[_hip.MV_PLAN_INSUFFICIENT]:
+            raise IndexError(
+                f"block_table with {max_blocks} blocks per row (block_size={block_size}) is "
+                f"insufficient to cover kv_len_after for {st[_hip.MV_PLAN_INSUFFICIENT]} "
+                f"sequence(s)"
+            )
+        if st[_hip.MV_PLAN_BAD_BLOCK]:
+            raise IndexError(
+                f"block_table has {st[_hip.MV_PLAN_BAD_BLOCK]} entr(ies) within kv_len_after "
+                f"that are not pool blocks [0, {num_blocks})"
+            )
+        if st[_hip.MV_PLAN_NUM_ITEMS] > cap or st[_hip.MV_PLAN_IDS_PER_ITEM] < 0:
+            raise RuntimeError(
+                f"decode plan: {st[_hip.MV_PLAN_NUM_ITEMS]} work groups exceed the plan "
+                f"capacity {cap}"
+            )
+
+    if fixed:
+        _defer(raise_plan, status)
+        plan = DecodePlan(work, block_ids, counters, cap, fixed_parts, fixed)
+    else:
+        st = status.tolist()
+        raise_plan(st)
+        plan = DecodePlan(work, block_ids, counters, st[_hip.MV_PLAN_NUM_ITEMS],
+                          st[_hip.MV_PLAN_MAX_PARTS], st[_hip.MV_PLAN_PARTITION_TOKENS])
+    _cache_put(name, (block_table, kv_len_after), extra, plan)
     return plan
 
 
@@ -431,8 +511,10 @@ def _check_positions(positions: torch.Tensor, max_positions: int) -> None:
     reference's lookup ``self._cos[positions]`` raises
     (mini_vllm/model/rotary.py:64-65). One device check per distinct
     positions tensor (the layers of a step share it)."""
+    capturing = _capturing()
+    name = "positions_graph" if capturing else "positions"
     extra = (max_positions,)
-    if _cache_get("positions", (positions,), extra) is not None:
+    if _cache_get(name, (positions,), extra) is not None:
         return
     lib = _hip.load()
     device = positions.device
@@ -442,12 +524,16 @@ def _check_positions(positions: torch.Tensor, max_positions: int) -> None:
                                _stream(device)),
         "mv_positions_check",
     )
-    bad = status.item()
-    if bad:
-        raise IndexError(
-            f"{bad} position(s) outside the rotary tables [0, {max_positions})"
-        )
-    _cache_put("positions", (positions,), extra, True)
+
+    def raise_positions(st) -> None:
+        if st[0]:
+            raise IndexError(f"{st[0]} position(s) outside the rotary tables [0, {max_positions})")
+
+    if capturing:
+        _defer(raise_positions, status)
+    else:
+        raise_positions(status.tolist())
+    _cache_put(name, (positions,), extra, True)
 
 
 def _rope_operand(x: torch.Tensor) -> torch.Tensor:

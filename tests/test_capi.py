@@ -59,7 +59,7 @@ def test_every_declared_symbol_is_exported_and_typed(lib):
 
 
 def test_abi_queries(lib):
-    assert lib.mv_abi_version() == _hip.ABI_VERSION == 1
+    assert lib.mv_abi_version() == _hip.ABI_VERSION == 2
     assert lib.mv_decode_chunk_tokens(64, 2) == 64       # 4 waves x one 16-token tile
     assert lib.mv_decode_chunk_tokens(128, 0) == 64
     assert lib.mv_decode_chunk_tokens(96, 2) == 0
@@ -103,10 +103,27 @@ def test_block_ids_capacity(lib):
 
 def test_plan_rejects_small_block_ids_buffer_on_host(lib):
     # dummy addresses: the call fails on the capacity before anything is launched
-    rc = lib.mv_decode_plan(16, 1, 16, 1, 8, 4, 8, 16, 100, 2, 3, 256,
+    rc = lib.mv_decode_plan(16, 1, 16, 1, 8, 4, 8, 16, 100, 2, 3, 256, 0,
                             16, 8, 16, 10, 16, 16, None)
     assert rc == _hip.MV_ERR_INVALID_ARGUMENT
     assert b"block_ids capacity" in lib.mv_last_error()
+
+
+def test_graph_bounds(lib):
+    import ctypes
+    out = (ctypes.c_int64 * 3)()
+    # c2-like: 64 sequences x 128 entries of 16 tokens, 2 kv heads, 3 groups/CU, 256 CUs
+    assert lib.mv_decode_graph_bounds(64, 128, 16, 2, 3, 256, out) == 0
+    groups, part, parts = list(out)
+    assert part == 511 * 16  # the widest piece: 511 table entries
+    assert parts == 128 // 4  # pieces of at least 4 tiles
+    # units + max(resident target, units * tiles / widest piece), capped by units * parts
+    assert groups == min(128 + max(3 * 256, -(-128 * 128 // 511)), 128 * parts)
+    # tiny tables: at most one piece per sequence
+    assert lib.mv_decode_graph_bounds(10, 2, 16, 2, 3, 256, out) == 0
+    assert list(out)[0] == 20 and list(out)[2] == 1
+    assert lib.mv_decode_graph_bounds(4, 8, 12, 2, 3, 256, out) == _hip.MV_ERR_UNSUPPORTED
+    assert lib.mv_decode_graph_bounds(0, 8, 16, 2, 3, 256, out) == _hip.MV_ERR_INVALID_ARGUMENT
 
 
 def test_decode_param_list_matches_header():

@@ -1,0 +1,162 @@
+"""A decode step captured into a HIP graph and replayed with new metadata.
+
+The step is three layers of (KV write, paged decode) on static tensors. The
+capture runs the plan without reading it back (a launch of fixed size,
+unused slots marked); each replay plans again from whatever the static
+block table / kv_len / slot tensors hold. Every replay is checked against
+the oracle, with eager work (the metadata copies) between replays, and the
+checks captured with the step report bad metadata through check_deferred().
+"""
+
+import pytest
+import torch
+
+from gpu_util import DEV, TOL, bits, say
+from mini_vllm.attention import paged_attention_gpu as pg
+from oracle import paged_ref
+
+pytestmark = pytest.mark.gpu
+
+NB, BS, MB, B, HQ, HKV, D, LAYERS = 2048, 16, 64, 24, 14, 2, 64, 3
+DT = torch.bfloat16
+
+
+def _case(seed, lo, hi):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (B,), generator=g)
+    need = [(int(n) + BS - 1) // BS for n in lens]
+    perm = torch.randperm(NB, generator=g)
+    bt = torch.full((B, MB), -1, dtype=torch.int64)
+    pos = 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[pos:pos + n]
+        pos += n
+    last = lens - 1
+    slots = bt[torch.arange(B), last // BS] * BS + last % BS
+    layers = []
+    for _ in range(LAYERS):
+        layers.append(dict(
+            q=torch.randn(B, HQ, D, generator=g).to(DT),
+            nk=torch.randn(B, HKV, D, generator=g).to(DT),
+            nv=torch.randn(B, HKV, D, generator=g).to(DT),
+            kc=torch.randn(NB, HKV, BS, D, generator=g).to(DT),
+            vc=torch.randn(NB, HKV, BS, D, generator=g).to(DT),
+        ))
+    return dict(bt=bt, kv=lens.to(torch.int64), slots=slots, layers=layers)
+
+
+def _oracle(case):
+    res = []
+    for L in case["layers"]:
+        kc, vc = L["kc"].clone(), L["vc"].clone()
+        paged_ref.write_to_paged_cache(L["nk"], L["nv"], kc, vc, case["slots"], BS)
+        out = paged_ref.decode_from_tables(L["q"].float(), kc.float(), vc.float(), case["bt"],
+                                           case["kv"], BS)
+        res.append((out, kc, vc))
+    return res
+
+
+class _Static:
+    """Device tensors whose addresses the graph keeps; cases are copied in."""
+
+    def __init__(self):
+        self.bt = torch.empty(B, MB, dtype=torch.int64, device=DEV)
+        self.kv = torch.empty(B, dtype=torch.int64, device=DEV)
+        self.slots = torch.empty(B, dtype=torch.int64, device=DEV)
+        self.layers = [dict(q=torch.empty(B, HQ, D, dtype=DT, device=DEV),
+                            nk=torch.empty(B, HKV, D, dtype=DT, device=DEV),
+                            nv=torch.empty(B, HKV, D, dtype=DT, device=DEV),
+                            kc=torch.empty(NB, HKV, BS, D, dtype=DT, device=DEV),
+                            vc=torch.empty(NB, HKV, BS, D, dtype=DT, device=DEV))
+                       for _ in range(LAYERS)]
+
+    def load(self, case):
+        self.bt.copy_(case["bt"])
+        self.kv.copy_(case["kv"])
+        self.slots.copy_(case["slots"])
+        for dst, src in zip(self.layers, case["layers"]):
+            for k in dst:
+                dst[k].copy_(src[k])
+
+    def step(self):
+        outs = []
+        for L in self.layers:
+            pg.hip_cache_write(L["nk"], L["nv"], L["kc"], L["vc"], self.slots, BS)
+            outs.append(pg.hip_decode_attention(L["q"], L["kc"], L["vc"], self.bt, self.kv, BS))
+        return outs
+
+
+def _check(st, outs, ref, tag):
+    for layer, (L, out, (o_ref, kc_ref, vc_ref)) in enumerate(zip(st.layers, outs, ref)):
+        err = (out.float().cpu() - o_ref).abs().max().item()
+        assert err <= TOL[DT], (tag, layer, err)
+        assert torch.equal(bits(L["kc"].cpu()), bits(kc_ref)), (tag, layer)
+        assert torch.equal(bits(L["vc"].cpu()), bits(vc_ref)), (tag, layer)
+
+
+def test_captured_step_replays_new_metadata():
+    say("graph: capture")
+    pg.clear_deferred()
+    case_a, case_b = _case(1, 1, MB * BS), _case(2, 300, 700)
+    ref_a, ref_b = _oracle(case_a), _oracle(case_b)
+    st = _Static()
+    st.load(case_a)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # eager warm-up: library, workspace, split
+        st.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = st.step()
+    for tag, case, ref in (("A", case_a, ref_a), ("B", case_b, ref_b), ("A again", case_a, ref_a)):
+        say("graph: replay", tag)
+        st.load(case)
+        graph.replay()
+        torch.cuda.synchronize()
+        pg.check_deferred()
+        _check(st, outs, ref, tag)
+
+    say("graph: replay with a zero kv_len")
+    bad = dict(case_b)
+    bad["kv"] = case_b["kv"].clone()
+    bad["kv"][3] = 0
+    st.load(bad)
+    graph.replay()
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError, match="kv_len"):
+        pg.check_deferred()
+
+    say("graph: replay with a table entry outside the pool")
+    bad = dict(case_b)
+    bad["bt"] = case_b["bt"].clone()
+    bad["bt"][5, 0] = NB + 7
+    st.load(bad)
+    graph.replay()
+    torch.cuda.synchronize()
+    with pytest.raises(IndexError, match="not pool blocks"):
+        pg.check_deferred()
+
+    say("graph: replay B after the bad ones")
+    st.load(case_b)
+    graph.replay()
+    torch.cuda.synchronize()
+    pg.check_deferred()
+    _check(st, outs, ref_b, "B last")
+    del graph
+    pg.clear_deferred()
+
+
+def test_eager_calls_after_capture_still_validate():
+    say("graph: eager after capture")
+    case = _case(3, 50, 400)
+    st = _Static()
+    st.load(case)
+    ref = _oracle(case)
+    outs = st.step()
+    torch.cuda.synchronize()
+    _check(st, outs, ref, "eager")
+    st.kv[0] = 0  # in-place edit: the next call plans (and checks) again
+    with pytest.raises(ValueError, match="kv_len"):
+        st.step()
