@@ -279,6 +279,40 @@ int mv_rope_kv_cache_write(const void* query, int64_t q_stride_tok, int64_t q_st
 int mv_positions_check(const int64_t* positions, int64_t num_tokens, int64_t max_positions,
                        int32_t* status, void* stream);
 
+/* Query tokens one mv_paged_prefill work group covers for this head shape
+ * (0: unsupported; at most 16 query heads per kv head at head_dim 128, 32
+ * at 64). */
+int mv_prefill_tokens_per_group(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim);
+
+/*
+ * Chunked-prefill attention over the paged pool.
+ * Replaces `AttentionBackendGPU.prefill_attention`
+ * (mini_vllm/attention/paged_attention_gpu.py:577-661): its per-sequence
+ * gather of the cached prefix (`gather_prefix_kv` / `_gather_prefix_kv_kernel`
+ * :330-446), `cat` with the chunk, `repeat_interleave` and masked SDPA,
+ * with one launch and no gathered copy. For sequence i,
+ *   seqs[4i .. 4i+3] = (table row, cached tokens, first chunk row, chunk tokens)  int64
+ * and chunk token t (row first + t of query / key / value / out) attends
+ * keys 0 .. cached + t: prefix keys from the pool through block_table row
+ * (int64 or int32, row stride bt_stride; every entry a prefix needs must
+ * be a pool block -- the caller checks), chunk keys from key / value.
+ *   work_items  int32[4] per work group: (sequence, kv head, first chunk
+ *               token, tokens <= mv_prefill_tokens_per_group); the caller
+ *               lists every (sequence, kv head, token block) once, in any
+ *               order (longest first balances best);
+ *   out         [rows, num_q_heads, head_dim], query dtype.
+ * head_dim 64 or 128, power-of-two block_size, 16-byte aligned rows.
+ */
+int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                     const void* key, int64_t k_stride_tok, int64_t k_stride_head,
+                     const void* value, int64_t v_stride_tok, int64_t v_stride_head,
+                     const void* key_cache, const void* value_cache, const void* block_table,
+                     int32_t bt_is_i64, int64_t bt_stride, const int64_t* seqs, int32_t num_seqs,
+                     const int32_t* work_items, int32_t num_work_groups, void* out,
+                     int64_t out_stride_tok, int64_t out_stride_head, float scale,
+                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,158 @@
+// Tile building blocks shared by the paged decode and prefill kernels
+// (gfx950, wave64 + MFMA): 16-token K/V tiles staged in LDS by direct
+// HBM -> LDS copies under an XOR piece swizzle, the S^T = K Q^T and
+// O += P V MFMA tile updates, and exact vmcnt waits.
+#pragma once
+
+#include "mv_common.h"
+
+namespace mv {
+namespace {
+
+constexpr int kTile = 16;       // tokens per K/V tile (MFMA M of S^T)
+constexpr int kMaxGroup = 16;   // MFMA N: query rows per tile
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// Geometry of one 16-token tile of one head.
+template <int DTYPE, int D>
+struct TileGeom {
+  static constexpr int kElemBytes = Elem<DTYPE>::bytes;
+  static constexpr int kRowBytes = D * kElemBytes;     // one token row of one head
+  static constexpr int kTileBytes = kTile * kRowBytes;  // 2 KiB (D=64, 16-bit) .. 8 KiB
+  static constexpr int kLoads = kTileBytes / 1024;      // 1 KiB load instructions per tile
+  static constexpr int kRowPieces = kRowBytes / 16;     // 16-byte pieces per row: 8, 16, 32
+  static constexpr int kLaneElems = D / 4;              // MFMA: dims per lane per token
+  static constexpr int kLanePieces = kLaneElems * kElemBytes / 16;
+  static constexpr int kElemsPerPiece = 16 / kElemBytes;
+};
+
+// Swizzle of the 16-byte pieces of LDS row r: slot s holds piece s ^ sw(r).
+// With it, a K-operand read (16 rows, one piece each) and a transposed V
+// read (rows 4g+e, two to four neighbouring pieces each) touch 16 distinct
+// 4-bank groups.
+template <int ROW_PIECES>
+__device__ __forceinline__ int piece_swizzle(int r) {
+  return ROW_PIECES == 8 ? (r >> 1) & 7 : r & 15;
+}
+
+// S^T tile update: acc += K(16 tokens x 32 dims) * Q^T(32 dims x 16 heads)
+// for the 16-bit types; one call per 16-byte piece of the lane's dims.
+template <int DTYPE>
+__device__ __forceinline__ f32x4 mfma_qk(const uint4& k, const uint4& q, f32x4 acc);
+template <>
+__device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_BF16>(const uint4& k, const uint4& q, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, k),
+                                                  __builtin_bit_cast(bf16x8, q), acc, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_F16>(const uint4& k, const uint4& q, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, k),
+                                                 __builtin_bit_cast(f16x8, q), acc, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_F32>(const uint4& k, const uint4& q, f32x4 acc) {
+  // 4 dims per 16-byte piece, one 16x16x4 fp32 MFMA per dim slot.
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.x), __uint_as_float(q.x), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.y), __uint_as_float(q.y), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.z), __uint_as_float(q.z), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.w), __uint_as_float(q.w), acc, 0, 0, 0);
+  return acc;
+}
+
+// O tile update for one 16-token tile from its swizzled LDS tile:
+// o[c] += P(16 heads x 16 tokens) V(16 tokens x 16 dims), V element
+// (row 4g+e, column 16c+t) per lane.
+template <int DTYPE, int D>
+__device__ __forceinline__ void mfma_pv(const float (&p)[4], const char* v_tile, int g, int t,
+                                        f32x4 (&o)[D / 16]) {
+  using Tr = TileGeom<DTYPE, D>;
+  constexpr int RP = Tr::kRowPieces;
+  constexpr int EPP = Tr::kElemsPerPiece;
+  int row_base[4], row_sw[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    row_base[e] = (4 * g + e) * RP * 16;
+    row_sw[e] = piece_swizzle<RP>(4 * g + e);
+  }
+  if constexpr (DTYPE == MV_DTYPE_F32) {
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      const int col = 16 * c + t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int off = row_base[e] + (((col / EPP) ^ row_sw[e]) << 4) + (col % EPP) * 4;
+        const float vv = *reinterpret_cast<const float*>(v_tile + off);
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[e], vv, o[c], 0, 0, 0);
+      }
+    }
+  } else {
+    s16x4 pa;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pa[e] = static_cast<short>(from_f32<DTYPE>(p[e]));
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      const int col = 16 * c + t;
+      s16x4 vb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int off = row_base[e] + (((col / EPP) ^ row_sw[e]) << 4) + (col % EPP) * 2;
+        vb[e] = *reinterpret_cast<const short*>(v_tile + off);
+      }
+      if constexpr (DTYPE == MV_DTYPE_BF16) {
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[c], 0, 0, 0);
+      } else {
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa),
+                                                    __builtin_bit_cast(f16x4, vb), o[c], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this
+// wave's vector memory operations, stores included, are complete.
+constexpr unsigned kWaitVmcnt0 = 0x0F70;
+
+// s_waitcnt vmcnt(N), N <= 63 (expcnt and lgkmcnt at their maxima; vmcnt
+// is split over bits [3:0] and [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+}
+
+// Waits until at most R * PER vector memory instructions of this wave are
+// outstanding, R <= RMAX (R is wave-uniform, the count an immediate).
+template <int PER, int RMAX>
+__device__ __forceinline__ void wait_vmcnt_groups(int r) {
+  if constexpr (RMAX == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (r >= RMAX) wait_vmcnt<PER * RMAX>();
+    else wait_vmcnt_groups<PER, RMAX - 1>(r);
+  }
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
+}
+
+// HBM -> LDS copy of 16 bytes per lane: lane l's bytes land at LDS address
+// lds_base + 16 l (lds_base wave-uniform, passed in M0). Written as inline
+// asm on purpose: the compiler then does not see a pending LDS write and
+// does not put a vmcnt(0) in front of every later LDS access (which would
+// wait for the tiles still streaming into the other buffers); the tile loop
+// counts these loads itself. The "memory" clobber keeps LDS accesses of the
+// wave on their side of the copy.
+__device__ __forceinline__ void copy_to_lds_16B(const char* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+
+template <int C>
+struct IntC {
+  static constexpr int value = C;
+};
+
+}  // namespace
+}  // namespace mv

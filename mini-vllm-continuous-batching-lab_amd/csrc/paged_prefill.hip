@@ -1,0 +1,412 @@
+// Paged prefill attention for gfx950 (MI355X), wave64 + MFMA.
+//
+// Math (AttentionBackendGPU.prefill_attention,
+// mini_vllm/attention/paged_attention_gpu.py:577-661): for every prefill
+// sequence with `cached` tokens already in the pool and a chunk of
+// `q_len` new tokens,
+//   keys 0 .. cached-1     from the pool (table row `seq_indices[i]`),
+//   keys cached .. +q_len  from the chunk's own key / value rows,
+//   out[t, hq] = softmax_j<=cached+t(scale * q[t, hq] . k_j) v_j,
+// kv head hk = hq / n_rep, scale = head_dim^-1/2 -- the reference's
+// gather + cat + repeat_interleave + masked SDPA, in one pass over the
+// keys with no gathered copy.
+//
+// Work decomposition: one work group of 4 waves per (sequence, kv head,
+// block of query tokens). A wave owns R x 16 MFMA rows (R = 2 at head_dim
+// 64, 1 at 128); row r is query head (h * n_rep + r % n_rep) of token
+// (r / n_rep) of the wave's tpw = 16 R / n_rep tokens, so one K/V pass serves the whole GQA
+// group of several tokens. The four waves share one stream of keys:
+//   * a stage is 64 keys: wave w copies sub-tile w (16 keys of K and V)
+//     from HBM straight to LDS (global_load_lds, XOR piece swizzle as in
+//     the decode kernel), kStages stages in flight;
+//   * after one barrier per stage every wave computes all four sub-tiles
+//     for its rows: S^T = K Q^T (MFMA), per-row causal mask key <= cached +
+//     token, online softmax, O += P V (MFMA);
+//   * prefix keys are addressed through the sequence's block ids, staged
+//     in LDS per window of kPfIdCap blocks; chunk keys through the chunk's
+//     row strides (q / k / v may be views of one fused QKV output).
+// Waves skip sub-tiles that lie wholly past their rows' causal limit.
+#include <algorithm>
+#include <climits>
+
+#include "mv_common.h"
+#include "mv_tile.h"
+
+namespace mv {
+namespace {
+
+constexpr int kPfWaves = 4;
+constexpr int kPfStageTokens = kPfWaves * kTile;  // keys per stage: one 16-key sub-tile per wave
+constexpr int kPfIdCap = 2048;                    // prefix block ids staged in LDS per window
+// 16-row MFMA tiles per wave: two at head_dim 64 (twice the rows per K/V
+// pass), one at 128 (the O accumulators of two would take every register).
+__host__ __device__ constexpr int pf_row_tiles(int d) { return d == 64 ? 2 : 1; }
+
+template <int DTYPE, int D>
+struct PfTraits : TileGeom<DTYPE, D> {
+  using G = TileGeom<DTYPE, D>;
+  static constexpr int kSubBytes = 2 * G::kTileBytes;  // K and V sub-tile of one wave
+  static constexpr int kStageBytes = kPfWaves * kSubBytes;
+  static constexpr int kStages = G::kTileBytes <= 2048 ? 3 : 2;
+  static constexpr int kIdsOffset = kStages * kStageBytes;
+  static constexpr int kLdsBytes = kIdsOffset + kPfIdCap * 4;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS of one work group");
+};
+
+struct PrefillArgs {
+  const int32_t* work;   // per work group: (sequence, kv head, first token, tokens)
+  const int64_t* seqs;   // per sequence: (table row, cached tokens, first chunk row, chunk tokens)
+  const void* q;
+  const char* k_new;
+  const char* v_new;
+  const char* k_cache;
+  const char* v_cache;
+  const void* block_table;
+  void* out;
+  int64_t q_st, q_sh;     // elements
+  int64_t k_st, k_sh;     // bytes
+  int64_t v_st, v_sh;     // bytes
+  int64_t o_st, o_sh;     // elements
+  int64_t bt_stride;      // elements
+  float scale_log2;
+  int32_t num_kv_heads, n_rep, tpw, bs_log2;
+  uint32_t num_blocks_u32;
+};
+
+template <int DTYPE, int D, typename BT>
+__global__ __launch_bounds__(kPfWaves * 64) void paged_prefill_kernel(PrefillArgs a) {
+  using Tr = PfTraits<DTYPE, D>;
+  using raw_t = typename Elem<DTYPE>::raw;
+  constexpr int L = Tr::kLoads;
+  constexpr int RP = Tr::kRowPieces;
+  constexpr int QP = Tr::kLanePieces;
+  constexpr int S = Tr::kStages;
+  constexpr int R = pf_row_tiles(D);
+
+  __shared__ __attribute__((aligned(16))) char s_lds[Tr::kLdsBytes];
+  int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
+  const uint32_t lds0 = lds_address(s_lds);
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int t = lane & 15;  // MFMA: key row (K operand) / query row (results)
+  const int g = lane >> 4;  // MFMA: dim quarter (K operand) / key quad (results)
+
+  const int4 w = reinterpret_cast<const int4*>(a.work)[blockIdx.x];
+  const int seq = w.x, h = w.y, tok0 = w.z, ntok = w.w;
+  const int64_t row = a.seqs[4 * seq];
+  const int cached = static_cast<int>(a.seqs[4 * seq + 1]);
+  const int64_t qbase = a.seqs[4 * seq + 2] + tok0;  // chunk row of token tok0
+  const int key_end = cached + tok0 + ntok;           // keys of the work group: [0, key_end)
+  const int bs_mask = (1 << a.bs_log2) - 1;
+
+  // ---- rows of this wave: limits and Q (registers, straight from HBM)
+  const int wtok0 = wave * a.tpw;
+  const int wtok_end = min(ntok, wtok0 + a.tpw);
+  // the last key any row of the wave sees (-1: the wave has no rows)
+  const int wave_limit = wtok0 < ntok ? cached + tok0 + wtok_end - 1 : -1;
+  int limit[R];
+  uint4 qr[R][QP];
+#pragma unroll
+  for (int rt = 0; rt < R; ++rt) {
+    const int r = rt * 16 + t;
+    const int rtok = wtok0 + r / a.n_rep;
+    const bool ok = r < a.tpw * a.n_rep && rtok < ntok;
+    limit[rt] = ok ? cached + tok0 + rtok : -1;  // -1: a padding row, never written
+    const int tq = ok ? rtok : 0;
+    const int head = h * a.n_rep + (ok ? r % a.n_rep : 0);
+    const char* qrow = reinterpret_cast<const char*>(static_cast<const raw_t*>(a.q) +
+                                                     (qbase + tq) * a.q_st + head * a.q_sh);
+#pragma unroll
+    for (int c = 0; c < QP; ++c) qr[rt][c] = *reinterpret_cast<const uint4*>(qrow + (g * QP + c) * 16);
+  }
+  // Q must have landed before the tile copies are counted by vmcnt.
+#pragma unroll
+  for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+    for (int c = 0; c < QP; ++c)
+      asm volatile("" ::"v"(qr[rt][c].x), "v"(qr[rt][c].y), "v"(qr[rt][c].z), "v"(qr[rt][c].w));
+
+  int slot_row[L], slot_piece[L];
+#pragma unroll
+  for (int c = 0; c < L; ++c) {
+    const int slot = 64 * c + lane;
+    slot_row[c] = slot / RP;
+    slot_piece[c] = (slot % RP) ^ piece_swizzle<RP>(slot_row[c]);
+  }
+
+  float m_run[R], l_run[R];
+  f32x4 o[R][D / 16];
+#pragma unroll
+  for (int rt = 0; rt < R; ++rt) {
+    m_run[rt] = kNegInf;
+    l_run[rt] = 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) o[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const BT* btp = static_cast<const BT*>(a.block_table);
+  const int win_tokens = kPfIdCap << a.bs_log2;  // a multiple of the stage size
+  int win_blk0 = 0;
+
+  // Copies wave's sub-tile of stage k (keys 64k + 16 wave ..) into buffer ST;
+  // returns the slots that hold a key of the work group. Always 2L loads.
+  auto issue = [&](int k, auto st_c) __attribute__((always_inline)) -> unsigned {
+    constexpr int ST = decltype(st_c)::value;
+    const int kb = k * kPfStageTokens + wave * kTile;
+    unsigned valid = 0;
+    const char* srck[L];
+    const char* srcv[L];
+#pragma unroll
+    for (int c = 0; c < L; ++c) {
+      const int j = kb + slot_row[c];
+      bool ok = j < key_end;
+      int64_t offk = slot_piece[c] * 16, offv = offk;
+      const char* bk = a.k_cache;
+      const char* bv = a.v_cache;
+      if (j < cached) {
+        const int id = s_ids[min((j >> a.bs_log2) - win_blk0, kPfIdCap - 1)];
+        ok = ok && static_cast<uint32_t>(id) < a.num_blocks_u32;
+        const int64_t rowoff = (((static_cast<int64_t>(id) * a.num_kv_heads + h) << a.bs_log2) +
+                                (j & bs_mask)) * Tr::kRowBytes;
+        offk += ok ? rowoff : 0;
+        offv = offk;
+      } else if (ok) {
+        const int64_t cr = qbase - tok0 + (j - cached);  // chunk row of key j
+        offk += cr * a.k_st + h * a.k_sh;
+        offv += cr * a.v_st + h * a.v_sh;
+        bk = a.k_new;
+        bv = a.v_new;
+      }
+      srck[c] = bk + offk;
+      srcv[c] = bv + offv;
+      valid |= ok ? (1u << c) : 0u;
+    }
+    const uint32_t dst = lds0 + ST * Tr::kStageBytes + wave * Tr::kSubBytes;
+#pragma unroll
+    for (int c = 0; c < L; ++c) {
+      copy_to_lds_16B(srck[c], __builtin_amdgcn_readfirstlane(dst + c * 1024));
+      copy_to_lds_16B(srcv[c], __builtin_amdgcn_readfirstlane(dst + Tr::kTileBytes + c * 1024));
+    }
+    return valid;
+  };
+
+  // V slots of keys that were not loaded read pool row 0 instead: zero
+  // them (P is 0 there, but 0 * NaN would not be).
+  auto zero_invalid_v = [&](int st, unsigned valid) __attribute__((always_inline)) {
+    char* vdst = s_lds + st * Tr::kStageBytes + wave * Tr::kSubBytes + Tr::kTileBytes;
+#pragma unroll
+    for (int c = 0; c < L; ++c)
+      if (!((valid >> c) & 1u))
+        *reinterpret_cast<uint4*>(vdst + c * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
+  };
+
+  auto compute_stage = [&](int k, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kPfWaves; ++u) {
+      const int kb = k * kPfStageTokens + u * kTile;
+      if (kb > wave_limit) break;  // causal: the rest of the stage is masked for every row
+      const char* k_tile = s_lds + st * Tr::kStageBytes + u * Tr::kSubBytes;
+      const char* v_tile = k_tile + Tr::kTileBytes;
+      f32x4 acc[R];
+#pragma unroll
+      for (int rt = 0; rt < R; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int ksw = piece_swizzle<RP>(t);
+#pragma unroll
+      for (int c = 0; c < QP; ++c) {
+        const uint4 kp = *reinterpret_cast<const uint4*>(k_tile + (t * RP + ((g * QP + c) ^ ksw)) * 16);
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt) acc[rt] = mfma_qk<DTYPE>(kp, qr[rt][c], acc[rt]);
+      }
+#pragma unroll
+      for (int rt = 0; rt < R; ++rt) {
+        float s[4];
+        float mc = kNegInf;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[e] = kb + 4 * g + e <= limit[rt] ? acc[rt][e] * a.scale_log2 : kNegInf;
+          mc = fmaxf(mc, s[e]);
+        }
+        mc = fmaxf(mc, __shfl_xor(mc, 16));
+        mc = fmaxf(mc, __shfl_xor(mc, 32));
+        const float m_new = fmaxf(m_run[rt], mc);
+        const float m_ref = m_new == kNegInf ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
+        float p[4];
+        float lc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e] - m_ref)));
+          lc += p[e];
+        }
+        lc += __shfl_xor(lc, 16);
+        lc += __shfl_xor(lc, 32);
+        l_run[rt] = l_run[rt] * alpha + lc;
+        m_run[rt] = m_new;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float ar = __shfl(alpha, 4 * g + e);
+#pragma unroll
+          for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
+        }
+        mfma_pv<DTYPE, D>(p, v_tile, g, t, o[rt]);
+      }
+    }
+  };
+
+  // ---- windows of kPfIdCap prefix blocks (one window below 2048 blocks)
+  for (int win0 = 0; win0 < key_end; win0 += win_tokens) {
+    win_blk0 = win0 >> a.bs_log2;
+    if (win0 < cached) {
+      const int pref_end = min(cached, win0 + win_tokens);
+      const int nb = ((pref_end - 1) >> a.bs_log2) - win_blk0 + 1;
+      for (int i = threadIdx.x; i < nb; i += kPfWaves * 64)
+        s_ids[i] = static_cast<int32_t>(btp[row * a.bt_stride + win_blk0 + i]);
+    }
+    __syncthreads();  // block ids of the window visible; previous window's stages released
+    const int k0 = win0 / kPfStageTokens;
+    const int n = (min(key_end, win0 + win_tokens) - win0 + kPfStageTokens - 1) / kPfStageTokens;
+    unsigned valid[S];
+    valid[0] = issue(k0, IntC<0>{});
+    if constexpr (S > 2) {
+      if (1 < n) valid[1] = issue(k0 + 1, IntC<1>{});
+    }
+    // Stage i: wait for this wave's copies of it, clear its invalid V slots,
+    // one barrier (every wave's part landed; stage i-1 consumed by all),
+    // then refill stage i-1's buffer with stage i+S-1 and compute stage i.
+    auto step = [&](int i, auto st_c) __attribute__((always_inline)) {
+      constexpr int ST = decltype(st_c)::value;
+      constexpr int NX = (ST + S - 1) % S;
+      wait_vmcnt_groups<2 * L, S - 2>(min(S - 2, n - 1 - i));
+      asm volatile("" ::: "memory");
+      zero_invalid_v(ST, valid[ST]);
+      __syncthreads();
+      if (i + S - 1 < n) valid[NX] = issue(k0 + i + S - 1, IntC<NX>{});
+      asm volatile("" ::: "memory");
+      compute_stage(k0 + i, ST);
+    };
+    for (int i = 0; i < n; i += S) {
+      step(i, IntC<0>{});
+      if (i + 1 >= n) break;
+      step(i + 1, IntC<1>{});
+      if constexpr (S > 2) {
+        if (i + 2 >= n) break;
+        step(i + 2, IntC<2>{});
+      }
+    }
+    __syncthreads();  // every wave is done with this window's stages and ids
+  }
+
+  // ---- normalise and store this wave's rows
+#pragma unroll
+  for (int rt = 0; rt < R; ++rt) {
+    const float inv = l_run[rt] > 0.f ? 1.f / l_run[rt] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rr = 4 * g + e;  // row of o[rt][.][e]
+      const float ir = __shfl(inv, rr);
+      const int r = rt * 16 + rr;
+      const int rtok = wtok0 + r / a.n_rep;
+      if (r < a.tpw * a.n_rep && rtok < ntok) {
+        raw_t* op = static_cast<raw_t*>(a.out) + (qbase + rtok) * a.o_st +
+                    (h * a.n_rep + r % a.n_rep) * a.o_sh;
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) op[16 * c + t] = from_f32<DTYPE>(o[rt][c][e] * ir);
+      }
+    }
+  }
+}
+
+template <int DTYPE, int D>
+int launch_prefill(const PrefillArgs& a, int groups, bool bt_i64, hipStream_t s) {
+  if (bt_i64) paged_prefill_kernel<DTYPE, D, int64_t><<<groups, kPfWaves * 64, 0, s>>>(a);
+  else paged_prefill_kernel<DTYPE, D, int32_t><<<groups, kPfWaves * 64, 0, s>>>(a);
+  return check_launch("mv_paged_prefill");
+}
+
+template <int DTYPE>
+int launch_prefill_d(const PrefillArgs& a, int d, int groups, bool bt_i64, hipStream_t s) {
+  return d == 64 ? launch_prefill<DTYPE, 64>(a, groups, bt_i64, s)
+                 : launch_prefill<DTYPE, 128>(a, groups, bt_i64, s);
+}
+
+}  // namespace
+}  // namespace mv
+
+extern "C" int mv_prefill_tokens_per_group(int32_t num_q_heads, int32_t num_kv_heads,
+                                           int32_t head_dim) {
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return 0;
+  if (head_dim != 64 && head_dim != 128) return 0;
+  const int rows = 16 * mv::pf_row_tiles(head_dim);
+  const int n_rep = num_q_heads / num_kv_heads;
+  if (n_rep > rows) return 0;
+  return mv::kPfWaves * (rows / n_rep);
+}
+
+extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                                const void* key, int64_t k_stride_tok, int64_t k_stride_head,
+                                const void* value, int64_t v_stride_tok, int64_t v_stride_head,
+                                const void* key_cache, const void* value_cache,
+                                const void* block_table, int32_t bt_is_i64, int64_t bt_stride,
+                                const int64_t* seqs, int32_t num_seqs, const int32_t* work_items,
+                                int32_t num_work_groups, void* out, int64_t out_stride_tok,
+                                int64_t out_stride_head, float scale, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                int64_t num_blocks, int32_t dtype, void* stream) {
+  using namespace mv;
+  const int eb = dtype_bytes(dtype);
+  if (eb == 0) return fail(MV_ERR_UNSUPPORTED, "mv_paged_prefill: unknown dtype %d", dtype);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(MV_ERR_UNSUPPORTED, "mv_paged_prefill: head_dim %d not supported (64, 128)", head_dim);
+  if (!is_pow2(block_size))
+    return fail(MV_ERR_UNSUPPORTED, "mv_paged_prefill: block_size %d is not a power of 2", block_size);
+  const int tpg = mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim);
+  if (tpg == 0)
+    return fail(MV_ERR_UNSUPPORTED, "mv_paged_prefill: %d query heads over %d kv heads not supported",
+                num_q_heads, num_kv_heads);
+  if (num_seqs < 0 || num_work_groups < 0 || num_blocks <= 0)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_prefill: bad sizes");
+  if (num_work_groups == 0) return MV_OK;
+  if (!query || !key || !value || !key_cache || !value_cache || !seqs || !work_items || !out ||
+      (!block_table && bt_stride != 0))
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_prefill: null pointer");
+  if ((reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key) |
+       reinterpret_cast<uintptr_t>(value) | reinterpret_cast<uintptr_t>(key_cache) |
+       reinterpret_cast<uintptr_t>(value_cache) | reinterpret_cast<uintptr_t>(work_items)) % 16 ||
+      ((q_stride_tok | q_stride_head | k_stride_tok | k_stride_head | v_stride_tok |
+        v_stride_head) * eb) % 16)
+    return fail(MV_ERR_INVALID_ARGUMENT,
+                "mv_paged_prefill: query/key/value rows and caches must be 16-byte aligned");
+  PrefillArgs a;
+  a.work = work_items;
+  a.seqs = seqs;
+  a.q = query;
+  a.k_new = static_cast<const char*>(key);
+  a.v_new = static_cast<const char*>(value);
+  a.k_cache = static_cast<const char*>(key_cache);
+  a.v_cache = static_cast<const char*>(value_cache);
+  a.block_table = block_table;
+  a.out = out;
+  a.q_st = q_stride_tok;
+  a.q_sh = q_stride_head;
+  a.k_st = k_stride_tok * eb;
+  a.k_sh = k_stride_head * eb;
+  a.v_st = v_stride_tok * eb;
+  a.v_sh = v_stride_head * eb;
+  a.o_st = out_stride_tok;
+  a.o_sh = out_stride_head;
+  a.bt_stride = bt_stride;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.num_kv_heads = num_kv_heads;
+  a.n_rep = num_q_heads / num_kv_heads;
+  a.tpw = tpg / kPfWaves;
+  a.bs_log2 = ilog2_exact(block_size);
+  a.num_blocks_u32 = static_cast<uint32_t>(std::min<int64_t>(num_blocks, int64_t(1) << 31));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool i64 = bt_is_i64 != 0;
+  switch (dtype) {
+    case MV_DTYPE_F32: return launch_prefill_d<MV_DTYPE_F32>(a, head_dim, num_work_groups, i64, s);
+    case MV_DTYPE_F16: return launch_prefill_d<MV_DTYPE_F16>(a, head_dim, num_work_groups, i64, s);
+    default: return launch_prefill_d<MV_DTYPE_BF16>(a, head_dim, num_work_groups, i64, s);
+  }
+}

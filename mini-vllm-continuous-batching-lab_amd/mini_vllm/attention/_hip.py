@@ -97,6 +97,18 @@ SIGNATURES = {
         _I32, _I64, _I32, _P,      # block_size, num_blocks, dtype, stream
     ]),
     "mv_positions_check": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "mv_prefill_tokens_per_group": (ctypes.c_int, [_I32, _I32, _I32]),
+    "mv_paged_prefill": (ctypes.c_int, [
+        _P, _I64, _I64,            # query, strides
+        _P, _I64, _I64,            # key, strides
+        _P, _I64, _I64,            # value, strides
+        _P, _P,                    # key_cache, value_cache
+        _P, _I32, _I64,            # block_table, bt_is_i64, bt_stride
+        _P, _I32, _P, _I32,        # seqs, num_seqs, work_items, num_work_groups
+        _P, _I64, _I64,            # out, strides
+        _F, _I32, _I32, _I32,      # scale, num_q_heads, num_kv_heads, head_dim
+        _I32, _I64, _I32, _P,      # block_size, num_blocks, dtype, stream
+    ]),
 }
 
 _lock = threading.Lock()

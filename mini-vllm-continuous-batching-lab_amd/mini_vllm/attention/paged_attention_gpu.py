@@ -31,7 +31,6 @@ from dataclasses import dataclass
 from typing import Any, List, Optional, Sequence, Tuple
 
 import torch
-import torch.nn.functional as F
 
 from . import _hip
 from ..cache.pool import KVCachePool
@@ -50,6 +49,7 @@ __all__ = [
     "gather_prefix_kv",
     "hip_cache_write",
     "hip_decode_attention",
+    "hip_prefill_attention",
     "hip_rope_kv_cache_write",
     "hip_rotary",
     "plan_decode",
@@ -703,15 +703,7 @@ def gather_prefix_kv(
     bt_host = block_table.detach().to("cpu", torch.int64)
     if bt_host.dim() != 2:
         bt_host = bt_host.reshape(-1, bt_host.shape[-1] if bt_host.dim() else 0)
-    for row, n in zip(rows, lens):
-        need = -(-n // block_size)
-        if not 0 <= row < bt_host.shape[0] or need > bt_host.shape[1]:
-            raise IndexError(f"block_table row {row} insufficient to cover {n} tokens")
-        ids = bt_host[row, :need]
-        if need and (int(ids.min()) < 0 or int(ids.max()) >= num_blocks):
-            raise IndexError(
-                f"block_table row {row} insufficient: entries {ids.tolist()} are not all pool blocks"
-            )
+    _check_prefix_tables(bt_host, rows, lens, block_size, num_blocks)
     bt = block_table.to(device)
     if bt.dtype not in (torch.int32, torch.int64):
         bt = bt.to(torch.int64)
@@ -733,6 +725,139 @@ def gather_prefix_kv(
         "mv_gather_paged_kv",
     )
     return out_k, out_v
+
+
+# ============================================================================
+# Prefill attention
+# ============================================================================
+
+
+def _check_prefix_tables(bt_host: torch.Tensor, rows: Sequence[int], lens: Sequence[int],
+                         block_size: int, num_blocks: int) -> None:
+    """``IndexError`` ("insufficient") when a table row cannot cover its
+    sequence's cached prefix or one of the entries it needs is not a pool
+    block (reference cache/cache_read.py:60-67)."""
+    for row, n in zip(rows, lens):
+        need = -(-n // block_size)
+        if not 0 <= row < bt_host.shape[0] or need > bt_host.shape[1]:
+            raise IndexError(f"block_table row {row} insufficient to cover {n} tokens")
+        ids = bt_host[row, :need]
+        if need and (int(ids.min()) < 0 or int(ids.max()) >= num_blocks):
+            raise IndexError(
+                f"block_table row {row} insufficient: entries {ids.tolist()} are not all pool blocks"
+            )
+
+
+def _aligned_rows(x: torch.Tensor) -> torch.Tensor:
+    """x with 16-byte aligned, head_dim-contiguous rows (a copy only if not)."""
+    eb = x.element_size()
+    if (x.stride(-1) != 1 or (x.stride(0) * eb) % 16 or (x.stride(1) * eb) % 16
+            or x.data_ptr() % 16):
+        x = x.contiguous()
+    return x
+
+
+def hip_prefill_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_indices: Sequence[int],
+    cached_len_before: Sequence[int],
+    query_len: Sequence[int],
+    block_size: int,
+) -> torch.Tensor:
+    """Chunked-prefill attention over the paged pool in one HIP launch.
+
+    The computation of ``AttentionBackendGPU.prefill_attention`` (reference
+    paged_attention_gpu.py:577-661): sequence i (table row
+    ``seq_indices[i]``) has ``cached_len_before[i]`` tokens in the pool and
+    a chunk of ``query_len[i]`` tokens whose rows in ``query`` / ``key`` /
+    ``value`` follow the previous sequences'; chunk token t attends the
+    prefix from the pool and chunk keys 0..t from ``key`` / ``value``
+    (causal, offset by the prefix), ``scale = head_dim ** -0.5``, query
+    head h reads kv head ``h // n_rep``. Returns ``[sum(query_len), Hq, D]``
+    in the query dtype. ``IndexError`` (message "insufficient") for a table
+    that cannot cover a prefix, as the reference's gather raises. q / k / v
+    may be column views of one fused QKV output.
+    """
+    total_q, num_q_heads, head_dim = query.shape
+    num_blocks, num_kv_heads, bs, _ = key_cache.shape
+    assert bs == block_size, f"block_size {block_size} != cache dim2 {bs}"
+    assert head_dim in SUPPORTED_HEAD_DIMS, f"head_dim {head_dim} not supported (only 64, 128)"
+    assert _is_pow2(block_size), f"block_size {block_size} must be a power of 2"
+    assert key.shape[1:] == (num_kv_heads, head_dim) and value.shape == key.shape
+    assert query.dtype in SUPPORTED_DTYPES and key.dtype == query.dtype and value.dtype == query.dtype
+    assert key_cache.dtype == query.dtype and value_cache.dtype == query.dtype
+    assert key_cache.shape == value_cache.shape
+    assert key_cache.is_contiguous() and value_cache.is_contiguous()
+    assert query.device.type == "cuda"
+    rows = [int(r) for r in seq_indices]
+    cached = [int(c) for c in cached_len_before]
+    qlens = [int(q) for q in query_len]
+    assert len(rows) == len(cached) == len(qlens)
+    total = sum(qlens)
+    assert total <= total_q and total <= key.shape[0], (
+        f"{total} chunk tokens, query has {total_q} rows, key {key.shape[0]}"
+    )
+    device = query.device
+    lib = _hip.load()
+    tpg = lib.mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim)
+    if tpg == 0:
+        raise RuntimeError(
+            f"prefill: {num_q_heads} query heads over {num_kv_heads} kv heads not supported"
+        )
+    out = torch.empty(total, num_q_heads, head_dim, dtype=query.dtype, device=device)
+    if total == 0:
+        return out
+    bt = block_table
+    if bt.dim() != 2:
+        bt = bt.reshape(-1, bt.shape[-1] if bt.dim() else 0)
+    if any(cached):
+        _check_prefix_tables(bt.detach().to("cpu", torch.int64), rows, cached, block_size,
+                             num_blocks)
+    bt = bt.to(device)
+    if bt.dtype not in (torch.int32, torch.int64):
+        bt = bt.to(torch.int64)
+    if bt.numel() and bt.stride(1) != 1:
+        bt = bt.contiguous()
+
+    # per sequence (table row, cached, first chunk row, chunk tokens); work
+    # groups (sequence, kv head, first token, tokens), the most keys first
+    seqs, items, keys = [], [], []
+    start = 0
+    for i, (r, c, ql) in enumerate(zip(rows, cached, qlens)):
+        seqs.append((r, c, start, ql))
+        for t0 in range(0, ql, tpg):
+            nt = min(tpg, ql - t0)
+            for h in range(num_kv_heads):
+                items.append((i, h, t0, nt))
+                keys.append(c + t0 + nt)
+        start += ql
+    if not items:
+        return out
+    order = sorted(range(len(items)), key=lambda k: -keys[k])
+    work = torch.tensor([items[k] for k in order], dtype=torch.int32).to(device, non_blocking=True)
+    meta = torch.tensor(seqs, dtype=torch.int64).to(device, non_blocking=True)
+
+    q = _aligned_rows(query)
+    k = _aligned_rows(key)
+    v = _aligned_rows(value)
+    _hip.check(
+        lib.mv_paged_prefill(
+            _ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), k.stride(1),
+            _ptr(v), v.stride(0), v.stride(1), _ptr(key_cache), _ptr(value_cache),
+            _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
+            bt.stride(0) if bt.numel() else 0, _ptr(meta), len(seqs), _ptr(work), len(items),
+            _ptr(out), out.stride(0), out.stride(1), float(head_dim ** -0.5), num_q_heads,
+            num_kv_heads, head_dim, block_size, num_blocks, _hip.MV_DTYPE[query.dtype],
+            _stream(device),
+        ),
+        "mv_paged_prefill",
+    )
+    return out
 
 
 # ============================================================================
@@ -864,52 +989,28 @@ class AttentionBackendGPU(AttentionBackend):
         attn_metadata: AttentionMetadata,
         pool: KVCachePool,
     ) -> torch.Tensor:
-        """Prefill: HIP prefix gather from the pool + SDPA with an offset causal mask.
+        """Prefill over the pool in one HIP launch (``hip_prefill_attention``).
 
-        Same structure as the reference's GPU prefill
+        Same contract as the reference's GPU prefill
         (paged_attention_gpu.py:577-661): the cached prefix comes from the
         pool, the current chunk's K/V from the arguments, and query i of a
-        chunk starting at position P sees key positions <= P + i.
+        chunk starting at position P sees key positions <= P + i; the
+        outputs of all prefill groups, in order, in one tensor.
         """
-        total = query.shape[0]
-        if total == 0:
+        if query.shape[0] == 0:
             return query
-        num_heads, head_dim = query.shape[1], query.shape[2]
-        n_rep = num_heads // pool.num_kv_heads
-        scale = head_dim ** -0.5
-        kc = pool.key_caches[layer_idx]
-        vc = pool.value_caches[layer_idx]
-        outputs: List[torch.Tensor] = []
-        offset = 0
+        rows: List[int] = []
+        cached: List[int] = []
+        qlens: List[int] = []
         for group in attn_metadata.groups:
             if group.attention_type not in ("prefill_gpu", "prefill_ref"):
                 continue
-            cached = [int(c) for c in group.cached_len_before.tolist()]
-            qlens = [int(q) for q in group.query_len.tolist()]
-            rows = [int(s) for s in group.seq_indices]
-            pref_k, pref_v = gather_prefix_kv(
-                kc, vc, attn_metadata.prefill_block_tables, cached, rows, pool.block_size
-            )
-            poff = 0
-            for c, ql in zip(cached, qlens):
-                full_k = torch.cat([pref_k[poff:poff + c], key[offset:offset + ql]], dim=0)
-                full_v = torch.cat([pref_v[poff:poff + c], value[offset:offset + ql]], dim=0)
-                poff += c
-                full_k = full_k.repeat_interleave(n_rep, dim=1)
-                full_v = full_v.repeat_interleave(n_rep, dim=1)
-                q_pos = torch.arange(c, c + ql, device=query.device)
-                k_pos = torch.arange(c + ql, device=query.device)
-                mask = k_pos.unsqueeze(0) <= q_pos.unsqueeze(1)
-                # fp32: SDPA's math path issues batched products on transposed
-                # views, which are not safe in 16-bit types on this platform.
-                out = F.scaled_dot_product_attention(
-                    query[offset:offset + ql].permute(1, 0, 2).unsqueeze(0).float().contiguous(),
-                    full_k.permute(1, 0, 2).unsqueeze(0).float().contiguous(),
-                    full_v.permute(1, 0, 2).unsqueeze(0).float().contiguous(),
-                    attn_mask=mask, is_causal=False, scale=scale,
-                )
-                outputs.append(out.squeeze(0).permute(1, 0, 2).to(query.dtype))
-                offset += ql
-        if not outputs:
+            rows += [int(s) for s in group.seq_indices]
+            cached += [int(c) for c in group.cached_len_before.tolist()]
+            qlens += [int(q) for q in group.query_len.tolist()]
+        if not rows:
             return query
-        return torch.cat(outputs, dim=0)
+        return hip_prefill_attention(
+            query, key, value, pool.key_caches[layer_idx], pool.value_caches[layer_idx],
+            attn_metadata.prefill_block_tables, rows, cached, qlens, pool.block_size,
+        )

@@ -217,3 +217,48 @@ def prefill_attention(
         outs.append(o.squeeze(0).permute(1, 0, 2))
         off += ql
     return torch.cat(outs, dim=0)
+
+
+def prefill_attention_chunk_args(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_indices: Sequence[int],
+    cached_len_before: Sequence[int],
+    query_len: Sequence[int],
+    block_size: int,
+) -> torch.Tensor:
+    """``AttentionBackendGPU.prefill_attention`` (paged_attention_gpu.py:
+    577-661): the cached prefix from the pool (gather of ``cached`` tokens),
+    the chunk's keys / values from ``key`` / ``value`` (rows in sequence
+    order), ``cat``, ``repeat_interleave`` to the query heads, SDPA with the
+    offset causal mask ``key_pos <= cached + t``."""
+    num_heads, head_dim = query.shape[1], query.shape[2]
+    n_rep = num_heads // key_cache.shape[1]
+    scale = head_dim ** -0.5
+    outs, off = [], 0
+    for i, s in enumerate(seq_indices):
+        c, ql = int(cached_len_before[i]), int(query_len[i])
+        if c > 0:
+            ids = [int(b) for b in block_tables[int(s)].tolist() if b != -1]
+            pk, pv = gather_paged_kv(key_cache, value_cache, ids, c, block_size)
+        else:
+            pk = key_cache.new_empty(0, key_cache.shape[1], head_dim)
+            pv = pk.clone()
+        k = torch.cat([pk, key[off:off + ql]], dim=0).repeat_interleave(n_rep, dim=1)
+        v = torch.cat([pv, value[off:off + ql]], dim=0).repeat_interleave(n_rep, dim=1)
+        mask = torch.arange(c + ql).unsqueeze(0) <= torch.arange(c, c + ql).unsqueeze(1)
+        o = F.scaled_dot_product_attention(
+            query[off:off + ql].permute(1, 0, 2).unsqueeze(0),
+            k.permute(1, 0, 2).unsqueeze(0),
+            v.permute(1, 0, 2).unsqueeze(0),
+            attn_mask=mask,
+            is_causal=False,
+            scale=scale,
+        )
+        outs.append(o.squeeze(0).permute(1, 0, 2))
+        off += ql
+    return torch.cat(outs, dim=0)

@@ -1,0 +1,154 @@
+"""Paged prefill attention (mv_paged_prefill) against the oracle.
+
+The oracle restates the reference GPU backend's prefill
+(oracle/paged_ref.py:prefill_attention_chunk_args): prefix from the pool,
+chunk K/V from the arguments, offset causal mask, in fp32 on the same
+(rounded) inputs. Pool rows the kernel must not read (free blocks and the
+chunk's own slots) hold NaN, so a stray read fails the comparison.
+"""
+
+import pytest
+import torch
+
+from gpu_util import DEV, TOL, say
+from mini_vllm.attention import AttentionBackend
+from mini_vllm.attention.paged_attention_gpu import hip_prefill_attention
+from mini_vllm.model_runner.base import AttentionGroup, AttentionMetadata, ModelConfig
+from oracle import paged_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(hq, hkv, d, bs, dtype, cached, qlen, seed=0, fused=False, extra_blocks=16):
+    g = torch.Generator().manual_seed(seed)
+    n = len(cached)
+    need = [-(-c // bs) for c in cached]
+    nb = sum(need) + extra_blocks
+    width = max(need + [1]) + 2
+    perm = torch.randperm(nb, generator=g)
+    bt = torch.full((n + 1, width), -1, dtype=torch.int64)  # row 0 unused: rows are seq_indices
+    pos = 0
+    for i, m in enumerate(need):
+        bt[i + 1, :m] = perm[pos:pos + m]
+        pos += m
+    kc = torch.full((nb, hkv, bs, d), float("nan"))
+    vc = torch.full((nb, hkv, bs, d), float("nan"))
+    for i, c in enumerate(cached):  # real values only in the prefix slots
+        for p in range(c):
+            b = int(bt[i + 1, p // bs])
+            kc[b, :, p % bs] = torch.randn(hkv, d, generator=g)
+            vc[b, :, p % bs] = torch.randn(hkv, d, generator=g)
+    t = sum(qlen)
+    if fused:
+        qkv = torch.randn(t, (hq + 2 * hkv) * d, generator=g)
+        q = qkv[:, : hq * d].reshape(t, hq, d)
+        k = qkv[:, hq * d:(hq + hkv) * d].reshape(t, hkv, d)
+        v = qkv[:, (hq + hkv) * d:].reshape(t, hkv, d)
+    else:
+        q = torch.randn(t, hq, d, generator=g)
+        k = torch.randn(t, hkv, d, generator=g)
+        v = torch.randn(t, hkv, d, generator=g)
+    r = lambda x: x.to(dtype).float()  # noqa: E731  values the kernel sees
+    return dict(q=r(q), k=r(k), v=r(v), kc=r(kc), vc=r(vc), bt=bt, rows=list(range(1, n + 1)),
+                cached=cached, qlen=qlen, bs=bs, dtype=dtype, fused=fused, hq=hq, hkv=hkv, d=d)
+
+
+def _run(c):
+    dt = c["dtype"]
+    if c["fused"]:
+        t = c["q"].shape[0]
+        qkv = torch.cat([c["q"].reshape(t, -1), c["k"].reshape(t, -1), c["v"].reshape(t, -1)], 1)
+        qkv = qkv.to(dt).to(DEV)
+        hq, hkv, d = c["hq"], c["hkv"], c["d"]
+        q = qkv[:, : hq * d].view(t, hq, d)
+        k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+        v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    else:
+        q, k, v = (c[n].to(dt).to(DEV) for n in ("q", "k", "v"))
+    out = hip_prefill_attention(q, k, v, c["kc"].to(dt).to(DEV), c["vc"].to(dt).to(DEV),
+                                c["bt"].to(DEV), c["rows"], c["cached"], c["qlen"], c["bs"])
+    torch.cuda.synchronize()
+    return out.float().cpu()
+
+
+def _ref(c):
+    return paged_ref.prefill_attention_chunk_args(c["q"], c["k"], c["v"], c["kc"], c["vc"], c["bt"],
+                                                  c["rows"], c["cached"], c["qlen"], c["bs"])
+
+
+CACHED = [0, 100, 5, 300, 2047, 64]
+QLEN = [37, 64, 1, 129, 3, 200]
+
+SHAPES = [  # (hq, hkv, d, bs, dtype)
+    (14, 2, 64, 16, torch.bfloat16),
+    (14, 2, 64, 16, torch.float32),
+    (28, 4, 128, 16, torch.bfloat16),
+    (8, 8, 64, 32, torch.float16),     # n_rep 1
+    (16, 1, 128, 16, torch.bfloat16),  # n_rep 16
+    (32, 1, 64, 64, torch.bfloat16),   # n_rep 32
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}-{s[1]}-{s[2]}-bs{s[3]}-{s[4]}")
+def test_prefill_matches_oracle(shape):
+    hq, hkv, d, bs, dt = shape
+    say("prefill", shape)
+    c = _case(hq, hkv, d, bs, dt, CACHED, QLEN, seed=1)
+    out = _run(c)
+    ref = _ref(c)
+    assert not torch.isnan(out).any()
+    err = (out - ref).abs().max().item()
+    assert err <= TOL[dt], err
+
+
+def test_fused_qkv_views():
+    say("prefill fused qkv")
+    c = _case(14, 2, 64, 16, torch.bfloat16, [40, 0, 333], [77, 16, 50], seed=2, fused=True)
+    err = (_run(c) - _ref(c)).abs().max().item()
+    assert err <= TOL[torch.bfloat16], err
+
+
+def test_prefix_spanning_two_id_windows():
+    """block_size 1: a 3000-token prefix needs 3000 block ids, two windows of 2048."""
+    say("prefill two windows")
+    c = _case(14, 2, 64, 1, torch.bfloat16, [3000, 10], [40, 20], seed=3, extra_blocks=64)
+    err = (_run(c) - _ref(c)).abs().max().item()
+    assert err <= TOL[torch.bfloat16], err
+
+
+def test_insufficient_table_raises():
+    say("prefill insufficient table")
+    c = _case(14, 2, 64, 16, torch.bfloat16, [50], [8], seed=4)
+    c["bt"][1, 2] = 10_000  # not a pool block
+    with pytest.raises(IndexError, match="insufficient"):
+        _run(c)
+    c["bt"] = c["bt"][:, :2]  # too short for 50 tokens
+    with pytest.raises(IndexError, match="insufficient"):
+        _run(c)
+
+
+def test_backend_prefill_groups():
+    """AttentionBackendGPU.prefill_attention over two prefill groups."""
+    say("backend prefill")
+    c = _case(14, 2, 64, 16, torch.bfloat16, [0, 90, 17], [33, 21, 8], seed=5)
+    cfg = ModelConfig(num_layers=1, hidden_size=896, num_heads=14, num_kv_heads=2, head_dim=64,
+                      dtype=torch.bfloat16)
+    be = AttentionBackend.create(cfg, backend="hip")
+    nb = c["kc"].shape[0]
+    pool = be.allocate_pool(1, nb, 16, 2, 64, torch.bfloat16, DEV)
+    pool.key_caches[0].copy_(c["kc"].to(torch.bfloat16))
+    pool.value_caches[0].copy_(c["vc"].to(torch.bfloat16))
+    lt = lambda x: torch.tensor(x, dtype=torch.long)  # noqa: E731
+    groups = [
+        AttentionGroup([1, 2], "prefill_gpu", lt(c["cached"][:2]), lt(c["qlen"][:2]),
+                       lt([a + b for a, b in zip(c["cached"][:2], c["qlen"][:2])])),
+        AttentionGroup([3], "prefill_gpu", lt(c["cached"][2:]), lt(c["qlen"][2:]),
+                       lt([c["cached"][2] + c["qlen"][2]])),
+    ]
+    meta = AttentionMetadata(groups=groups, prefill_block_tables=c["bt"].to(DEV), block_size=16,
+                             num_kv_heads=2, head_dim=64)
+    out = be.prefill_attention(0, c["q"].to(torch.bfloat16).to(DEV), c["k"].to(torch.bfloat16).to(DEV),
+                               c["v"].to(torch.bfloat16).to(DEV), meta, pool)
+    torch.cuda.synchronize()
+    err = (out.float().cpu() - _ref(c)).abs().max().item()
+    assert err <= TOL[torch.bfloat16], err

@@ -54,3 +54,28 @@ def test_causal_mask_excludes_future_positions():
     b = paged_ref.prefill_attention(q, kc, vc2, bt, [0], [2], [5], 4)
     assert torch.equal(a[:4], b[:4])
     assert not torch.allclose(a[4], b[4])
+
+
+def test_chunk_argument_form_equals_pool_form_after_write():
+    """The GPU backend's form (prefix from the pool, chunk K/V from the
+    arguments) equals the pool-only form once the chunk has been written
+    to its slots -- the runner's write-first order."""
+    kc, vc, g = _pool(5, nb=30)
+    bs = 4
+    bt = torch.tensor([[7, 1, 22, 4, 9, -1], [3, 28, 15, 11, 0, 2], [5, 6, -1, -1, -1, -1]])
+    seqs, cached, qlen = [1, 0, 2], [6, 0, 3], [13, 10, 4]
+    q = torch.randn(sum(qlen), 4, 8, generator=g, dtype=torch.float64)
+    k = torch.randn(sum(qlen), 2, 8, generator=g, dtype=torch.float64)
+    v = torch.randn(sum(qlen), 2, 8, generator=g, dtype=torch.float64)
+    got = paged_ref.prefill_attention_chunk_args(q, k, v, kc, vc, bt, seqs, cached, qlen, bs)
+    kc2, vc2 = kc.clone(), vc.clone()
+    slots, off = [], 0
+    for s, c, ql in zip(seqs, cached, qlen):
+        for t in range(ql):
+            p = c + t
+            slots.append(int(bt[s, p // bs]) * bs + p % bs)
+    paged_ref.write_to_paged_cache(k, v, kc2, vc2, torch.tensor(slots), bs)
+    want = paged_ref.prefill_attention(q, kc2, vc2, bt, seqs, cached, qlen, bs)
+    assert torch.allclose(got, want, atol=1e-12)
+    ref = brute.prefill(q.numpy(), kc2.numpy(), vc2.numpy(), bt.numpy(), seqs, cached, qlen, bs)
+    assert np.abs(got.numpy() - ref).max() < 1e-10
