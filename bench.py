@@ -128,6 +128,78 @@ def torch_rope(x, pos, cos, sin):
     return x * c + torch.cat((-x[..., h:], x[..., :h]), dim=-1) * s
 
 
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def prefill_measure(dev, steps, warmup):
+    """Chunked prefill at the Qwen2-0.5B shape (14 q / 2 kv heads, head_dim
+    64, block 16, bf16): 4 sequences with 1536 cached tokens and a 512-token
+    chunk each. The HIP kernel against the reference's algorithm
+    (paged_attention_gpu.py:577-661: prefix gather, cat, repeat_interleave,
+    masked SDPA per sequence; SDPA in fp32, the safe path for batched
+    products on this platform)."""
+    import torch.nn.functional as F
+    from mini_vllm.attention.paged_attention_gpu import gather_prefix_kv, hip_prefill_attention
+
+    hq, hkv, d, bs, dt = 14, 2, 64, 16, torch.bfloat16
+    cached, qlen = [1536] * 4, [512] * 4
+    n = len(cached)
+    need = [-(-(c + q) // bs) for c, q in zip(cached, qlen)]
+    nb = sum(need) + 64
+    g = torch.Generator(device=dev).manual_seed(0)
+    perm = torch.randperm(nb, device=dev, generator=g)
+    bt = torch.full((n, max(need)), -1, dtype=torch.int64, device=dev)
+    pos = 0
+    for i, m in enumerate(need):
+        bt[i, :m] = perm[pos:pos + m]
+        pos += m
+    kc = torch.randn(nb, hkv, bs, d, device=dev, generator=g).to(dt)
+    vc = torch.randn(nb, hkv, bs, d, device=dev, generator=g).to(dt)
+    t = sum(qlen)
+    q = torch.randn(t, hq, d, device=dev, generator=g).to(dt)
+    k = torch.randn(t, hkv, d, device=dev, generator=g).to(dt)
+    v = torch.randn(t, hkv, d, device=dev, generator=g).to(dt)
+    rows = list(range(n))
+    stream = torch.cuda.current_stream(dev)
+
+    def hip(i):
+        hip_prefill_attention(q, k, v, kc, vc, bt, rows, cached, qlen, bs)
+
+    def reference(i):
+        pk, pv = gather_prefix_kv(kc, vc, bt, cached, rows, bs)
+        off = poff = 0
+        for c, ql in zip(cached, qlen):
+            fk = torch.cat([pk[poff:poff + c], k[off:off + ql]]).repeat_interleave(hq // hkv, dim=1)
+            fv = torch.cat([pv[poff:poff + c], v[off:off + ql]]).repeat_interleave(hq // hkv, dim=1)
+            mask = (torch.arange(c + ql, device=dev).unsqueeze(0)
+                    <= torch.arange(c, c + ql, device=dev).unsqueeze(1))
+            F.scaled_dot_product_attention(
+                q[off:off + ql].permute(1, 0, 2).unsqueeze(0).float().contiguous(),
+                fk.permute(1, 0, 2).unsqueeze(0).float().contiguous(),
+                fv.permute(1, 0, 2).unsqueeze(0).float().contiguous(),
+                attn_mask=mask, scale=d ** -0.5)
+            off += ql
+            poff += c
+
+    for i in range(warmup):
+        hip(i)
+        reference(i)
+    n_steps = max(5, steps // 10)
+    us = time_loop(hip, n_steps, stream, host_us=300.0)
+    us_ref = time_loop(reference, n_steps, stream, host_us=2000.0)
+    # causal MACs: token t of a chunk attends cached + t + 1 keys, QK^T and PV
+    flops = sum(4 * hq * d * (ql * c + ql * (ql + 1) // 2) for c, ql in zip(cached, qlen))
+    tflops = flops / us / 1e6
+    return {
+        "workload": "Qwen2-0.5B chunked prefill: 14 q / 2 kv heads, head_dim 64, block 16, bf16, "
+                    "4 sequences x (1536 cached + 512 chunk)",
+        "us": round(us, 2),
+        "tflops": round(tflops, 2),
+        "frac_of_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "reference_algorithm_us": round(us_ref, 1),
+    }
+
+
 def plan_step_us(bt, kv, bs, num_blocks, dev, spec, plan_decode, reps=20):
     """Host time of one step's decode plan in steady state (median): the
     plan kernel plus the read-back of its status. Fresh copies of the
@@ -307,6 +379,10 @@ def main(argv=None) -> int:
     log(f"[bench] captured step ({graph_layers} layers + plan): {us_graph:.1f} us GPU, "
         f"{us_graph_wall:.1f} us host-inclusive")
 
+    prefill = prefill_measure(dev, args.steps, min(args.warmup, 5))
+    log(f"[bench] prefill {prefill['us']:.1f} us ({prefill['tflops']:.1f} TFLOP/s), "
+        f"reference algorithm {prefill['reference_algorithm_us']:.1f} us")
+
     # RoPE of the step's q and new k + KV write: fused kernel against the
     # reference's sequence (two eager rotaries, then the cache write)
     cos, sin = rope_tables(spec.head_dim, 1000000.0, 32768, spec.dtype, dev)
@@ -373,6 +449,7 @@ def main(argv=None) -> int:
             "us_per_layer_call": round(us_graph / graph_layers, 3),
             "host_inclusive_us_per_step": round(us_graph_wall, 2),
         },
+        "prefill": prefill,
         "rope_write": {
             "what": "RoPE of the step's q and new k + KV write (qwen_runner.py:164-170)",
             "fused_us": round(us_rope, 3),

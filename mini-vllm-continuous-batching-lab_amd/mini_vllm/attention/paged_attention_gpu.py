@@ -748,6 +748,56 @@ def _check_prefix_tables(bt_host: torch.Tensor, rows: Sequence[int], lens: Seque
             )
 
 
+def _prefill_plan(block_table, rows, cached, qlens, block_size, num_blocks, num_q_heads,
+                  num_kv_heads, head_dim, device):
+    """Validated table and device work list of one step's prefill, built once:
+    the layers of a step pass the same (unmodified) block table and lengths,
+    so only the first call validates (one host copy of the table) and
+    uploads; the others reuse it.
+
+    Work groups are (sequence, kv head, first token, tokens), the most keys
+    first; per sequence (table row, cached, first chunk row, chunk tokens).
+    """
+    lib = _hip.load()
+    extra = (tuple(rows), tuple(cached), tuple(qlens), block_size, num_blocks, num_q_heads,
+             num_kv_heads, head_dim, device)
+    hit = _cache_get("prefill", (block_table,), extra)
+    if hit is not None:
+        return hit
+    tpg = lib.mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim)
+    if tpg == 0:
+        raise RuntimeError(
+            f"prefill: {num_q_heads} query heads over {num_kv_heads} kv heads not supported"
+        )
+    bt = block_table
+    if bt.dim() != 2:
+        bt = bt.reshape(-1, bt.shape[-1] if bt.dim() else 0)
+    if any(cached):
+        _check_prefix_tables(bt.detach().to("cpu", torch.int64), rows, cached, block_size,
+                             num_blocks)
+    bt = bt.to(device)
+    if bt.dtype not in (torch.int32, torch.int64):
+        bt = bt.to(torch.int64)
+    if bt.numel() and bt.stride(1) != 1:
+        bt = bt.contiguous()
+    seqs, items, keys = [], [], []
+    start = 0
+    for i, (r, c, ql) in enumerate(zip(rows, cached, qlens)):
+        seqs.append((r, c, start, ql))
+        for t0 in range(0, ql, tpg):
+            nt = min(tpg, ql - t0)
+            for h in range(num_kv_heads):
+                items.append((i, h, t0, nt))
+                keys.append(c + t0 + nt)
+        start += ql
+    order = sorted(range(len(items)), key=lambda k: -keys[k])
+    work = torch.tensor([items[k] for k in order] or [(0, 0, 0, 0)], dtype=torch.int32)
+    meta = torch.tensor(seqs or [(0, 0, 0, 0)], dtype=torch.int64)
+    plan = (bt, meta.to(device, non_blocking=True), work.to(device, non_blocking=True), len(items))
+    _cache_put("prefill", (block_table,), extra, plan)
+    return plan
+
+
 def _aligned_rows(x: torch.Tensor) -> torch.Tensor:
     """x with 16-byte aligned, head_dim-contiguous rows (a copy only if not)."""
     eb = x.element_size()
@@ -804,43 +854,12 @@ def hip_prefill_attention(
     )
     device = query.device
     lib = _hip.load()
-    tpg = lib.mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim)
-    if tpg == 0:
-        raise RuntimeError(
-            f"prefill: {num_q_heads} query heads over {num_kv_heads} kv heads not supported"
-        )
     out = torch.empty(total, num_q_heads, head_dim, dtype=query.dtype, device=device)
     if total == 0:
         return out
-    bt = block_table
-    if bt.dim() != 2:
-        bt = bt.reshape(-1, bt.shape[-1] if bt.dim() else 0)
-    if any(cached):
-        _check_prefix_tables(bt.detach().to("cpu", torch.int64), rows, cached, block_size,
-                             num_blocks)
-    bt = bt.to(device)
-    if bt.dtype not in (torch.int32, torch.int64):
-        bt = bt.to(torch.int64)
-    if bt.numel() and bt.stride(1) != 1:
-        bt = bt.contiguous()
-
-    # per sequence (table row, cached, first chunk row, chunk tokens); work
-    # groups (sequence, kv head, first token, tokens), the most keys first
-    seqs, items, keys = [], [], []
-    start = 0
-    for i, (r, c, ql) in enumerate(zip(rows, cached, qlens)):
-        seqs.append((r, c, start, ql))
-        for t0 in range(0, ql, tpg):
-            nt = min(tpg, ql - t0)
-            for h in range(num_kv_heads):
-                items.append((i, h, t0, nt))
-                keys.append(c + t0 + nt)
-        start += ql
-    if not items:
-        return out
-    order = sorted(range(len(items)), key=lambda k: -keys[k])
-    work = torch.tensor([items[k] for k in order], dtype=torch.int32).to(device, non_blocking=True)
-    meta = torch.tensor(seqs, dtype=torch.int64).to(device, non_blocking=True)
+    bt, meta, work, n_work = _prefill_plan(block_table, rows, cached, qlens, block_size,
+                                           num_blocks, num_q_heads, num_kv_heads, head_dim,
+                                           device)
 
     q = _aligned_rows(query)
     k = _aligned_rows(key)
@@ -850,7 +869,7 @@ def hip_prefill_attention(
             _ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), k.stride(1),
             _ptr(v), v.stride(0), v.stride(1), _ptr(key_cache), _ptr(value_cache),
             _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
-            bt.stride(0) if bt.numel() else 0, _ptr(meta), len(seqs), _ptr(work), len(items),
+            bt.stride(0) if bt.numel() else 0, _ptr(meta), len(rows), _ptr(work), n_work,
             _ptr(out), out.stride(0), out.stride(1), float(head_dim ** -0.5), num_q_heads,
             num_kv_heads, head_dim, block_size, num_blocks, _hip.MV_DTYPE[query.dtype],
             _stream(device),
