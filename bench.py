@@ -3,15 +3,17 @@
 One *step* is one decode-layer call of the attention backend on the
 headline workload (c2: 14 query / 2 kv heads, head_dim 64, block 16, bf16,
 batch 64, kv_len ~ U{128..2048}): the KV write of the step's 64 new tokens
-followed by the paged decode over every sequence's blocks. Successive steps
+and the paged decode over every sequence's blocks, as one launch (the write
+fused into the decode kernel; pool and output bit-identical to the two
+separate calls, which are timed beside it). Successive steps
 use successive layers of a pool that holds >= 1 GiB in total (the same step
 metadata, a different layer's K/V, as in a real engine step), so the
 256 MB Infinity Cache cannot serve the reads and the measured bandwidth is
 HBM bandwidth. All inputs are resident in HBM before timing starts.
 
 Printed (one JSON line): ``value`` = algorithmic bytes of the layer call
-(decode + write) / µs per layer call, in GB/s; ``roofline`` for the decode
-kernel (one launch, cross-partition merge fused) against 8 TB/s; and
+(decode + write) / µs per layer call, in GB/s; ``roofline`` for that one
+kernel (KV write and cross-partition merge fused) against 8 TB/s; and
 ``cpu_baseline`` = the oracle's PyTorch CPU path (the reference's
 per-sequence gather + SDPA loop) timed on this host's cores on the same
 workload in fp32.
@@ -19,7 +21,7 @@ workload in fp32.
     python bench.py [--steps K] [--warmup W] [--workload c2] [--no-cpu-baseline]
     python bench.py --copy-calibration   # plain 256 MiB copies, for PMC byte scaling
 
-``roofline.traffic`` (HBM bytes per decode launch) comes from the
+``roofline.traffic`` (HBM bytes per layer-call launch) comes from the
 rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under profiles/ for
 the workload, when there is one; otherwise it is null.
 """
@@ -255,12 +257,13 @@ def cpu_baseline(spec, layout, layer, budget_s=12.0):
     }
 
 
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "paged_decode_kernel_{workload}_traffic.md")
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "paged_decode_write_kernel_{workload}_traffic.md")
 COPY_BYTES = 256 << 20
 
 
 def measured_traffic(workload):
-    """HBM bytes per decode launch from the committed PMC summary (a line
+    """HBM bytes per layer-call launch (the decode kernel with the KV write
+    fused) from the committed PMC summary (a line
     ``traffic_bytes_per_launch: N``), or None."""
     path = TRAFFIC_SUMMARY.format(workload=workload)
     try:
@@ -335,7 +338,13 @@ def main(argv=None) -> int:
                        spec.num_kv_heads)
     plan_us = plan_step_us(bt, kv, bs, layout.num_blocks, dev, spec, plan_decode)
 
-    def layer_call(i):
+    def layer_call(i):  # one launch: the step's KV write fused into the decode
+        L = layers[i % n_layers]
+        outs[i % n_layers] = hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs,
+                                                  new_key=L["nk"], new_value=L["nv"],
+                                                  slot_mapping=slots)
+
+    def layer_call_two(i):  # the reference's two calls: write, then decode
         L = layers[i % n_layers]
         hip_cache_write(L["nk"], L["nv"], L["k"], L["v"], slots, bs)
         outs[i % n_layers] = hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs)
@@ -349,14 +358,18 @@ def main(argv=None) -> int:
         hip_cache_write(L["nk"], L["nv"], L["k"], L["v"], slots, bs)
 
     for i in range(args.warmup):
+        layer_call_two(i)
         layer_call(i)
     torch.cuda.synchronize()
     log(f"[bench] warmup done ({args.warmup} steps); timing {args.steps} steps")
     us_step = time_loop(layer_call, args.steps, stream)
+    us_two = time_loop(layer_call_two, args.steps, stream)
     us_decode = time_loop(decode_only, args.steps, stream)
     us_write = time_loop(write_only, args.steps, stream)
     us_wall = wall_loop(layer_call, args.steps)
-    log(f"[bench] layer call {us_step:.2f} us, decode {us_decode:.2f} us, write {us_write:.2f} us")
+    us_two_wall = wall_loop(layer_call_two, args.steps)
+    log(f"[bench] layer call {us_step:.2f} us (write fused); write + decode calls {us_two:.2f} us "
+        f"(decode {us_decode:.2f}, write {us_write:.2f})")
 
     # A whole decode step captured into one HIP graph: the plan (replanned
     # from the static metadata at every replay) and Qwen2-0.5B's 24 layer
@@ -412,7 +425,6 @@ def main(argv=None) -> int:
     dec_bytes = decode_bytes(layout, spec.dtype)
     wr_bytes = write_bytes(layout, spec.dtype)
     gbs = (dec_bytes + wr_bytes) / us_step / 1e3
-    dec_gbs = dec_bytes / us_decode / 1e3
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -437,9 +449,14 @@ def main(argv=None) -> int:
             "parallelism": "single GPU",
         },
         "us_per_layer_call": round(us_step, 3),
+        "layer_call": "one launch: decode with the step's KV write fused (hip_decode_attention "
+                      "with new_key/new_value/slot_mapping); pool and output bit-identical to "
+                      "the two calls",
+        "two_call_us_per_layer_call": round(us_two, 3),
         "decode_us": round(us_decode, 3),
         "write_us": round(us_write, 3),
         "host_inclusive_us_per_layer_call": round(us_wall, 3),
+        "two_call_host_inclusive_us": round(us_two_wall, 3),
         "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "plan_us_per_step": round(plan_us, 1),
         "graph_step": {
@@ -461,12 +478,14 @@ def main(argv=None) -> int:
         "work_groups": plan.num_groups,
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_kernel (one launch, partition merge fused)",
-            "achieved": round(dec_gbs, 2),
+            "kernel": "paged_decode_kernel with the KV write fused (one launch per layer call, "
+                      "partition merge fused)",
+            "achieved": round(gbs, 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
-            "frac": round(dec_gbs / PEAK_HBM_GBS, 4),
-            "algorithmic_bytes": dec_bytes,
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "algorithmic_bytes": dec_bytes + wr_bytes,
+            "decode_only_frac": round(dec_bytes / us_decode / 1e3 / PEAK_HBM_GBS, 4),
             "traffic": measured_traffic(spec.name),
         },
         "cpu_baseline": None,

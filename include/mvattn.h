@@ -279,6 +279,34 @@ int mv_rope_kv_cache_write(const void* query, int64_t q_stride_tok, int64_t q_st
 int mv_positions_check(const int64_t* positions, int64_t num_tokens, int64_t max_positions,
                        int32_t* status, void* stream);
 
+/*
+ * Decode layer call with the step's KV write fused in (no counterpart
+ * function in the reference: it does `triton_cache_write` of the decode
+ * tokens (paged_attention_gpu.py:90-154) and `triton_decode_attention`
+ * (:252-321) in one launch). Arguments as mv_paged_decode, plus the new
+ * rows new_key / new_value [num_seqs, num_kv_heads, head_dim] (strides in
+ * elements, 16-byte aligned rows) and slot_mapping [num_seqs] int64:
+ * row b is stored bitwise into pool slot slot_mapping[b] (-1 skips; slots
+ * outside the pool are skipped -- mv_kv_slots_check reports them and
+ * duplicates first). Sequence b's last token (kv_len - 1) is taken from
+ * the new rows when its slot is that token's table position, which is
+ * what the block manager produces; otherwise it is read from the pool.
+ * Precondition, as the block manager guarantees: no slot lies in a block
+ * that another sequence of the batch attends. The output and the pool are
+ * then bit-identical to mv_kv_cache_write followed by mv_paged_decode.
+ */
+int mv_paged_decode_write(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                          const void* new_key, int64_t nk_stride_tok, int64_t nk_stride_head,
+                          const void* new_value, int64_t nv_stride_tok, int64_t nv_stride_head,
+                          const int64_t* slot_mapping, void* key_cache, void* value_cache,
+                          const int32_t* work_items, const int32_t* block_ids,
+                          int64_t block_ids_capacity, int32_t num_work_groups,
+                          int32_t partition_tokens, int32_t max_partitions, int32_t* counters,
+                          void* out, int64_t out_stride_tok, int64_t out_stride_head, float scale,
+                          int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t dtype,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* Query tokens one mv_paged_prefill work group covers for this head shape
  * (0: unsupported; at most 16 query heads per kv head at head_dim 128, 32
  * at 64). */

@@ -141,6 +141,13 @@ struct DecodeArgs {
   int64_t out_stride_tok, out_stride_head;  // elements
   float* ws_o;                              // [num_seqs, Hq, max_parts, D]
   float* ws_ml;                             // [num_seqs, Hq, max_parts, 2]: (max, sum)
+  // Fused KV write of the step's new tokens (FUSED kernels only): row b of
+  // new_k / new_v goes to pool slot slots[b].
+  const char* new_k;
+  const char* new_v;
+  int64_t nk_st, nk_sh, nv_st, nv_sh;  // bytes
+  const int64_t* slots;
+  int64_t total_slots;
 };
 
 // --------------------------------------------------------------- MFMA ----
@@ -163,7 +170,7 @@ __device__ __forceinline__ float unpack_hi(uint64_t v) { return __uint_as_float(
 
 // ----------------------------------------------------------- the kernel ---
 
-template <int DTYPE, int D>
+template <int DTYPE, int D, bool FUSED>
 __global__ __launch_bounds__(kWaves * 64)
 __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged_decode_kernel(DecodeArgs a) {
   using Tr = Traits<DTYPE, D>;
@@ -218,6 +225,33 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const int first_blk = tok_begin >> a.bs_log2;  // s_ids[i] = pool block of table entry first_blk + i
   const char* wave_tiles = s_lds + wave * Tr::kWaveLds;  // [stage][K, V][tile bytes]
   const uint32_t wave_tiles_lds = lds0 + wave * Tr::kWaveLds;
+
+  // ---- fused KV write (FUSED): the work group holding sequence b's last
+  // token stores the new K / V rows of b into slot slots[b] once its loop
+  // is done. When that slot is the token's table position (as the block
+  // manager lays it out) the token's row in the LDS tile is overwritten
+  // with the new rows -- the bytes the write stores -- before it is used;
+  // otherwise the token is the one read from the pool. Wave new_wave (the
+  // one whose tile holds the token) keeps the rows in registers: lanes
+  // [0, RP) the K row's 16-byte pieces, [RP, 2 RP) the V row's, loaded
+  // before any tile copy so the loop's vmcnt waits still count only tile
+  // copies; the tile copies themselves are those of the plain kernel.
+  const bool last_piece = FUSED && part == n_parts - 1;
+  const int new_wave = ((tok_end - 1 - tok_begin) / kTile) % kWaves;
+  int64_t new_slot = -1;
+  uint4 new_piece = make_uint4(0, 0, 0, 0);
+  const bool new_lane = wave == new_wave && lane < 2 * RP;
+  const int new_pc = lane < RP ? lane : lane - RP;
+  if constexpr (FUSED) {
+    if (last_piece) {
+      new_slot = a.slots[b];
+      if (new_lane) {
+        const char* src = lane < RP ? a.new_k + b * a.nk_st + h * a.nk_sh
+                                    : a.new_v + b * a.nv_st + h * a.nv_sh;
+        new_piece = *reinterpret_cast<const uint4*>(src + new_pc * 16);
+      }
+    }
+  }
 
   // ---- Q rows of the group -> LDS (wave 0). Rows r >= n_rep repeat row
   // n_rep - 1: MFMA columns (and the softmax state per column) are
@@ -360,6 +394,21 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     wait_vmcnt_groups<2 * L, S - 1>(n_chunks - 1 - k);
     asm volatile("" ::: "memory");
     zero_invalid_v(ST, valid[ST]);
+    if constexpr (FUSED) {
+      // the new token's row: last chunk, wave new_wave, row (tok_end - 1) % 16,
+      // replaced when the slot is the token's table position (checked here,
+      // long after the slot's load was issued)
+      if (last_piece && k == n_chunks - 1 && wave == new_wave) {
+        const int lt = tok_end - 1;
+        const int id = s_ids[min((lt >> a.bs_log2) - first_blk, kIdCap - 1)];
+        if (id >= 0 && new_slot == (static_cast<int64_t>(id) << a.bs_log2) + (lt & bs_mask) &&
+            lane < 2 * RP) {
+          const int r = (lt - tok_begin) % kTile;
+          char* tile = s_lds + wave * Tr::kWaveLds + ST * Tr::kStageBytes + (lane < RP ? 0 : Tr::kTileBytes);
+          *reinterpret_cast<uint4*>(tile + (r * RP + (new_pc ^ piece_swizzle<RP>(r))) * 16) = new_piece;
+        }
+      }
+    }
     compute_tile(k, ST);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage's LDS accesses are done
     asm volatile("" ::: "memory");
@@ -391,6 +440,15 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     if constexpr (S > 3) {
       if (k + 3 >= n_chunks) break;
       step(k + 3, IntC<3>{});
+    }
+  }
+
+  if constexpr (FUSED) {  // the KV write of the new token (-1 skips)
+    if (last_piece && new_lane && new_slot >= 0 && new_slot < a.total_slots) {
+      const int64_t blk = new_slot >> a.bs_log2;
+      const int64_t row = ((blk * a.num_kv_heads + h) << a.bs_log2) + (new_slot & bs_mask);
+      char* dst = const_cast<char*>(lane < RP ? a.k_cache : a.v_cache) + row * Tr::kRowBytes;
+      *reinterpret_cast<uint4*>(dst + new_pc * 16) = new_piece;
     }
   }
 
@@ -1069,7 +1127,8 @@ int chunk_tokens(int head_dim, int dtype) { return trait_value<ChunkOf>(head_dim
 
 template <int DTYPE, int D>
 int launch_decode(const DecodeArgs& a, int num_groups, hipStream_t s) {
-  paged_decode_kernel<DTYPE, D><<<static_cast<unsigned>(num_groups), kWaves * 64, 0, s>>>(a);
+  if (a.new_k) paged_decode_kernel<DTYPE, D, true><<<static_cast<unsigned>(num_groups), kWaves * 64, 0, s>>>(a);
+  else paged_decode_kernel<DTYPE, D, false><<<static_cast<unsigned>(num_groups), kWaves * 64, 0, s>>>(a);
   return check_launch("mv_paged_decode");
 }
 
@@ -1077,6 +1136,15 @@ template <int DTYPE>
 int launch_decode_d(const DecodeArgs& a, int d, int num_groups, hipStream_t s) {
   return d == 64 ? launch_decode<DTYPE, 64>(a, num_groups, s) : launch_decode<DTYPE, 128>(a, num_groups, s);
 }
+
+// The step's new rows for the fused KV write (mv_paged_decode_write).
+struct NewRows {
+  const void* key;
+  int64_t key_stride_tok, key_stride_head;      // elements
+  const void* value;
+  int64_t value_stride_tok, value_stride_head;  // elements
+  const int64_t* slots;
+};
 
 }  // namespace
 }  // namespace mv
@@ -1112,7 +1180,10 @@ extern "C" int mv_decode_graph_bounds(int32_t num_seqs, int32_t max_blocks, int3
   const int64_t max_parts =
       std::max<int64_t>(1, std::min<int64_t>(kMaxParts, (max_tiles + kWaves - 1) / kWaves));
   const int64_t units = static_cast<int64_t>(num_kv_heads) * num_seqs;
-  const int64_t target = static_cast<int64_t>(std::max(2, groups_per_cu)) * cu_count;
+  // the plan's resident target: 2 per CU when its (live) units fit the CUs
+  const int gpc = std::max(1, groups_per_cu);
+  const int64_t target =
+      static_cast<int64_t>(units <= cu_count ? std::min(2, gpc) : std::max(2, gpc)) * cu_count;
   const int64_t by_fair = units + std::max<int64_t>(target, (units * max_tiles + l_cap - 1) / l_cap);
   const int64_t groups = std::min<int64_t>(by_fair, units * max_parts);
   if (groups > INT_MAX / 8)
@@ -1215,7 +1286,8 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
   return check_launch("mv_decode_plan");
 }
 
-extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+namespace mv {
+int decode_launch(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
                                const void* key_cache, const void* value_cache,
                                const int32_t* work_items, const int32_t* block_ids,
                                int64_t block_ids_capacity, int32_t num_work_groups,
@@ -1224,8 +1296,7 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
                                float scale, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                int64_t num_blocks, int32_t dtype, void* workspace,
-                               size_t workspace_bytes, void* stream) {
-  using namespace mv;
+                               size_t workspace_bytes, const NewRows* nr, void* stream) {
   const int eb = dtype_bytes(dtype);
   if (eb == 0) return fail(MV_ERR_UNSUPPORTED, "mv_paged_decode: unknown dtype %d", dtype);
   if (head_dim != 64 && head_dim != 128)
@@ -1307,10 +1378,66 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
     a.ws_o = static_cast<float*>(workspace);
     a.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((o + 255) / 256) * 256);
   }
+  a.new_k = nullptr;
+  a.new_v = nullptr;
+  a.nk_st = a.nk_sh = a.nv_st = a.nv_sh = 0;
+  a.slots = nullptr;
+  a.total_slots = num_blocks * block_size;
+  if (nr) {
+    if (!nr->key || !nr->value || !nr->slots)
+      return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode_write: null new rows or slots");
+    if ((reinterpret_cast<uintptr_t>(nr->key) | reinterpret_cast<uintptr_t>(nr->value)) % 16 ||
+        ((nr->key_stride_tok | nr->key_stride_head | nr->value_stride_tok |
+          nr->value_stride_head) * eb) % 16)
+      return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode_write: new rows not 16-byte aligned");
+    a.new_k = static_cast<const char*>(nr->key);
+    a.new_v = static_cast<const char*>(nr->value);
+    a.nk_st = nr->key_stride_tok * eb;
+    a.nk_sh = nr->key_stride_head * eb;
+    a.nv_st = nr->value_stride_tok * eb;
+    a.nv_sh = nr->value_stride_head * eb;
+    a.slots = nr->slots;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, num_work_groups, s);
     case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, num_work_groups, s);
     default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, num_work_groups, s);
   }
+}
+}  // namespace mv
+
+extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                               const void* key_cache, const void* value_cache,
+                               const int32_t* work_items, const int32_t* block_ids,
+                               int64_t block_ids_capacity, int32_t num_work_groups,
+                               int32_t partition_tokens, int32_t max_partitions, int32_t* counters,
+                               void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                               float scale, int32_t num_seqs, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                               int64_t num_blocks, int32_t dtype, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return mv::decode_launch(query, q_stride_tok, q_stride_head, key_cache, value_cache, work_items,
+                           block_ids, block_ids_capacity, num_work_groups, partition_tokens,
+                           max_partitions, counters, out, out_stride_tok, out_stride_head, scale,
+                           num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                           dtype, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int mv_paged_decode_write(
+    const void* query, int64_t q_stride_tok, int64_t q_stride_head, const void* new_key,
+    int64_t nk_stride_tok, int64_t nk_stride_head, const void* new_value, int64_t nv_stride_tok,
+    int64_t nv_stride_head, const int64_t* slot_mapping, void* key_cache, void* value_cache,
+    const int32_t* work_items, const int32_t* block_ids, int64_t block_ids_capacity,
+    int32_t num_work_groups, int32_t partition_tokens, int32_t max_partitions, int32_t* counters,
+    void* out, int64_t out_stride_tok, int64_t out_stride_head, float scale, int32_t num_seqs,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int64_t num_blocks, int32_t dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const mv::NewRows nr{new_key, nk_stride_tok, nk_stride_head, new_value, nv_stride_tok,
+                       nv_stride_head, slot_mapping};
+  return mv::decode_launch(query, q_stride_tok, q_stride_head, key_cache, value_cache, work_items,
+                           block_ids, block_ids_capacity, num_work_groups, partition_tokens,
+                           max_partitions, counters, out, out_stride_tok, out_stride_head, scale,
+                           num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                           dtype, workspace, workspace_bytes, &nr, stream);
 }

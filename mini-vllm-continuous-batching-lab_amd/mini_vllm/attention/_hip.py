@@ -97,6 +97,18 @@ SIGNATURES = {
         _I32, _I64, _I32, _P,      # block_size, num_blocks, dtype, stream
     ]),
     "mv_positions_check": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "mv_paged_decode_write": (ctypes.c_int, [
+        _P, _I64, _I64,            # query, strides
+        _P, _I64, _I64,            # new_key, strides
+        _P, _I64, _I64,            # new_value, strides
+        _P, _P, _P,                # slot_mapping, key_cache, value_cache
+        _P, _P, _I64, _I32,        # work_items, block_ids, block_ids_capacity, num_work_groups
+        _I32, _I32, _P,            # partition_tokens, max_partitions, counters
+        _P, _I64, _I64,            # out, strides
+        _F, _I32, _I32, _I32, _I32,  # scale, num_seqs, num_q_heads, num_kv_heads, head_dim
+        _I32, _I64, _I32,          # block_size, num_blocks, dtype
+        _P, _SZ, _P,               # workspace, workspace_bytes, stream
+    ]),
     "mv_prefill_tokens_per_group": (ctypes.c_int, [_I32, _I32, _I32]),
     "mv_paged_prefill": (ctypes.c_int, [
         _P, _I64, _I64,            # query, strides

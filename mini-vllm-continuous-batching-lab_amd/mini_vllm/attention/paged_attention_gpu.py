@@ -431,6 +431,10 @@ def hip_decode_attention(
     block_table: torch.Tensor,
     kv_len_after: torch.Tensor,
     block_size: int,
+    *,
+    new_key: Optional[torch.Tensor] = None,
+    new_value: Optional[torch.Tensor] = None,
+    slot_mapping: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Paged decode attention on the HIP kernels.
 
@@ -445,6 +449,14 @@ def hip_decode_attention(
     Returns ``[total_decode, num_q_heads, head_dim]`` in ``query.dtype``.
     Query head h attends kv head ``h // (num_q_heads // num_kv_heads)`` with
     scale ``head_dim ** -0.5``.
+
+    With ``new_key`` / ``new_value`` ``[total_decode, num_kv_heads,
+    head_dim]`` and ``slot_mapping`` ``[total_decode]`` the call also does
+    the step's KV write of those rows (``triton_cache_write``, with its
+    checks) in the same launch: pool and output are bit-identical to
+    ``hip_cache_write`` followed by this call without them, provided no
+    slot lies in a block another sequence of the batch attends (what the
+    block manager guarantees).
     """
     total_decode, num_q_heads, head_dim = query.shape
     num_kv_heads = key_cache.shape[1]
@@ -480,6 +492,37 @@ def hip_decode_attention(
     lib = _hip.load()
     ws_bytes = lib.mv_paged_decode_workspace_bytes(total_decode, num_q_heads, head_dim, plan.max_parts)
     ws = _workspace(device, ws_bytes) if ws_bytes else None
+    if new_key is not None:
+        assert new_value is not None and slot_mapping is not None
+        assert new_key.shape == (total_decode, num_kv_heads, head_dim), (
+            f"new_key {tuple(new_key.shape)} != ({total_decode}, {num_kv_heads}, {head_dim})"
+        )
+        assert new_value.shape == new_key.shape
+        assert new_key.dtype == query.dtype and new_value.dtype == query.dtype
+        assert new_key.device == device and new_value.device == device
+        assert slot_mapping.shape == (total_decode,)
+        if slot_mapping.device != device:
+            slot_mapping = slot_mapping.to(device)
+        if slot_mapping.dtype != torch.int64:
+            slot_mapping = slot_mapping.to(torch.int64)
+        slot_mapping = slot_mapping.contiguous()
+        _check_slots(slot_mapping, num_blocks * block_size)
+        nk, nv = _aligned_rows(new_key), _aligned_rows(new_value)
+        _hip.check(
+            lib.mv_paged_decode_write(
+                _ptr(query), query.stride(0), query.stride(1),
+                _ptr(nk), nk.stride(0), nk.stride(1), _ptr(nv), nv.stride(0), nv.stride(1),
+                _ptr(slot_mapping), _ptr(key_cache), _ptr(value_cache),
+                _ptr(plan.work), _ptr(plan.block_ids), plan.block_ids.numel(), plan.num_groups,
+                plan.partition_tokens, plan.max_parts, _ptr(plan.counters),
+                _ptr(output), output.stride(0), output.stride(1),
+                float(head_dim ** -0.5), total_decode, num_q_heads, num_kv_heads, head_dim,
+                block_size, num_blocks, _hip.MV_DTYPE[query.dtype],
+                _ptr(ws), ws.numel() if ws is not None else 0, _stream(device),
+            ),
+            "mv_paged_decode_write",
+        )
+        return output
     _hip.check(
         lib.mv_paged_decode(
             _ptr(query), query.stride(0), query.stride(1),
@@ -997,6 +1040,33 @@ class AttentionBackendGPU(AttentionBackend):
         return hip_decode_attention(
             query, pool.key_caches[layer_idx], pool.value_caches[layer_idx],
             attn_metadata.decode_block_tables, group.kv_len_after, pool.block_size,
+        )
+
+    def decode_attention_with_write(
+        self,
+        layer_idx: int,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        slot_mapping: torch.Tensor,
+        attn_metadata: AttentionMetadata,
+        pool: KVCachePool,
+    ) -> torch.Tensor:
+        """``write_kv_cache(layer, key, value, slot_mapping)`` of the decode
+        tokens and ``decode_attention(layer, query, ...)`` in one launch
+        (the runner's two calls, qwen_runner.py:168-190, for the decode
+        rows). ``key`` / ``value`` / ``slot_mapping`` are the decode rows
+        (``k[num_prefill:]`` ...); same results as the two calls."""
+        if query.shape[0] == 0:
+            return query
+        group = _find_group(attn_metadata, ("decode_gpu",))
+        if group is None:
+            self.write_kv_cache(layer_idx, key, value, slot_mapping)
+            return query
+        return hip_decode_attention(
+            query, pool.key_caches[layer_idx], pool.value_caches[layer_idx],
+            attn_metadata.decode_block_tables, group.kv_len_after, pool.block_size,
+            new_key=key, new_value=value, slot_mapping=slot_mapping,
         )
 
     def prefill_attention(

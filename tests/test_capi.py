@@ -117,8 +117,12 @@ def test_graph_bounds(lib):
     groups, part, parts = list(out)
     assert part == 511 * 16  # the widest piece: 511 table entries
     assert parts == 128 // 4  # pieces of at least 4 tiles
-    # units + max(resident target, units * tiles / widest piece), capped by units * parts
-    assert groups == min(128 + max(3 * 256, -(-128 * 128 // 511)), 128 * parts)
+    # units + max(resident target, units * tiles / widest piece), capped by units * parts;
+    # 128 units fit 256 CUs, so the plan aims at 2 groups per CU
+    assert groups == min(128 + max(2 * 256, -(-128 * 128 // 511)), 128 * parts)
+    # more units than CUs: all 3 slots per CU
+    assert lib.mv_decode_graph_bounds(256, 128, 16, 2, 3, 256, out) == 0
+    assert list(out)[0] == min(512 + max(3 * 256, -(-512 * 128 // 511)), 512 * 32)
     # tiny tables: at most one piece per sequence
     assert lib.mv_decode_graph_bounds(10, 2, 16, 2, 3, 256, out) == 0
     assert list(out)[0] == 20 and list(out)[2] == 1

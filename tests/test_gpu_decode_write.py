@@ -1,0 +1,103 @@
+"""Decode layer call with the KV write fused in (mv_paged_decode_write).
+
+It must leave the pool and the output bit-identical to the two calls it
+replaces: hip_cache_write of the step's new rows, then hip_decode_attention.
+In the NaN-filled cases every slot about to be written holds NaN, so a
+fused call that read the new token from the pool, or skipped the write,
+would not match.
+"""
+
+import pytest
+import torch
+
+from benchmarks.paged_decode_workloads import make_case
+from gpu_util import DEV, TOL, bits, oracle_step, say, to_device
+from mini_vllm.attention import AttentionBackend
+from mini_vllm.attention.paged_attention_gpu import hip_cache_write, hip_decode_attention
+from mini_vllm.model_runner.base import AttentionGroup, AttentionMetadata, ModelConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def _both(case, slots=None, new_k=None, new_v=None):
+    d = to_device(case)
+    bs = case.layout.spec.block_size
+    slots = d.slot_mapping if slots is None else slots.to(DEV)
+    nk = d.new_key if new_k is None else new_k
+    nv = d.new_value if new_v is None else new_v
+    kc1, vc1 = d.key_cache.clone(), d.value_cache.clone()
+    hip_cache_write(nk, nv, kc1, vc1, slots, bs)
+    out1 = hip_decode_attention(d.query, kc1, vc1, d.block_table, d.kv_len, bs)
+    kc2, vc2 = d.key_cache.clone(), d.value_cache.clone()
+    out2 = hip_decode_attention(d.query, kc2, vc2, d.block_table, d.kv_len, bs,
+                                new_key=nk, new_value=nv, slot_mapping=slots)
+    torch.cuda.synchronize()
+    return (out1, kc1, vc1), (out2, kc2, vc2)
+
+
+def _same(a, b):
+    for x, y in zip(a, b):
+        assert torch.equal(bits(x.cpu()), bits(y.cpu()))
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+def test_fused_equals_write_then_decode(name):
+    say("decode+write", name)
+    case = make_case(name, seed=0, nan_fill=True)
+    ref, fused = _both(case)
+    _same(ref, fused)
+    out = fused[0].float().cpu()
+    want, _, _ = oracle_step(case)
+    assert not torch.isnan(out).any()
+    assert (out - want).abs().max().item() <= TOL[case.layout.spec.dtype]
+
+
+def test_slot_off_the_table_and_skipped_slot():
+    """Sequence 0's slot is a free block's row (not its table position) and
+    sequence 1's is -1: the fused call reads those sequences' last tokens
+    from the pool and writes (or skips) exactly as the two calls do."""
+    say("decode+write: off-table and -1 slots")
+    case = make_case("c2", seed=1, nan_fill=False)
+    lay = case.layout
+    slots = case.slot_mapping.clone()
+    used = set(int(x) for x in case.block_table.flatten().tolist() if x >= 0)
+    free = next(b for b in range(lay.num_blocks) if b not in used)
+    slots[0] = free * lay.spec.block_size + 3
+    slots[1] = -1
+    ref, fused = _both(case, slots=slots)
+    _same(ref, fused)
+
+
+def test_strided_new_rows():
+    """New K / V as column views of one [B, 2 Hkv D] buffer."""
+    say("decode+write: strided rows")
+    case = make_case("c2", seed=2, nan_fill=True)
+    b, hkv, d = case.new_key.shape
+    kv = torch.cat([case.new_key.reshape(b, -1), case.new_value.reshape(b, -1)], dim=1).to(DEV)
+    nk = kv[:, : hkv * d].view(b, hkv, d)
+    nv = kv[:, hkv * d:].view(b, hkv, d)
+    ref, fused = _both(case, new_k=nk, new_v=nv)
+    _same(ref, fused)
+
+
+def test_backend_method():
+    say("decode+write: backend method")
+    case = make_case("c1", seed=3, nan_fill=True)
+    spec, lay = case.layout.spec, case.layout
+    cfg = ModelConfig(num_layers=1, num_heads=spec.num_q_heads, num_kv_heads=spec.num_kv_heads,
+                      head_dim=spec.head_dim, dtype=spec.dtype)
+    be = AttentionBackend.create(cfg, backend="hip")
+    pool = be.allocate_pool(1, lay.num_blocks, spec.block_size, spec.num_kv_heads, spec.head_dim,
+                            spec.dtype, DEV)
+    d = to_device(case)
+    pool.key_caches[0].copy_(d.key_cache)
+    pool.value_caches[0].copy_(d.value_cache)
+    kv = d.kv_len
+    group = AttentionGroup(list(range(len(kv))), "decode_gpu", kv - 1, torch.ones_like(kv), kv)
+    meta = AttentionMetadata(groups=[group], decode_block_tables=d.block_table,
+                             decode_slot_mapping=d.slot_mapping, block_size=spec.block_size,
+                             num_kv_heads=spec.num_kv_heads, head_dim=spec.head_dim)
+    out = be.decode_attention_with_write(0, d.query, d.new_key, d.new_value, d.slot_mapping, meta, pool)
+    ref, _ = _both(case)
+    torch.cuda.synchronize()
+    _same(ref, (out, pool.key_caches[0], pool.value_caches[0]))
