@@ -59,22 +59,39 @@ __device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_F32>(const uint4& k, const uin
   return acc;
 }
 
-// O tile update for one 16-token tile from its swizzled LDS tile:
-// o[c] += P(16 heads x 16 tokens) V(16 tokens x 16 dims), V element
-// (row 4g+e, column 16c+t) per lane.
-template <int DTYPE, int D>
-__device__ __forceinline__ void mfma_pv(const float (&p)[4], const char* v_tile, int g, int t,
-                                        f32x4 (&o)[D / 16]) {
+// V elements (row 4g+e, column 16c+t), e = 0..3, of a swizzled 16-bit LDS
+// tile in one instruction: gfx950's transposed LDS read. Within each group
+// of 16 lanes, lane i receives halfword (i % 4) of the 8 bytes that lane
+// 4e + i / 4 of the group addresses, for e = 0..3 (lane layout measured on
+// the hardware with an in-bounds probe). Lane (g, t) therefore addresses
+// row 4g + t/4 at columns 16c + 4(t%4) .. +3 and gets column 16c+t of rows
+// 4g..4g+3 -- the B operand of a 16x16x16 MFMA with K = tokens.
+template <int RP>
+__device__ __forceinline__ s16x4 v_column_tr(const char* v_tile, int g, int t, int c) {
+  const int row = 4 * g + (t >> 2);
+  const int col = 16 * c + 4 * (t & 3);  // halfword column, 8-byte aligned
+  const int piece = col >> 3;            // 8 halfwords per 16-byte piece
+  const char* src = v_tile + row * RP * 16 + ((piece ^ piece_swizzle<RP>(row)) << 4) + ((col & 7) << 1);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(const_cast<char*>(src)));
+}
+
+// O tile update for one 16-token tile from its swizzled LDS tile, for R
+// row tiles that share the tile: o[r][c] += P_r(16 rows x 16 tokens)
+// V(16 tokens x 16 dims), V element (row 4g+e, column 16c+t) per lane.
+template <int DTYPE, int D, int R>
+__device__ __forceinline__ void mfma_pv_rows(const float (&p)[R][4], const char* v_tile, int g,
+                                             int t, f32x4 (&o)[R][D / 16]) {
   using Tr = TileGeom<DTYPE, D>;
   constexpr int RP = Tr::kRowPieces;
   constexpr int EPP = Tr::kElemsPerPiece;
-  int row_base[4], row_sw[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    row_base[e] = (4 * g + e) * RP * 16;
-    row_sw[e] = piece_swizzle<RP>(4 * g + e);
-  }
   if constexpr (DTYPE == MV_DTYPE_F32) {
+    int row_base[4], row_sw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      row_base[e] = (4 * g + e) * RP * 16;
+      row_sw[e] = piece_swizzle<RP>(4 * g + e);
+    }
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       const int col = 16 * c + t;
@@ -82,30 +99,40 @@ __device__ __forceinline__ void mfma_pv(const float (&p)[4], const char* v_tile,
       for (int e = 0; e < 4; ++e) {
         const int off = row_base[e] + (((col / EPP) ^ row_sw[e]) << 4) + (col % EPP) * 4;
         const float vv = *reinterpret_cast<const float*>(v_tile + off);
-        o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[e], vv, o[c], 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          o[r][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r][e], vv, o[r][c], 0, 0, 0);
       }
     }
   } else {
-    s16x4 pa;
+    s16x4 pa[R];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pa[e] = static_cast<short>(from_f32<DTYPE>(p[e]));
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pa[r][e] = static_cast<short>(from_f32<DTYPE>(p[r][e]));
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
-      const int col = 16 * c + t;
-      s16x4 vb;
+      const s16x4 vb = v_column_tr<RP>(v_tile, g, t, c);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int off = row_base[e] + (((col / EPP) ^ row_sw[e]) << 4) + (col % EPP) * 2;
-        vb[e] = *reinterpret_cast<const short*>(v_tile + off);
-      }
-      if constexpr (DTYPE == MV_DTYPE_BF16) {
-        o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[c], 0, 0, 0);
-      } else {
-        o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa),
-                                                    __builtin_bit_cast(f16x4, vb), o[c], 0, 0, 0);
+      for (int r = 0; r < R; ++r) {
+        if constexpr (DTYPE == MV_DTYPE_BF16) {
+          o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[r], vb, o[r][c], 0, 0, 0);
+        } else {
+          o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa[r]),
+                                                         __builtin_bit_cast(f16x4, vb), o[r][c], 0,
+                                                         0, 0);
+        }
       }
     }
   }
+}
+
+// One row tile: o[c] += P V.
+template <int DTYPE, int D>
+__device__ __forceinline__ void mfma_pv(const float (&p)[4], const char* v_tile, int g, int t,
+                                        f32x4 (&o)[D / 16]) {
+  mfma_pv_rows<DTYPE, D, 1>(reinterpret_cast<const float(&)[1][4]>(p), v_tile, g, t,
+                            reinterpret_cast<f32x4(&)[1][D / 16]>(o));
 }
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this

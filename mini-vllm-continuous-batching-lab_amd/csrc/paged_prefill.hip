@@ -218,6 +218,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void paged_prefill_kernel(PrefillArg
 #pragma unroll
         for (int rt = 0; rt < R; ++rt) acc[rt] = mfma_qk<DTYPE>(kp, qr[rt][c], acc[rt]);
       }
+      float pr[R][4];
 #pragma unroll
       for (int rt = 0; rt < R; ++rt) {
         float s[4];
@@ -232,12 +233,11 @@ __global__ __launch_bounds__(kPfWaves * 64) void paged_prefill_kernel(PrefillArg
         const float m_new = fmaxf(m_run[rt], mc);
         const float m_ref = m_new == kNegInf ? 0.f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
-        float p[4];
         float lc = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          p[e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e] - m_ref)));
-          lc += p[e];
+          pr[rt][e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e] - m_ref)));
+          lc += pr[rt][e];
         }
         lc += __shfl_xor(lc, 16);
         lc += __shfl_xor(lc, 32);
@@ -249,8 +249,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void paged_prefill_kernel(PrefillArg
 #pragma unroll
           for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
         }
-        mfma_pv<DTYPE, D>(p, v_tile, g, t, o[rt]);
       }
+      mfma_pv_rows<DTYPE, D, R>(pr, v_tile, g, t, o);  // one read of V for all row tiles
     }
   };
 
