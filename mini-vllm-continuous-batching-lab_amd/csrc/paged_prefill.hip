@@ -25,7 +25,8 @@
 //   * prefix keys are addressed through the sequence's block ids, staged
 //     in LDS per window of kPfIdCap blocks; chunk keys through the chunk's
 //     row strides (q / k / v may be views of one fused QKV output).
-// Waves skip sub-tiles that lie wholly past their rows' causal limit.
+// Waves skip sub-tiles that lie wholly past their rows' causal limit; the
+// online softmax is updated once per stage of 64 keys.
 #include <algorithm>
 #include <climits>
 
@@ -201,57 +202,72 @@ __global__ __launch_bounds__(kPfWaves * 64) void paged_prefill_kernel(PrefillArg
         *reinterpret_cast<uint4*>(vdst + c * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
   };
 
+  // One stage (4 sub-tiles of 16 keys) for this wave's rows: S^T for every
+  // sub-tile some row may see, one online-softmax update per row tile over
+  // the whole stage (one max / sum exchange and one rescale of O), then
+  // O += P V per sub-tile.
   auto compute_stage = [&](int k, int st) __attribute__((always_inline)) {
+    const int k_first = k * kPfStageTokens;
+    if (k_first > wave_limit) return;  // causal: no row of the wave sees this stage
+    // sub-tiles u < nu hold keys some row of the wave sees
+    const int nu = min(kPfWaves, (wave_limit - k_first) / kTile + 1);
+    const char* stage = s_lds + st * Tr::kStageBytes;
+    const int ksw = piece_swizzle<RP>(t);
+    f32x4 acc[kPfWaves][R];
 #pragma unroll
     for (int u = 0; u < kPfWaves; ++u) {
-      const int kb = k * kPfStageTokens + u * kTile;
-      if (kb > wave_limit) break;  // causal: the rest of the stage is masked for every row
-      const char* k_tile = s_lds + st * Tr::kStageBytes + u * Tr::kSubBytes;
-      const char* v_tile = k_tile + Tr::kTileBytes;
-      f32x4 acc[R];
 #pragma unroll
-      for (int rt = 0; rt < R; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int ksw = piece_swizzle<RP>(t);
+      for (int rt = 0; rt < R; ++rt) acc[u][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (u < nu) {
+        const char* k_tile = stage + u * Tr::kSubBytes;
 #pragma unroll
-      for (int c = 0; c < QP; ++c) {
-        const uint4 kp = *reinterpret_cast<const uint4*>(k_tile + (t * RP + ((g * QP + c) ^ ksw)) * 16);
+        for (int c = 0; c < QP; ++c) {
+          const uint4 kp = *reinterpret_cast<const uint4*>(k_tile + (t * RP + ((g * QP + c) ^ ksw)) * 16);
 #pragma unroll
-        for (int rt = 0; rt < R; ++rt) acc[rt] = mfma_qk<DTYPE>(kp, qr[rt][c], acc[rt]);
-      }
-      float pr[R][4];
-#pragma unroll
-      for (int rt = 0; rt < R; ++rt) {
-        float s[4];
-        float mc = kNegInf;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s[e] = kb + 4 * g + e <= limit[rt] ? acc[rt][e] * a.scale_log2 : kNegInf;
-          mc = fmaxf(mc, s[e]);
-        }
-        mc = fmaxf(mc, __shfl_xor(mc, 16));
-        mc = fmaxf(mc, __shfl_xor(mc, 32));
-        const float m_new = fmaxf(m_run[rt], mc);
-        const float m_ref = m_new == kNegInf ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
-        float lc = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pr[rt][e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e] - m_ref)));
-          lc += pr[rt][e];
-        }
-        lc += __shfl_xor(lc, 16);
-        lc += __shfl_xor(lc, 32);
-        l_run[rt] = l_run[rt] * alpha + lc;
-        m_run[rt] = m_new;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float ar = __shfl(alpha, 4 * g + e);
-#pragma unroll
-          for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
+          for (int rt = 0; rt < R; ++rt) acc[u][rt] = mfma_qk<DTYPE>(kp, qr[rt][c], acc[u][rt]);
         }
       }
-      mfma_pv_rows<DTYPE, D, R>(pr, v_tile, g, t, o);  // one read of V for all row tiles
     }
+    float pr[kPfWaves][R][4];
+#pragma unroll
+    for (int rt = 0; rt < R; ++rt) {
+      float mc = kNegInf;
+#pragma unroll
+      for (int u = 0; u < kPfWaves; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = k_first + u * kTile + 4 * g + e;
+          const float sv = u < nu && key <= limit[rt] ? acc[u][rt][e] * a.scale_log2 : kNegInf;
+          acc[u][rt][e] = sv;
+          mc = fmaxf(mc, sv);
+        }
+      mc = fmaxf(mc, __shfl_xor(mc, 16));
+      mc = fmaxf(mc, __shfl_xor(mc, 32));
+      const float m_new = fmaxf(m_run[rt], mc);
+      const float m_ref = m_new == kNegInf ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
+      float lc = 0.f;
+#pragma unroll
+      for (int u = 0; u < kPfWaves; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pr[u][rt][e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(acc[u][rt][e] - m_ref)));
+          lc += pr[u][rt][e];
+        }
+      lc += __shfl_xor(lc, 16);
+      lc += __shfl_xor(lc, 32);
+      l_run[rt] = l_run[rt] * alpha + lc;
+      m_run[rt] = m_new;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float ar = __shfl(alpha, 4 * g + e);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kPfWaves; ++u)
+      if (u < nu) mfma_pv_rows<DTYPE, D, R>(pr[u], stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, o);
   };
 
   // ---- windows of kPfIdCap prefix blocks (one window below 2048 blocks)
