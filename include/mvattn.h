@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define MVATTN_ABI_VERSION 2
+#define MVATTN_ABI_VERSION 3
 
 /* Element types of query / key / value / cache / output. */
 #define MV_DTYPE_F32 0
@@ -308,9 +308,9 @@ int mv_paged_decode_write(const void* query, int64_t q_stride_tok, int64_t q_str
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* Query tokens one mv_paged_prefill work group covers for this head shape
- * (0: unsupported; at most 16 query heads per kv head at head_dim 128, 32
- * at 64). */
-int mv_prefill_tokens_per_group(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim);
+ * and dtype (0: unsupported; at most 16 query heads per kv head). */
+int mv_prefill_tokens_per_group(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t dtype);
 
 /*
  * Chunked-prefill attention over the paged pool.

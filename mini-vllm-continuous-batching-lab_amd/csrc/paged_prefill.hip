@@ -11,17 +11,17 @@
 // gather + cat + repeat_interleave + masked SDPA, in one pass over the
 // keys with no gathered copy.
 //
-// Work decomposition: one work group of 4 waves per (sequence, kv head,
-// block of query tokens). A wave owns R x 16 MFMA rows (R = 2 at head_dim
-// 64, 1 at 128); row r is query head (h * n_rep + r % n_rep) of token
-// (r / n_rep) of the wave's tpw = 16 R / n_rep tokens, so one K/V pass serves the whole GQA
-// group of several tokens. The four waves share one stream of keys:
-//   * a stage is 64 keys: wave w copies sub-tile w (16 keys of K and V)
+// Work decomposition: one work group of W waves (8, or 4 for fp32 at
+// head_dim 128) per (sequence, kv head, block of query tokens). A wave owns
+// 16 MFMA rows; row r is query head (h * n_rep + r % n_rep) of token
+// (r / n_rep) of the wave's tpw = 16 / n_rep tokens, so one K/V pass serves
+// the whole GQA group of W * tpw tokens. The waves share one stream of keys:
+//   * a stage is 16 W keys: wave w copies sub-tile w (16 keys of K and V)
 //     from HBM straight to LDS (global_load_lds, XOR piece swizzle as in
-//     the decode kernel), kStages stages in flight;
-//   * after one barrier per stage every wave computes all four sub-tiles
-//     for its rows: S^T = K Q^T (MFMA), per-row causal mask key <= cached +
-//     token, online softmax, O += P V (MFMA);
+//     the decode kernel), two stages in flight;
+//   * after one barrier per stage every wave computes all sub-tiles for its
+//     rows: S^T = K Q^T (MFMA), per-row causal mask key <= cached + token,
+//     online softmax, O += P V (MFMA, V read by transposed LDS loads);
 //   * prefix keys are addressed through the sequence's block ids, staged
 //     in LDS per window of kPfIdCap blocks; chunk keys through the chunk's
 //     row strides (q / k / v may be views of one fused QKV output).
@@ -36,23 +36,30 @@
 namespace mv {
 namespace {
 
-constexpr int kPfWaves = 4;
-constexpr int kPfStageTokens = kPfWaves * kTile;  // keys per stage: one 16-key sub-tile per wave
-constexpr int kPfIdCap = 2048;                    // prefix block ids staged in LDS per window
-// 16-row MFMA tiles per wave: two at head_dim 64 (twice the rows per K/V
-// pass), one at 128 (the O accumulators of two would take every register).
-__host__ __device__ constexpr int pf_row_tiles(int d) { return d == 64 ? 2 : 1; }
-
+constexpr int kPfIdCap = 2048;  // prefix block ids staged in LDS per window
+// Waves per work group: 8 (twice the query rows per pass over the keys,
+// and more waves to hide latency -- 52 us against 60 us with 4 on a
+// 4 x (1536 + 512) bf16 step) when two stages of 8 sub-tiles fit the LDS,
+// else 4 (fp32 at head_dim 128). Two stages: a third measured no faster.
 template <int DTYPE, int D>
 struct PfTraits : TileGeom<DTYPE, D> {
   using G = TileGeom<DTYPE, D>;
   static constexpr int kSubBytes = 2 * G::kTileBytes;  // K and V sub-tile of one wave
-  static constexpr int kStageBytes = kPfWaves * kSubBytes;
-  static constexpr int kStages = G::kTileBytes <= 2048 ? 3 : 2;
+  static constexpr int kStages = 2;
+  static constexpr int kWaves = kStages * 8 * kSubBytes + kPfIdCap * 4 <= 160 * 1024 ? 8 : 4;
+  static constexpr int kStageTokens = kWaves * kTile;  // keys per stage: one sub-tile per wave
+  static constexpr int kStageBytes = kWaves * kSubBytes;
   static constexpr int kIdsOffset = kStages * kStageBytes;
   static constexpr int kLdsBytes = kIdsOffset + kPfIdCap * 4;
   static_assert(kLdsBytes <= 160 * 1024, "LDS of one work group");
 };
+
+// Query tokens one work group covers: 16 MFMA rows per wave hold
+// floor(16 / n_rep) tokens' GQA groups.
+template <int DTYPE, int D>
+constexpr int pf_tokens_per_group(int n_rep) {
+  return n_rep > 16 ? 0 : PfTraits<DTYPE, D>::kWaves * (16 / n_rep);
+}
 
 struct PrefillArgs {
   const int32_t* work;   // per work group: (sequence, kv head, first token, tokens)
@@ -75,14 +82,16 @@ struct PrefillArgs {
 };
 
 template <int DTYPE, int D, typename BT>
-__global__ __launch_bounds__(kPfWaves * 64) void paged_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefill_kernel(PrefillArgs a) {
   using Tr = PfTraits<DTYPE, D>;
   using raw_t = typename Elem<DTYPE>::raw;
   constexpr int L = Tr::kLoads;
   constexpr int RP = Tr::kRowPieces;
   constexpr int QP = Tr::kLanePieces;
   constexpr int S = Tr::kStages;
-  constexpr int R = pf_row_tiles(D);
+  constexpr int R = 1;  // 16-row MFMA tiles per wave (two measured slower: fewer work groups)
+  constexpr int kPfWaves = Tr::kWaves;
+  constexpr int kPfStageTokens = Tr::kStageTokens;
 
   __shared__ __attribute__((aligned(16))) char s_lds[Tr::kLdsBytes];
   int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
@@ -334,29 +343,42 @@ __global__ __launch_bounds__(kPfWaves * 64) void paged_prefill_kernel(PrefillArg
 }
 
 template <int DTYPE, int D>
-int launch_prefill(const PrefillArgs& a, int groups, bool bt_i64, hipStream_t s) {
-  if (bt_i64) paged_prefill_kernel<DTYPE, D, int64_t><<<groups, kPfWaves * 64, 0, s>>>(a);
-  else paged_prefill_kernel<DTYPE, D, int32_t><<<groups, kPfWaves * 64, 0, s>>>(a);
+int launch_prefill(PrefillArgs a, int n_rep, int groups, bool bt_i64, hipStream_t s) {
+  constexpr int kThreads = PfTraits<DTYPE, D>::kWaves * 64;
+  a.tpw = pf_tokens_per_group<DTYPE, D>(n_rep) / PfTraits<DTYPE, D>::kWaves;
+  if (bt_i64) paged_prefill_kernel<DTYPE, D, int64_t><<<groups, kThreads, 0, s>>>(a);
+  else paged_prefill_kernel<DTYPE, D, int32_t><<<groups, kThreads, 0, s>>>(a);
   return check_launch("mv_paged_prefill");
 }
 
+template <template <int, int> class F>
+int by_type(int head_dim, int dtype, int n_rep) {
+  const bool d64 = head_dim == 64;
+  switch (dtype) {
+    case MV_DTYPE_F32: return d64 ? F<MV_DTYPE_F32, 64>::get(n_rep) : F<MV_DTYPE_F32, 128>::get(n_rep);
+    case MV_DTYPE_F16: return d64 ? F<MV_DTYPE_F16, 64>::get(n_rep) : F<MV_DTYPE_F16, 128>::get(n_rep);
+    default: return d64 ? F<MV_DTYPE_BF16, 64>::get(n_rep) : F<MV_DTYPE_BF16, 128>::get(n_rep);
+  }
+}
+template <int DTYPE, int D>
+struct TokensPerGroup {
+  static int get(int n_rep) { return pf_tokens_per_group<DTYPE, D>(n_rep); }
+};
+
 template <int DTYPE>
-int launch_prefill_d(const PrefillArgs& a, int d, int groups, bool bt_i64, hipStream_t s) {
-  return d == 64 ? launch_prefill<DTYPE, 64>(a, groups, bt_i64, s)
-                 : launch_prefill<DTYPE, 128>(a, groups, bt_i64, s);
+int launch_prefill_d(const PrefillArgs& a, int d, int n_rep, int groups, bool bt_i64, hipStream_t s) {
+  return d == 64 ? launch_prefill<DTYPE, 64>(a, n_rep, groups, bt_i64, s)
+                 : launch_prefill<DTYPE, 128>(a, n_rep, groups, bt_i64, s);
 }
 
 }  // namespace
 }  // namespace mv
 
 extern "C" int mv_prefill_tokens_per_group(int32_t num_q_heads, int32_t num_kv_heads,
-                                           int32_t head_dim) {
+                                           int32_t head_dim, int32_t dtype) {
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return 0;
-  if (head_dim != 64 && head_dim != 128) return 0;
-  const int rows = 16 * mv::pf_row_tiles(head_dim);
-  const int n_rep = num_q_heads / num_kv_heads;
-  if (n_rep > rows) return 0;
-  return mv::kPfWaves * (rows / n_rep);
+  if ((head_dim != 64 && head_dim != 128) || mv::dtype_bytes(dtype) == 0) return 0;
+  return mv::by_type<mv::TokensPerGroup>(head_dim, dtype, num_q_heads / num_kv_heads);
 }
 
 extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
@@ -376,7 +398,7 @@ extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t
     return fail(MV_ERR_UNSUPPORTED, "mv_paged_prefill: head_dim %d not supported (64, 128)", head_dim);
   if (!is_pow2(block_size))
     return fail(MV_ERR_UNSUPPORTED, "mv_paged_prefill: block_size %d is not a power of 2", block_size);
-  const int tpg = mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim);
+  const int tpg = mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim, dtype);
   if (tpg == 0)
     return fail(MV_ERR_UNSUPPORTED, "mv_paged_prefill: %d query heads over %d kv heads not supported",
                 num_q_heads, num_kv_heads);
@@ -415,14 +437,15 @@ extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t
   a.scale_log2 = scale * 1.4426950408889634f;
   a.num_kv_heads = num_kv_heads;
   a.n_rep = num_q_heads / num_kv_heads;
-  a.tpw = tpg / kPfWaves;
+  a.tpw = 0;  // set per instantiation at launch
   a.bs_log2 = ilog2_exact(block_size);
   a.num_blocks_u32 = static_cast<uint32_t>(std::min<int64_t>(num_blocks, int64_t(1) << 31));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool i64 = bt_is_i64 != 0;
+  const int n_rep = num_q_heads / num_kv_heads;
   switch (dtype) {
-    case MV_DTYPE_F32: return launch_prefill_d<MV_DTYPE_F32>(a, head_dim, num_work_groups, i64, s);
-    case MV_DTYPE_F16: return launch_prefill_d<MV_DTYPE_F16>(a, head_dim, num_work_groups, i64, s);
-    default: return launch_prefill_d<MV_DTYPE_BF16>(a, head_dim, num_work_groups, i64, s);
+    case MV_DTYPE_F32: return launch_prefill_d<MV_DTYPE_F32>(a, head_dim, n_rep, num_work_groups, i64, s);
+    case MV_DTYPE_F16: return launch_prefill_d<MV_DTYPE_F16>(a, head_dim, n_rep, num_work_groups, i64, s);
+    default: return launch_prefill_d<MV_DTYPE_BF16>(a, head_dim, n_rep, num_work_groups, i64, s);
   }
 }

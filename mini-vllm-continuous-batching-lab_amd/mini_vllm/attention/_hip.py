@@ -14,7 +14,7 @@ import threading
 
 import torch  # noqa: F401  (must be loaded before the kernel library)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MV_OK = 0
 MV_ERR_INVALID_ARGUMENT = -1
@@ -109,7 +109,7 @@ SIGNATURES = {
         _I32, _I64, _I32,          # block_size, num_blocks, dtype
         _P, _SZ, _P,               # workspace, workspace_bytes, stream
     ]),
-    "mv_prefill_tokens_per_group": (ctypes.c_int, [_I32, _I32, _I32]),
+    "mv_prefill_tokens_per_group": (ctypes.c_int, [_I32, _I32, _I32, _I32]),
     "mv_paged_prefill": (ctypes.c_int, [
         _P, _I64, _I64,            # query, strides
         _P, _I64, _I64,            # key, strides

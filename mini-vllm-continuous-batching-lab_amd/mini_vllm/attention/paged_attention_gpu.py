@@ -792,7 +792,7 @@ def _check_prefix_tables(bt_host: torch.Tensor, rows: Sequence[int], lens: Seque
 
 
 def _prefill_plan(block_table, rows, cached, qlens, block_size, num_blocks, num_q_heads,
-                  num_kv_heads, head_dim, device):
+                  num_kv_heads, head_dim, dtype, device):
     """Validated table and device work list of one step's prefill, built once:
     the layers of a step pass the same (unmodified) block table and lengths,
     so only the first call validates (one host copy of the table) and
@@ -803,11 +803,12 @@ def _prefill_plan(block_table, rows, cached, qlens, block_size, num_blocks, num_
     """
     lib = _hip.load()
     extra = (tuple(rows), tuple(cached), tuple(qlens), block_size, num_blocks, num_q_heads,
-             num_kv_heads, head_dim, device)
+             num_kv_heads, head_dim, dtype, device)
     hit = _cache_get("prefill", (block_table,), extra)
     if hit is not None:
         return hit
-    tpg = lib.mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim)
+    tpg = lib.mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim,
+                                          _hip.MV_DTYPE[dtype])
     if tpg == 0:
         raise RuntimeError(
             f"prefill: {num_q_heads} query heads over {num_kv_heads} kv heads not supported"
@@ -902,7 +903,7 @@ def hip_prefill_attention(
         return out
     bt, meta, work, n_work = _prefill_plan(block_table, rows, cached, qlens, block_size,
                                            num_blocks, num_q_heads, num_kv_heads, head_dim,
-                                           device)
+                                           query.dtype, device)
 
     q = _aligned_rows(query)
     k = _aligned_rows(key)

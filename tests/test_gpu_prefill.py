@@ -85,7 +85,7 @@ SHAPES = [  # (hq, hkv, d, bs, dtype)
     (28, 4, 128, 16, torch.bfloat16),
     (8, 8, 64, 32, torch.float16),     # n_rep 1
     (16, 1, 128, 16, torch.bfloat16),  # n_rep 16
-    (32, 1, 64, 64, torch.bfloat16),   # n_rep 32
+    (16, 1, 64, 64, torch.bfloat16),   # n_rep 16, block 64
 ]
 
 
@@ -114,6 +114,14 @@ def test_prefix_spanning_two_id_windows():
     c = _case(14, 2, 64, 1, torch.bfloat16, [3000, 10], [40, 20], seed=3, extra_blocks=64)
     err = (_run(c) - _ref(c)).abs().max().item()
     assert err <= TOL[torch.bfloat16], err
+
+
+def test_more_than_16_query_heads_per_kv_head_is_unsupported():
+    """As the decode path (and the backend's constructor): at most 16 query
+    heads per kv head -- one MFMA row tile per wave."""
+    c = _case(32, 1, 64, 16, torch.bfloat16, [10], [4], seed=6)
+    with pytest.raises(RuntimeError, match="not supported"):
+        _run(c)
 
 
 def test_insufficient_table_raises():
