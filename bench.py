@@ -113,6 +113,20 @@ def wall_loop(fn, n):
     return (time.perf_counter() - t0) * 1e6 / n
 
 
+def same_bytes_copy_us(nbytes, device, steps, stream):
+    """One plain device copy (torch's copy kernel) moving ``nbytes`` of HBM
+    traffic, half read and half written, rotated over >= 1 GiB of buffers
+    so the 256 MB MALL cannot serve it: what one launch of that much
+    traffic costs on this GPU at this size, launch and ramp included."""
+    elems = max(1, nbytes // 4)  # bf16 elements per side: nbytes / 2 bytes each way
+    n_buf = max(2, math.ceil(MIN_WORKING_SET / (4 * elems)))
+    src = [torch.empty(elems, dtype=torch.bfloat16, device=device).fill_(1) for _ in range(n_buf)]
+    dst = [torch.empty_like(x) for x in src]
+    for i in range(n_buf):
+        dst[i].copy_(src[i])
+    return time_loop(lambda i: dst[i % n_buf].copy_(src[i % n_buf]), steps, stream)
+
+
 def rope_tables(head_dim, theta, max_pos, dtype, device):
     """cos / sin tables of the model's rotary embedding (RotaryEmbedding,
     mini_vllm/model/rotary.py:16-35), built on the device."""
@@ -424,6 +438,8 @@ def main(argv=None) -> int:
 
     dec_bytes = decode_bytes(layout, spec.dtype)
     wr_bytes = write_bytes(layout, spec.dtype)
+    us_copy = same_bytes_copy_us(dec_bytes + wr_bytes, dev, args.steps, stream)
+    log(f"[bench] plain copy of the same HBM bytes: {us_copy:.2f} us")
     gbs = (dec_bytes + wr_bytes) / us_step / 1e3
     result = {
         "metric": METRIC,
@@ -486,6 +502,8 @@ def main(argv=None) -> int:
             "frac": round(gbs / PEAK_HBM_GBS, 4),
             "algorithmic_bytes": dec_bytes + wr_bytes,
             "decode_only_frac": round(dec_bytes / us_decode / 1e3 / PEAK_HBM_GBS, 4),
+            "same_bytes_copy_us": round(us_copy, 3),
+            "same_bytes_copy_frac": round((dec_bytes + wr_bytes) / us_copy / 1e3 / PEAK_HBM_GBS, 4),
             "traffic": measured_traffic(spec.name),
         },
         "cpu_baseline": None,
