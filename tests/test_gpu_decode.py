@@ -161,6 +161,44 @@ def test_reference_gpu_suite_ramp_inputs(lens, qh):
     assert torch.allclose(out.float().cpu(), ref, atol=1e-2, rtol=1e-2)
 
 
+def _split_ranges(lens, first, gap):
+    """Sequence i holds min(n, first) tokens from slot i*512 and the rest from
+    slot i*512 + gap, written in sequence order (a later sequence may
+    overwrite an earlier one's second range, as in the reference's own
+    setup); returns (kc, vc, table)."""
+    bs, hkv, d = 16, 2, 64
+    kc = torch.full((512, hkv, bs, d), float("nan"), dtype=torch.float16)
+    vc = kc.clone()
+    rows = []
+    for i, n in enumerate(lens):
+        k = _ramp((n, hkv, d), 10.0 + i * 100)
+        v = _ramp((n, hkv, d), 1010.0 + i * 100)
+        a = min(n, first)
+        row = []
+        for lo, hi, s0 in ((0, a, i * 512), (a, n, i * 512 + gap)):
+            if hi > lo:
+                paged_ref.write_to_paged_cache(k[lo:hi], v[lo:hi], kc, vc,
+                                               torch.arange(s0, s0 + hi - lo), bs)
+                row += list(range(s0 // bs, s0 // bs + -(-(hi - lo) // bs)))
+        rows.append(row)
+    mb = max(len(r) for r in rows)
+    return kc, vc, torch.tensor([r + [-1] * (mb - len(r)) for r in rows])
+
+
+@pytest.mark.parametrize("lens,gap", [([32] * 4, 256), ([7, 19, 33, 48], 512)])
+def test_reference_gpu_suite_split_ranges(lens, gap):
+    """Each sequence's blocks in two separate ranges of the pool
+    (test_paged_attention_gpu.py:562-646: batch 4 non-contiguous, batch 4
+    ragged non-contiguous); fp16 ramp inputs, atol = rtol = 1e-2 as there."""
+    say("decode split ranges", lens, gap)
+    kc, vc, bt = _split_ranges(lens, 16, gap)
+    kv = torch.tensor(lens, dtype=torch.int32)
+    q = _ramp((len(lens), 4, 64), 50.0)
+    ref = paged_ref.decode_from_tables(q.float(), kc.float(), vc.float(), bt, kv, 16)
+    out = triton_decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), kv.to(DEV), 16)
+    assert torch.allclose(out.float().cpu(), ref, atol=1e-2, rtol=1e-2)
+
+
 def test_noncontiguous_table_10_50():
     """Table [[10, 50]] with 19 tokens (test_paged_attention_gpu.py:357-381)."""
     say("decode [[10,50]]")
@@ -176,6 +214,23 @@ def test_noncontiguous_table_10_50():
     ref = paged_ref.decode_from_tables(q.float(), kc.float(), vc.float(), bt, kv, 16)
     out = hip_decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), kv.to(DEV), 16)
     assert torch.allclose(out.float().cpu(), ref, atol=1e-2, rtol=1e-2)
+
+
+def test_split_merges_in_a_row_are_deterministic():
+    """Sequences split into many partitions, several calls in a row with
+    different layouts (batch, partitions per sequence): each matches the
+    oracle and is bit-identical when repeated (the partials are merged in
+    partition order, whichever work group merges)."""
+    for seed, lens, dtype in ((31, [4000, 40, 9000, 700], torch.bfloat16),
+                              (32, [20000, 3], torch.float32),
+                              (33, [900] * 24 + [5000], torch.float16)):
+        say("decode split merges", seed, lens, dtype)
+        c = _random_case(14, 2, 64, 16, lens, dtype, seed)
+        ref, _, _ = oracle_step(c)
+        out, _ = _step_on_gpu(c)
+        _check(out, ref, dtype, f"split merges seed {seed}")
+        again, _ = _step_on_gpu(c)  # whichever work group merges, the same bits
+        assert torch.equal(bits(out), bits(again))
 
 
 def test_invalid_metadata_raises():
