@@ -21,7 +21,8 @@
 //   Q rows are then copied to LDS alongside the first tiles.
 //
 // Per tile (16 tokens x D) and wave, with lane = 16*g + t (g = 0..3):
-//   * HBM -> LDS without registers: global_load_lds_dwordx4 writes lane l's
+//   * HBM -> LDS without registers: global_load_lds_dwordx4 (non-temporal:
+//     each K/V byte is read once) writes lane l's
 //     16 bytes to LDS slot (64c + l) of load instruction c. Each lane
 //     fetches the 16-byte piece that belongs in its slot under an XOR
 //     swizzle (slot s of row r holds piece s ^ sw(r)), so every load
@@ -305,8 +306,8 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     const uint32_t kdst = wave_tiles_lds + ST * Tr::kStageBytes;
 #pragma unroll
     for (int c = 0; c < L; ++c) {
-      copy_to_lds_16B(a.k_cache + off[c], __builtin_amdgcn_readfirstlane(kdst + c * 1024));
-      copy_to_lds_16B(a.v_cache + off[c],
+      copy_to_lds_16B_stream(a.k_cache + off[c], __builtin_amdgcn_readfirstlane(kdst + c * 1024));
+      copy_to_lds_16B_stream(a.v_cache + off[c],
                       __builtin_amdgcn_readfirstlane(kdst + Tr::kTileBytes + c * 1024));
     }
     return valid;
