@@ -69,11 +69,13 @@ namespace {
 #define MV_DECODE_WAVES 4
 #endif
 #ifndef MV_DECODE_STAGES
-#define MV_DECODE_STAGES 3
+#define MV_DECODE_STAGES 2
 #endif
 constexpr int kWaves = MV_DECODE_WAVES;
 constexpr int kMaxParts = 128;  // partitions per sequence the plan aims for
 constexpr int kIdCap = 512;     // block ids one partition may span (staged in LDS)
+constexpr int kFewUnitsPerCU = 2;   // plan target when the (sequence, kv head) units fit the CUs
+constexpr int kManyUnitsPerCU = 3;  // plan target cap otherwise
 
 template <int DTYPE, int D>
 struct Traits : TileGeom<DTYPE, D> {
@@ -88,7 +90,9 @@ struct Traits : TileGeom<DTYPE, D> {
   using G::kElemsPerPiece;
   static constexpr int kChunk = kWaves * kTile;         // tokens per work-group iteration
   // Tile buffers per wave: up to S-1 tiles stream in while one is computed.
-  // Larger tiles get 2 stages so two work groups still fit one CU.
+  // Larger tiles get at most 2 stages so two work groups still fit one CU.
+  // With the non-temporal tile copies, 2 stages beat 3 at every size
+  // measured (c2-sized batches 1 %, 8k-32k contexts 6 %); 4 lose 5 %.
   static constexpr int kStages = kTileBytes <= 2048 ? MV_DECODE_STAGES
                                                     : (MV_DECODE_STAGES < 2 ? MV_DECODE_STAGES : 2);
   static constexpr int kStageBytes = 2 * kTileBytes;    // K tile, V tile
@@ -835,12 +839,13 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const int64_t units = live_seqs * hkv;  // (sequence, kv head) pairs
 
   // ---- 2. piece bound L (tiles)
-  // Resident slots to fill: all a CU holds, or 2 per CU when there is at
-  // most one (sequence, kv head) unit per CU -- fewer, longer pieces per CU
-  // stream at a steadier rate per CU than three (measured on c2/c3-like
-  // batches), and the split-K merge has fewer partials.
-  const int per_cu = units <= a.cu_count ? vmin(2, vmax(1, a.groups_per_cu))
-                                         : vmax(1, a.groups_per_cu);
+  // Resident slots to fill: 2 per CU when there is at most one (sequence,
+  // kv head) unit per CU -- fewer, longer pieces per CU stream at a
+  // steadier rate per CU than three or four (measured on c2/c3-like
+  // batches), and the split-K merge has fewer partials -- otherwise up to
+  // kManyUnitsPerCU (3 beat the 4 that LDS allows at D=64 on the c4 batch).
+  const int per_cu = units <= a.cu_count ? vmin(kFewUnitsPerCU, vmax(1, a.groups_per_cu))
+                                         : vmin(kManyUnitsPerCU, vmax(1, a.groups_per_cu));
   const int64_t target = static_cast<int64_t>(per_cu) * vmax(1, a.cu_count);
   // hard: a piece spans at most kIdCap table entries (they are staged in LDS)
   const int l_cap = static_cast<int>(vmax<int64_t>(
@@ -1181,10 +1186,13 @@ extern "C" int mv_decode_graph_bounds(int32_t num_seqs, int32_t max_blocks, int3
   const int64_t max_parts =
       std::max<int64_t>(1, std::min<int64_t>(kMaxParts, (max_tiles + kWaves - 1) / kWaves));
   const int64_t units = static_cast<int64_t>(num_kv_heads) * num_seqs;
-  // the plan's resident target: 2 per CU when its (live) units fit the CUs
+  // at least the plan's resident target (kFewUnitsPerCU per CU when its
+  // live units fit the CUs, else up to kManyUnitsPerCU)
   const int gpc = std::max(1, groups_per_cu);
   const int64_t target =
-      static_cast<int64_t>(units <= cu_count ? std::min(2, gpc) : std::max(2, gpc)) * cu_count;
+      static_cast<int64_t>(units <= cu_count ? std::min(kFewUnitsPerCU, gpc)
+                                             : std::max(kFewUnitsPerCU, std::min(kManyUnitsPerCU, gpc))) *
+      cu_count;
   const int64_t by_fair = units + std::max<int64_t>(target, (units * max_tiles + l_cap - 1) / l_cap);
   const int64_t groups = std::min<int64_t>(by_fair, units * max_parts);
   if (groups > INT_MAX / 8)

@@ -63,7 +63,7 @@ def test_abi_queries(lib):
     assert lib.mv_decode_chunk_tokens(64, 2) == 64       # 4 waves x one 16-token tile
     assert lib.mv_decode_chunk_tokens(128, 0) == 64
     assert lib.mv_decode_chunk_tokens(96, 2) == 0
-    assert lib.mv_decode_groups_per_cu(64, 2) == 3       # 3 stages x 4 waves x 4 KiB + 2 KiB ids
+    assert lib.mv_decode_groups_per_cu(64, 2) == 4       # 2 stages x 4 waves x 4 KiB + 2 KiB ids + 2 KiB Q
     assert lib.mv_decode_groups_per_cu(128, 2) == 2
     assert lib.mv_decode_groups_per_cu(96, 2) == 0
 

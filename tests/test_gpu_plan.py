@@ -109,18 +109,21 @@ def test_many_units_are_not_dealt():
 
 
 def test_skewed_batch_uses_fair_pieces():
-    """382 one-tile sequences and one of 16000 tokens (766 units of 768 slots
-    at 3 per CU): fitting one dispatch round would leave the long sequence
-    two pieces of 500 tiles, far over twice the fair share, so the plan cuts
-    fair pieces and runs more groups than resident slots."""
+    """One-tile sequences filling all but 2 of the slots LDS allows (2 kv
+    heads each; the plan's resident target is at most that) and one sequence
+    of 16000 tokens: fitting one dispatch round would leave the long
+    sequence at most one piece of 1000 tiles per kv head, far over twice the
+    fair share, so the plan cuts fair pieces and runs more groups than
+    resident slots."""
     from mini_vllm.attention import _hip
 
-    lens = [16] * 382 + [16000]
-    spec = WorkloadSpec("skew", 14, 2, 64, 16, torch.bfloat16, len(lens), ("fixed", lens))
-    say("plan: skewed batch")
-    plan, err = _run_and_check(spec)
     per_cu = _hip.load().mv_decode_groups_per_cu(64, _hip.MV_DTYPE[torch.bfloat16])
-    assert plan.num_groups > per_cu * _cus()
+    slots = per_cu * _cus()
+    lens = [16] * (slots // 2 - 1) + [16000]
+    spec = WorkloadSpec("skew", 14, 2, 64, 16, torch.bfloat16, len(lens), ("fixed", lens))
+    say("plan: skewed batch", len(lens), "sequences,", slots, "slots")
+    plan, err = _run_and_check(spec)
+    assert plan.num_groups > slots
     say(f"  groups {plan.num_groups} P {plan.partition_tokens} max abs err {err:.3g}")
 
 
