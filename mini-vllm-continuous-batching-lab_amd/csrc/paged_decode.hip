@@ -74,6 +74,7 @@ namespace {
 constexpr int kWaves = MV_DECODE_WAVES;
 constexpr int kMaxParts = 128;  // partitions per sequence the plan aims for
 constexpr int kIdCap = 512;     // block ids one partition may span (staged in LDS)
+constexpr int kIdsFirst = 64;   // ids copied before the work item is known, for long id lists
 constexpr int kFewUnitsPerCU = 2;   // plan target when the (sequence, kv head) units fit the CUs
 constexpr int kManyUnitsPerCU = 3;  // plan target cap otherwise
 
@@ -203,15 +204,19 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
 
   // ---- the work item and its block ids: both addressed by blockIdx alone,
-  // so they travel together (one memory round trip). Waves 0 and 1 copy
-  // 256 ids each; lanes past the list re-read its last 16 bytes. The copy
-  // is issued first: the work item's scalar load must not sit in front of
-  // it (a wait for it would also cover the kernel arguments the copy needs).
-  if (wave * 256 < a.ids_per_item) {
-    const int32_t* src = a.block_ids + static_cast<int64_t>(item) * a.ids_per_item +
-                         min(wave * 256 + 4 * lane, a.ids_per_item - 4);
-    copy_to_lds_16B(reinterpret_cast<const char*>(src),
-                    __builtin_amdgcn_readfirstlane(lds0 + Tr::kIdsOffset + wave * 1024));
+  // so they travel together (one memory round trip). Wave 0 copies the
+  // first window of the list: all of it when the list is at most 256 ids
+  // (a plan sized for this step's pieces), else kIdsFirst ids (a launch of
+  // fixed size, whose lists have the widest piece's stride: most pieces
+  // need far fewer, and unused slots none). Lanes past the window re-read
+  // its last 16 bytes. The copy is issued first: the work item's scalar
+  // load must not sit in front of it (a wait for it would also cover the
+  // kernel arguments the copy needs).
+  const int first_ids = a.ids_per_item <= 256 ? a.ids_per_item : kIdsFirst;
+  const int64_t ids_base = static_cast<int64_t>(item) * a.ids_per_item;
+  if (wave == 0) {
+    const int32_t* src = a.block_ids + ids_base + min(4 * lane, first_ids - 4);
+    copy_to_lds_16B(reinterpret_cast<const char*>(src), __builtin_amdgcn_readfirstlane(lds0 + Tr::kIdsOffset));
   }
   asm volatile("" ::: "memory");
   const int4 w0 = reinterpret_cast<const int4*>(a.work + 8 * static_cast<int64_t>(item))[0];
@@ -228,6 +233,25 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const int n_chunks = (tok_end - tok_begin + Tr::kChunk - 1) / Tr::kChunk;
   const int bs_mask = (1 << a.bs_log2) - 1;
   const int first_blk = tok_begin >> a.bs_log2;  // s_ids[i] = pool block of table entry first_blk + i
+  {
+    // All the ids when the piece spans more table entries than the first
+    // window held (a second round trip, for long pieces only): wave w
+    // copies ids [256 w, 256 w + 256) of [0, need) to their LDS slots (the
+    // first window again, with the same values); lanes past `need` re-read
+    // its last 16 bytes, so no copy leaves the item's list or the LDS id
+    // buffer (kWaves * 256 >= kIdCap).
+    static_assert(kWaves * 256 >= kIdCap, "the id copy covers the id buffer");
+    const int need = min((((tok_end - 1) >> a.bs_log2) - first_blk + 1 + 3) & ~3, a.ids_per_item);
+    if (need > first_ids) {
+      if (wave * 256 < need) {
+        const int32_t* src = a.block_ids + ids_base + min(wave * 256 + 4 * lane, need - 4);
+        copy_to_lds_16B(reinterpret_cast<const char*>(src),
+                        __builtin_amdgcn_readfirstlane(lds0 + Tr::kIdsOffset + wave * 1024));
+      }
+      wait_vmcnt<0>();
+      asm volatile("" ::: "memory");
+    }
+  }
   const char* wave_tiles = s_lds + wave * Tr::kWaveLds;  // [stage][K, V][tile bytes]
   const uint32_t wave_tiles_lds = lds0 + wave * Tr::kWaveLds;
 

@@ -233,6 +233,23 @@ def test_split_merges_in_a_row_are_deterministic():
         assert torch.equal(bits(out), bits(again))
 
 
+def test_block_size_one_long_id_lists():
+    """Block size 1 with many long sequences: pieces of up to 496 tokens
+    span up to 497 table entries, more than the 256 the first id copy
+    holds, so each work group fetches the rest of its list once the work
+    item is known."""
+    from mini_vllm.attention.paged_attention_gpu import plan_decode
+
+    say("decode block size 1, long id lists")
+    c = _random_case(14, 2, 64, 1, [900 + (7 * i) % 200 for i in range(300)], torch.bfloat16, 41)
+    ref, _, _ = oracle_step(c)
+    out, d = _step_on_gpu(c)
+    plan = plan_decode(d.block_table, d.kv_len, 1, d.key_cache.shape[0], d.key_cache.device, 64,
+                       torch.bfloat16, 2)
+    assert plan.partition_tokens + 1 > 256, plan.partition_tokens  # the second copy ran
+    _check(out, ref, torch.bfloat16, "block size 1")
+
+
 def test_invalid_metadata_raises():
     say("decode invalid metadata")
     q = torch.randn(1, 4, 64).half().to(DEV)

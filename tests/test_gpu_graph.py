@@ -11,6 +11,7 @@ checks captured with the step report bad metadata through check_deferred().
 import pytest
 import torch
 
+from benchmarks.paged_decode_workloads import WorkloadSpec, make_case
 from gpu_util import DEV, TOL, bits, say
 from mini_vllm.attention import paged_attention_gpu as pg
 from oracle import paged_ref
@@ -160,3 +161,46 @@ def test_eager_calls_after_capture_still_validate():
     st.kv[0] = 0  # in-place edit: the next call plans (and checks) again
     with pytest.raises(ValueError, match="kv_len"):
         st.step()
+
+
+def test_captured_long_pieces_fetch_the_rest_of_their_ids():
+    """A launch of fixed size stores each work group's block ids at the
+    widest piece's stride, and the kernel copies only the first 64 before
+    it knows its piece. Here 520 (sequence, kv head) units of 1100-1300
+    tokens make pieces of about 80 table entries: every work group fetches
+    the rest of its list once its work item is known. Replayed twice, the
+    second time with shorter kv_len in place."""
+    lens = [1100 + (37 * i) % 200 for i in range(260)]
+    spec = WorkloadSpec("long-pieces", 14, 2, 64, 16, DT, len(lens), ("fixed", lens))
+    case = make_case(spec, seed=5, nan_fill=True)
+    q, kc, vc = case.query.to(DEV), case.key_cache.to(DEV), case.value_cache.to(DEV)
+    bt, kv = case.block_table.to(DEV), case.kv_len.to(DEV)
+    # the step's new tokens (their slots are NaN until written)
+    pg.hip_cache_write(case.new_key.to(DEV), case.new_value.to(DEV), kc, vc,
+                       case.slot_mapping.to(DEV), 16)
+    kc_ref, vc_ref = case.key_cache.float(), case.value_cache.float()
+    paged_ref.write_to_paged_cache(case.new_key.float(), case.new_value.float(), kc_ref, vc_ref,
+                                   case.slot_mapping, 16)
+    pg.clear_deferred()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # eager warm-up
+        pg.hip_decode_attention(q, kc, vc, bt, kv, 16)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = pg.hip_decode_attention(q, kc, vc, bt, kv, 16)
+    shorter = case.kv_len - torch.arange(len(lens)) % 300
+    for tag, lengths in (("full", case.kv_len), ("shorter", shorter)):
+        say("graph: long pieces", tag)
+        kv.copy_(lengths)
+        graph.replay()
+        torch.cuda.synchronize()
+        pg.check_deferred()
+        ref = paged_ref.decode_from_tables(case.query.float(), kc_ref, vc_ref, case.block_table,
+                                           lengths, 16)
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert err <= TOL[DT], (tag, err)
+    del graph
+    pg.clear_deferred()
