@@ -38,15 +38,27 @@ namespace {
 
 constexpr int kPfIdCap = 2048;  // prefix block ids staged in LDS per window
 // Waves per work group: 8 (twice the query rows per pass over the keys,
-// and more waves to hide latency -- 52 us against 60 us with 4 on a
+// and more waves to hide latency -- 51 us against 60 us with 4 on a
 // 4 x (1536 + 512) bf16 step) when two stages of 8 sub-tiles fit the LDS,
 // else 4 (fp32 at head_dim 128). Two stages: a third measured no faster.
+// One 16-row MFMA tile per wave: two (half the LDS reads per key) measured
+// 76 us with 8 waves and 78 us with 4, three 103 us -- each wave's chain
+// of QK^T, softmax and PV per stage is what bounds the kernel, and more
+// rows per wave lengthen it.
+#ifndef MV_PREFILL_WAVES
+#define MV_PREFILL_WAVES 8
+#endif
+#ifndef MV_PREFILL_ROWS
+#define MV_PREFILL_ROWS 1
+#endif
 template <int DTYPE, int D>
 struct PfTraits : TileGeom<DTYPE, D> {
   using G = TileGeom<DTYPE, D>;
   static constexpr int kSubBytes = 2 * G::kTileBytes;  // K and V sub-tile of one wave
   static constexpr int kStages = 2;
-  static constexpr int kWaves = kStages * 8 * kSubBytes + kPfIdCap * 4 <= 160 * 1024 ? 8 : 4;
+  static constexpr int kRows = MV_PREFILL_ROWS;  // 16-row MFMA tiles per wave
+  static constexpr int kWaves =
+      kStages * MV_PREFILL_WAVES * kSubBytes + kPfIdCap * 4 <= 160 * 1024 ? MV_PREFILL_WAVES : 4;
   static constexpr int kStageTokens = kWaves * kTile;  // keys per stage: one sub-tile per wave
   static constexpr int kStageBytes = kWaves * kSubBytes;
   static constexpr int kIdsOffset = kStages * kStageBytes;
@@ -58,7 +70,7 @@ struct PfTraits : TileGeom<DTYPE, D> {
 // floor(16 / n_rep) tokens' GQA groups.
 template <int DTYPE, int D>
 constexpr int pf_tokens_per_group(int n_rep) {
-  return n_rep > 16 ? 0 : PfTraits<DTYPE, D>::kWaves * (16 / n_rep);
+  return n_rep > 16 ? 0 : PfTraits<DTYPE, D>::kWaves * (16 * PfTraits<DTYPE, D>::kRows / n_rep);
 }
 
 struct PrefillArgs {
@@ -89,7 +101,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   constexpr int RP = Tr::kRowPieces;
   constexpr int QP = Tr::kLanePieces;
   constexpr int S = Tr::kStages;
-  constexpr int R = 1;  // 16-row MFMA tiles per wave (two measured slower: fewer work groups)
+  constexpr int R = Tr::kRows;
   constexpr int kPfWaves = Tr::kWaves;
   constexpr int kPfStageTokens = Tr::kStageTokens;
 
