@@ -508,6 +508,10 @@ def main(argv=None) -> int:
         },
         "cpu_baseline": None,
     }
+    if layout.shared_blocks:  # shared prefixes: the roofline on the bytes that must move
+        uniq = decode_bytes(layout, spec.dtype, unique=True) + wr_bytes
+        result["roofline"]["unique_bytes"] = uniq
+        result["roofline"]["frac_unique"] = round(uniq / us_step / 1e3 / PEAK_HBM_GBS, 4)
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(spec, layout, layers[0])
