@@ -76,6 +76,58 @@ __device__ __forceinline__ s16x4 v_column_tr(const char* v_tile, int g, int t, i
       (__attribute__((address_space(3))) s16x4*)(const_cast<char*>(src)));
 }
 
+// P values of one lane (4 per 16-token tile, fp32) rounded to the 16-bit
+// MFMA input type in two packed conversions, returned as the PV MFMA's A
+// operand; `sum` accumulates the rounded values (two dot2 with (1, 1)), so
+// O / l stays an exact convex combination of V rows.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <int DTYPE>
+__device__ __forceinline__ s16x4 pack_p(float p0, float p1, float p2, float p3, float& sum) {
+  static_assert(DTYPE != MV_DTYPE_F32, "16-bit types only");
+  uint32_t lo, hi;
+  if constexpr (DTYPE == MV_DTYPE_BF16) {
+    const bf16x2_t a = __builtin_convertvector((f32x2_t){p0, p1}, bf16x2_t);
+    const bf16x2_t b = __builtin_convertvector((f32x2_t){p2, p3}, bf16x2_t);
+    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    sum = __builtin_amdgcn_fdot2_f32_bf16(a, ones, sum, false);
+    sum = __builtin_amdgcn_fdot2_f32_bf16(b, ones, sum, false);
+    lo = __builtin_bit_cast(uint32_t, a);
+    hi = __builtin_bit_cast(uint32_t, b);
+  } else {
+    const f16x2_t a = __builtin_convertvector((f32x2_t){p0, p1}, f16x2_t);
+    const f16x2_t b = __builtin_convertvector((f32x2_t){p2, p3}, f16x2_t);
+    const f16x2_t ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    sum = __builtin_amdgcn_fdot2(a, ones, sum, false);
+    sum = __builtin_amdgcn_fdot2(b, ones, sum, false);
+    lo = __builtin_bit_cast(uint32_t, a);
+    hi = __builtin_bit_cast(uint32_t, b);
+  }
+  return __builtin_bit_cast(s16x4, make_uint2(lo, hi));
+}
+
+// O tile update for one 16-token tile, 16-bit types, P already packed
+// (pack_p): o[r][c] += P_r V for R row tiles that share the tile.
+template <int DTYPE, int D, int R>
+__device__ __forceinline__ void mfma_pv_packed(const s16x4 (&pa)[R], const char* v_tile, int g, int t,
+                                               f32x4 (&o)[R][D / 16]) {
+  constexpr int RP = TileGeom<DTYPE, D>::kRowPieces;
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
+    const s16x4 vb = v_column_tr<RP>(v_tile, g, t, c);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if constexpr (DTYPE == MV_DTYPE_BF16) {
+        o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[r], vb, o[r][c], 0, 0, 0);
+      } else {
+        o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa[r]),
+                                                       __builtin_bit_cast(f16x4, vb), o[r][c], 0, 0, 0);
+      }
+    }
+  }
+}
+
 // O tile update for one 16-token tile from its swizzled LDS tile, for R
 // row tiles that share the tile: o[r][c] += P_r(16 rows x 16 tokens)
 // V(16 tokens x 16 dims), V element (row 4g+e, column 16c+t) per lane.
@@ -110,20 +162,7 @@ __device__ __forceinline__ void mfma_pv_rows(const float (&p)[R][4], const char*
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int e = 0; e < 4; ++e) pa[r][e] = static_cast<short>(from_f32<DTYPE>(p[r][e]));
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      const s16x4 vb = v_column_tr<RP>(v_tile, g, t, c);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if constexpr (DTYPE == MV_DTYPE_BF16) {
-          o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[r], vb, o[r][c], 0, 0, 0);
-        } else {
-          o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa[r]),
-                                                         __builtin_bit_cast(f16x4, vb), o[r][c], 0,
-                                                         0, 0);
-        }
-      }
-    }
+    mfma_pv_packed<DTYPE, D, R>(pa, v_tile, g, t, o);
   }
 }
 

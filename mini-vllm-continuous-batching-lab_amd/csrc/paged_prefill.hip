@@ -223,15 +223,23 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         *reinterpret_cast<uint4*>(vdst + c * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
   };
 
-  // One stage (4 sub-tiles of 16 keys) for this wave's rows: S^T for every
-  // sub-tile some row may see, one online-softmax update per row tile over
-  // the whole stage (one max / sum exchange and one rescale of O), then
-  // O += P V per sub-tile.
+  // The smallest causal limit among the wave's rows: a stage that ends at
+  // or before it is seen whole by every row (no mask).
+  const int wave_first_limit = cached + tok0 + wtok0;
+
+  // One stage (kPfWaves sub-tiles of 16 keys) for this wave's rows: S^T for
+  // every sub-tile some row may see, one online-softmax update per row tile
+  // over the whole stage (one max / sum exchange and one rescale of O),
+  // then O += P V per sub-tile. The 16-bit types mask only the stages that
+  // cross the causal diagonal, fold the scale into the exponent's FMA
+  // (exp2(s * scale - m); the max is taken on unscaled scores, as scale > 0)
+  // and round P once, packed, for both the PV MFMA and the row sum.
   auto compute_stage = [&](int k, int st) __attribute__((always_inline)) {
     const int k_first = k * kPfStageTokens;
     if (k_first > wave_limit) return;  // causal: no row of the wave sees this stage
     // sub-tiles u < nu hold keys some row of the wave sees
     const int nu = min(kPfWaves, (wave_limit - k_first) / kTile + 1);
+    const bool whole = k_first + kPfStageTokens - 1 <= wave_first_limit;  // then nu == kPfWaves
     const char* stage = s_lds + st * Tr::kStageBytes;
     const int ksw = piece_swizzle<RP>(t);
     f32x4 acc[kPfWaves][R];
@@ -249,46 +257,99 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         }
       }
     }
-    float pr[kPfWaves][R][4];
+    if constexpr (DTYPE == MV_DTYPE_F32) {
+      float pr[kPfWaves][R][4];
 #pragma unroll
-    for (int rt = 0; rt < R; ++rt) {
-      float mc = kNegInf;
+      for (int rt = 0; rt < R; ++rt) {
+        float mc = kNegInf;
 #pragma unroll
-      for (int u = 0; u < kPfWaves; ++u)
+        for (int u = 0; u < kPfWaves; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = k_first + u * kTile + 4 * g + e;
+            const float sv = u < nu && key <= limit[rt] ? acc[u][rt][e] * a.scale_log2 : kNegInf;
+            acc[u][rt][e] = sv;
+            mc = fmaxf(mc, sv);
+          }
+        mc = fmaxf(mc, __shfl_xor(mc, 16));
+        mc = fmaxf(mc, __shfl_xor(mc, 32));
+        const float m_new = fmaxf(m_run[rt], mc);
+        const float m_ref = m_new == kNegInf ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
+        float lc = 0.f;
+#pragma unroll
+        for (int u = 0; u < kPfWaves; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pr[u][rt][e] = __builtin_amdgcn_exp2f(acc[u][rt][e] - m_ref);
+            lc += pr[u][rt][e];
+          }
+        lc += __shfl_xor(lc, 16);
+        lc += __shfl_xor(lc, 32);
+        l_run[rt] = l_run[rt] * alpha + lc;
+        m_run[rt] = m_new;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int key = k_first + u * kTile + 4 * g + e;
-          const float sv = u < nu && key <= limit[rt] ? acc[u][rt][e] * a.scale_log2 : kNegInf;
-          acc[u][rt][e] = sv;
-          mc = fmaxf(mc, sv);
+          const float ar = __shfl(alpha, 4 * g + e);
+#pragma unroll
+          for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
         }
-      mc = fmaxf(mc, __shfl_xor(mc, 16));
-      mc = fmaxf(mc, __shfl_xor(mc, 32));
-      const float m_new = fmaxf(m_run[rt], mc);
-      const float m_ref = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
-      float lc = 0.f;
-#pragma unroll
-      for (int u = 0; u < kPfWaves; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pr[u][rt][e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(acc[u][rt][e] - m_ref)));
-          lc += pr[u][rt][e];
-        }
-      lc += __shfl_xor(lc, 16);
-      lc += __shfl_xor(lc, 32);
-      l_run[rt] = l_run[rt] * alpha + lc;
-      m_run[rt] = m_new;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float ar = __shfl(alpha, 4 * g + e);
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
       }
-    }
 #pragma unroll
-    for (int u = 0; u < kPfWaves; ++u)
-      if (u < nu) mfma_pv_rows<DTYPE, D, R>(pr[u], stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, o);
+      for (int u = 0; u < kPfWaves; ++u)
+        if (u < nu) mfma_pv_rows<DTYPE, D, R>(pr[u], stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, o);
+    } else {
+      // Two instantiations, chosen once per stage (a uniform branch): the
+      // compiler would otherwise compute the mask and select per element.
+      auto softmax_pv = [&](auto whole_c) __attribute__((always_inline)) {
+        constexpr bool kWhole = decltype(whole_c)::value;
+        s16x4 pk[kPfWaves][R];
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt) {
+          float mc = kNegInf;
+#pragma unroll
+          for (int u = 0; u < kPfWaves; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if constexpr (!kWhole) {
+                const int key = k_first + u * kTile + 4 * g + e;
+                acc[u][rt][e] = u < nu && key <= limit[rt] ? acc[u][rt][e] : kNegInf;
+              }
+              mc = fmaxf(mc, acc[u][rt][e]);
+            }
+          mc = fmaxf(mc, __shfl_xor(mc, 16));
+          mc = fmaxf(mc, __shfl_xor(mc, 32));
+          const float m_new = fmaxf(m_run[rt], mc * a.scale_log2);
+          const float m_ref = m_new == kNegInf ? 0.f : m_new;
+          const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
+          float lc = 0.f;
+#pragma unroll
+          for (int u = 0; u < kPfWaves; ++u) {
+            float pe[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              pe[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u][rt][e], a.scale_log2, -m_ref));
+            pk[u][rt] = pack_p<DTYPE>(pe[0], pe[1], pe[2], pe[3], lc);
+          }
+          lc += __shfl_xor(lc, 16);
+          lc += __shfl_xor(lc, 32);
+          l_run[rt] = l_run[rt] * alpha + lc;
+          m_run[rt] = m_new;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float ar = __shfl(alpha, 4 * g + e);
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kPfWaves; ++u)
+          if (kWhole || u < nu)
+            mfma_pv_packed<DTYPE, D, R>(pk[u], stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, o);
+      };
+      if (whole) softmax_pv(IntC<1>{});
+      else softmax_pv(IntC<0>{});
+    }
   };
 
   // ---- windows of kPfIdCap prefix blocks (one window below 2048 blocks)
