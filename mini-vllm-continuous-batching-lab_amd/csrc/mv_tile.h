@@ -76,6 +76,27 @@ __device__ __forceinline__ s16x4 v_column_tr(const char* v_tile, int g, int t, i
       (__attribute__((address_space(3))) s16x4*)(const_cast<char*>(src)));
 }
 
+// Max / sum over the four 16-lane rows of the wave (lanes t, t+16, t+32,
+// t+48: one MFMA result column), every lane receiving the result, in two
+// gfx950 permlane swaps (VALU) instead of two LDS permutes. permlane32_swap
+// of (x, x) yields (rows 0 1 0 1, rows 2 3 2 3), permlane16_swap yields
+// (rows 0 0 2 2, rows 1 1 3 3); combining each pair reduces over row bits
+// 1, then 0. Used by the decode tile loop (c2 layer call 1 % faster);
+// the prefill, bound by VALU issue, keeps the LDS permutes (3 % faster
+// there).
+__device__ __forceinline__ float rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // P values of one lane (4 per 16-token tile, fp32) rounded to the 16-bit
 // MFMA input type in two packed conversions, returned as the PV MFMA's A
 // operand; `sum` accumulates the rounded values (two dot2 with (1, 1)), so

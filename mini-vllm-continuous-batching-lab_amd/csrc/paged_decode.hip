@@ -368,9 +368,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       s[e] = tile_tok + 4 * g + e < tok_end ? acc[e] * a.scale_log2 : kNegInf;
       mc = fmaxf(mc, s[e]);
     }
-    // head t's max over the tile: lanes t, t+16, t+32, t+48
-    mc = fmaxf(mc, __shfl_xor(mc, 16));
-    mc = fmaxf(mc, __shfl_xor(mc, 32));
+    mc = rows_max(mc);  // head t's max over the tile: lanes t, t+16, t+32, t+48
     const float m_new = fmaxf(m_run, mc);
     const float m_ref = m_new == kNegInf ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
@@ -383,8 +381,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       p[e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e] - m_ref)));
       lc += p[e];
     }
-    lc += __shfl_xor(lc, 16);
-    lc += __shfl_xor(lc, 32);
+    lc = rows_sum(lc);
     l_run = l_run * alpha + lc;
     m_run = m_new;
     // rescale O rows (head 4g+e takes the alpha of lane 4g+e)
