@@ -134,16 +134,21 @@ template <int DTYPE, int D, int R>
 __device__ __forceinline__ void mfma_pv_packed(const s16x4 (&pa)[R], const char* v_tile, int g, int t,
                                                f32x4 (&o)[R][D / 16]) {
   constexpr int RP = TileGeom<DTYPE, D>::kRowPieces;
+  // All of the tile's V operands are read before the first MFMA, so the
+  // reads overlap each other instead of each MFMA waiting for its own.
+  s16x4 vb[D / 16];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) vb[c] = v_column_tr<RP>(v_tile, g, t, c);
+  __builtin_amdgcn_sched_barrier(0);  // keep the reads together (the scheduler sinks them)
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
-    const s16x4 vb = v_column_tr<RP>(v_tile, g, t, c);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if constexpr (DTYPE == MV_DTYPE_BF16) {
-        o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[r], vb, o[r][c], 0, 0, 0);
+        o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[r], vb[c], o[r][c], 0, 0, 0);
       } else {
         o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa[r]),
-                                                       __builtin_bit_cast(f16x4, vb), o[r][c], 0, 0, 0);
+                                                       __builtin_bit_cast(f16x4, vb[c]), o[r][c], 0, 0, 0);
       }
     }
   }
