@@ -128,18 +128,46 @@ __device__ __forceinline__ s16x4 pack_p(float p0, float p1, float p2, float p3, 
   return __builtin_bit_cast(s16x4, make_uint2(lo, hi));
 }
 
+// The transposed V operands of one 16-token tile (16-bit types), one per
+// 16-dim column block, for mfma_pv_operands.
+template <int DTYPE, int D>
+__device__ __forceinline__ void read_v_operands(const char* v_tile, int g, int t, s16x4 (&vb)[D / 16]) {
+  constexpr int RP = TileGeom<DTYPE, D>::kRowPieces;
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) vb[c] = v_column_tr<RP>(v_tile, g, t, c);
+}
+// o[r][c] += P_r V from V operands already read (read_v_operands).
+template <int DTYPE, int D, int R>
+__device__ __forceinline__ void mfma_pv_operands(const s16x4 (&pa)[R], const s16x4 (&vb)[D / 16],
+                                                 f32x4 (&o)[R][D / 16]) {
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if constexpr (DTYPE == MV_DTYPE_BF16) {
+        o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[r], vb[c], o[r][c], 0, 0, 0);
+      } else {
+        o[r][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa[r]),
+                                                       __builtin_bit_cast(f16x4, vb[c]), o[r][c], 0, 0, 0);
+      }
+    }
+  }
+}
+
 // O tile update for one 16-token tile, 16-bit types, P already packed
 // (pack_p): o[r][c] += P_r V for R row tiles that share the tile.
 template <int DTYPE, int D, int R>
 __device__ __forceinline__ void mfma_pv_packed(const s16x4 (&pa)[R], const char* v_tile, int g, int t,
                                                f32x4 (&o)[R][D / 16]) {
   constexpr int RP = TileGeom<DTYPE, D>::kRowPieces;
-  // All of the tile's V operands are read before the first MFMA, so the
-  // reads overlap each other instead of each MFMA waiting for its own.
+  // At head_dim 64 all of the tile's V operands are read before the first
+  // MFMA, so the reads overlap each other instead of each MFMA waiting for
+  // its own (the scheduler would sink them); at 128 the pinned reads would
+  // not fit the prefill's registers, and the scheduler places them.
   s16x4 vb[D / 16];
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) vb[c] = v_column_tr<RP>(v_tile, g, t, c);
-  __builtin_amdgcn_sched_barrier(0);  // keep the reads together (the scheduler sinks them)
+  if constexpr (D <= 64) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
 #pragma unroll
