@@ -268,6 +268,13 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 __device__ __forceinline__ void copy_to_lds_16B(const char* src, uint32_t lds_base) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
 }
+// The same copy from a wave-uniform base address (SGPRs) plus this lane's
+// 32-bit byte offset (global_load_lds_dwordx4 with saddr): no 64-bit
+// address arithmetic per lane. `sbase` must be the same in every lane.
+__device__ __forceinline__ void copy_to_lds_16B_sv(const char* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
+}
+
 // The same copy with the non-temporal hint (nt): for data read once per
 // launch, such as the decode's K/V tiles. Measured on the decode kernel:
 // 5 % (c2-sized batches) to 13 % (head_dim 128, long contexts) less time

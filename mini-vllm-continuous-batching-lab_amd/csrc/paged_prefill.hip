@@ -91,6 +91,7 @@ struct PrefillArgs {
   float scale_log2;
   int32_t num_kv_heads, n_rep, tpw, bs_log2;
   uint32_t num_blocks_u32;
+  int32_t lane_offsets_32;  // 16 chunk rows of K and of V span < 2 GiB: 32-bit lane offsets
 };
 
 template <int DTYPE, int D, typename BT>
@@ -171,11 +172,51 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   const int win_tokens = kPfIdCap << a.bs_log2;  // a multiple of the stage size
   int win_blk0 = 0;
 
+  // Byte offset of this lane's copy slot c within one 16-token tile of a
+  // pool block, and within 16 chunk rows of row stride `st` (computed where
+  // used: keeping all of them live spills registers at head_dim 128).
+  auto pool_lane = [&](int c) { return static_cast<uint32_t>(slot_row[c] * Tr::kRowBytes + slot_piece[c] * 16); };
+  auto chunk_lane = [&](int c, int64_t st) { return static_cast<uint32_t>(slot_row[c] * st + slot_piece[c] * 16); };
+  const unsigned all_valid = (1u << L) - 1;
+
   // Copies wave's sub-tile of stage k (keys 64k + 16 wave ..) into buffer ST;
   // returns the slots that hold a key of the work group. Always 2L loads.
+  // Two wave-uniform cases take one base address in SGPRs and a 32-bit
+  // offset per lane: 16 prefix keys in one pool block (block size >= 16),
+  // and 16 chunk keys all below key_end; the rest (a sub-tile that
+  // straddles the prefix end or key_end, or smaller blocks) computes each
+  // lane's address.
   auto issue = [&](int k, auto st_c) __attribute__((always_inline)) -> unsigned {
     constexpr int ST = decltype(st_c)::value;
     const int kb = k * kPfStageTokens + wave * kTile;
+    const uint32_t dst = lds0 + ST * Tr::kStageBytes + wave * Tr::kSubBytes;
+    // (Not for 16-bit types at head_dim 128: their registers are full, and
+    // the extra live offsets spill.)
+    constexpr bool kUniformPaths = D == 64 || DTYPE == MV_DTYPE_F32;
+    if (kUniformPaths && kb + kTile <= cached && a.bs_log2 >= 4) {
+      const int id = __builtin_amdgcn_readfirstlane(s_ids[min((kb >> a.bs_log2) - win_blk0, kPfIdCap - 1)]);
+      const bool ok = static_cast<uint32_t>(id) < a.num_blocks_u32;
+      const int64_t row0 = ok ? ((static_cast<int64_t>(id) * a.num_kv_heads + h) << a.bs_log2) + (kb & bs_mask) : 0;
+      const char* bk = a.k_cache + row0 * Tr::kRowBytes;
+      const char* bv = a.v_cache + row0 * Tr::kRowBytes;
+#pragma unroll
+      for (int c = 0; c < L; ++c) {
+        copy_to_lds_16B_sv(bk, pool_lane(c), __builtin_amdgcn_readfirstlane(dst + c * 1024));
+        copy_to_lds_16B_sv(bv, pool_lane(c), __builtin_amdgcn_readfirstlane(dst + Tr::kTileBytes + c * 1024));
+      }
+      return ok ? all_valid : 0u;
+    }
+    if (kUniformPaths && kb >= cached && kb + kTile <= key_end && a.lane_offsets_32) {
+      const int64_t cr0 = qbase - tok0 + (kb - cached);  // chunk row of key kb
+      const char* bk = a.k_new + cr0 * a.k_st + h * a.k_sh;
+      const char* bv = a.v_new + cr0 * a.v_st + h * a.v_sh;
+#pragma unroll
+      for (int c = 0; c < L; ++c) {
+        copy_to_lds_16B_sv(bk, chunk_lane(c, a.k_st), __builtin_amdgcn_readfirstlane(dst + c * 1024));
+        copy_to_lds_16B_sv(bv, chunk_lane(c, a.v_st), __builtin_amdgcn_readfirstlane(dst + Tr::kTileBytes + c * 1024));
+      }
+      return all_valid;
+    }
     unsigned valid = 0;
     const char* srck[L];
     const char* srcv[L];
@@ -204,7 +245,6 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
       srcv[c] = bv + offv;
       valid |= ok ? (1u << c) : 0u;
     }
-    const uint32_t dst = lds0 + ST * Tr::kStageBytes + wave * Tr::kSubBytes;
 #pragma unroll
     for (int c = 0; c < L; ++c) {
       copy_to_lds_16B(srck[c], __builtin_amdgcn_readfirstlane(dst + c * 1024));
@@ -532,6 +572,10 @@ extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t
   a.tpw = 0;  // set per instantiation at launch
   a.bs_log2 = ilog2_exact(block_size);
   a.num_blocks_u32 = static_cast<uint32_t>(std::min<int64_t>(num_blocks, int64_t(1) << 31));
+  {
+    const int64_t span = 16 * std::max(std::abs(a.k_st), std::abs(a.v_st)) + 16 * head_dim * eb;
+    a.lane_offsets_32 = a.k_st >= 0 && a.v_st >= 0 && span < (int64_t(1) << 31);
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool i64 = bt_is_i64 != 0;
   const int n_rep = num_q_heads / num_kv_heads;
