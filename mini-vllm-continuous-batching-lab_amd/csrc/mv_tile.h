@@ -275,6 +275,11 @@ __device__ __forceinline__ void copy_to_lds_16B_sv(const char* sbase, uint32_t v
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
 }
 
+// Scalar base plus lane offset, non-temporal (see the two copies below).
+__device__ __forceinline__ void copy_to_lds_16B_sv_stream(const char* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
+}
+
 // The same copy with the non-temporal hint (nt): for data read once per
 // launch, such as the decode's K/V tiles. Measured on the decode kernel:
 // 5 % (c2-sized batches) to 13 % (head_dim 128, long contexts) less time

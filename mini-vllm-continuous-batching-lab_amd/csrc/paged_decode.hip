@@ -317,6 +317,24 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   auto issue_tile = [&](int k, auto st_c) __attribute__((always_inline)) -> unsigned {
     constexpr int ST = decltype(st_c)::value;
     const int tile_tok = tok_begin + k * Tr::kChunk + wave * kTile;
+    const uint32_t kdst = wave_tiles_lds + ST * Tr::kStageBytes;
+    // A whole tile in one pool block (block size >= 16; pieces start on
+    // tile boundaries): one wave-uniform base in SGPRs and a 32-bit offset
+    // per lane, no per-lane 64-bit address arithmetic.
+    if (a.bs_log2 >= 4 && tile_tok + kTile <= tok_end) {
+      const int id = __builtin_amdgcn_readfirstlane(s_ids[min((tile_tok >> a.bs_log2) - first_blk, kIdCap - 1)]);
+      const bool ok = static_cast<uint32_t>(id) < a.num_blocks_u32;  // -1 and stale ids fail
+      const int64_t row0 = ok ? ((static_cast<int64_t>(id) * a.num_kv_heads + h) << a.bs_log2) + (tile_tok & bs_mask) : 0;
+      const char* bk = a.k_cache + row0 * Tr::kRowBytes;
+      const char* bv = a.v_cache + row0 * Tr::kRowBytes;
+#pragma unroll
+      for (int c = 0; c < L; ++c) {
+        const uint32_t lane_off = static_cast<uint32_t>(slot_row[c] * Tr::kRowBytes + slot_piece[c] * 16);
+        copy_to_lds_16B_sv_stream(bk, lane_off, __builtin_amdgcn_readfirstlane(kdst + c * 1024));
+        copy_to_lds_16B_sv_stream(bv, lane_off, __builtin_amdgcn_readfirstlane(kdst + Tr::kTileBytes + c * 1024));
+      }
+      return ok ? (1u << L) - 1 : 0u;
+    }
     int64_t off[L];
     unsigned valid = 0;
 #pragma unroll
@@ -331,7 +349,6 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
                   : 0;
       valid |= ok ? (1u << c) : 0u;
     }
-    const uint32_t kdst = wave_tiles_lds + ST * Tr::kStageBytes;
 #pragma unroll
     for (int c = 0; c < L; ++c) {
       copy_to_lds_16B_stream(a.k_cache + off[c], __builtin_amdgcn_readfirstlane(kdst + c * 1024));
