@@ -108,6 +108,18 @@ def test_many_units_are_not_dealt():
     say(f"  groups {plan.num_groups} max abs err {err:.3g}")
 
 
+def test_batch_beyond_the_plan_length_cache():
+    """5000 sequences (more than the 4096 lengths the plan kernel keeps in
+    shared memory): lengths are read from memory in every pass, the block
+    search runs over the whole work group, and the groups are not dealt."""
+    lens = [1 + (13 * i) % 37 for i in range(5000)]
+    spec = WorkloadSpec("huge-batch", 14, 2, 64, 16, torch.bfloat16, len(lens), ("fixed", lens))
+    say("plan: 5000 sequences")
+    plan, err = _run_and_check(spec)
+    assert plan.num_groups >= 2 * len(lens)
+    say(f"  groups {plan.num_groups} P {plan.partition_tokens} max abs err {err:.3g}")
+
+
 def test_skewed_batch_uses_fair_pieces():
     """One-tile sequences filling all but 2 of the slots LDS allows (2 kv
     heads each; the plan's resident target is at most that) and one sequence
