@@ -154,6 +154,31 @@ __device__ __forceinline__ void mfma_pv_operands(const s16x4 (&pa)[R], const s16
   }
 }
 
+// o[r][c] += P_r V over two 16-token tiles a and b in one 16x16x32 MFMA per
+// column block (16-bit types): K slots 8g..8g+3 are tile a's tokens 4g..4g+3
+// and slots 8g+4..8g+7 tile b's, in both the P operand (pack_p of a, then b)
+// and the V operand (transposed reads of a, then b).
+template <int DTYPE, int D, int R>
+__device__ __forceinline__ void mfma_pv2_operands(const s16x4 (&pa)[R], const s16x4 (&pb)[R],
+                                                  const s16x4 (&va)[D / 16], const s16x4 (&vb)[D / 16],
+                                                  f32x4 (&o)[R][D / 16]) {
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
+    const s16x8 v = __builtin_shufflevector(va[c], vb[c], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const s16x8 p = __builtin_shufflevector(pa[r], pb[r], 0, 1, 2, 3, 4, 5, 6, 7);
+      if constexpr (DTYPE == MV_DTYPE_BF16) {
+        o[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, p),
+                                                          __builtin_bit_cast(bf16x8, v), o[r][c], 0, 0, 0);
+      } else {
+        o[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, p),
+                                                         __builtin_bit_cast(f16x8, v), o[r][c], 0, 0, 0);
+      }
+    }
+  }
+}
+
 // O tile update for one 16-token tile, 16-bit types, P already packed
 // (pack_p): o[r][c] += P_r V for R row tiles that share the tile.
 template <int DTYPE, int D, int R>

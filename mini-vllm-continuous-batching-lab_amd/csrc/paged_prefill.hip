@@ -38,9 +38,10 @@ namespace {
 
 constexpr int kPfIdCap = 2048;  // prefix block ids staged in LDS per window
 // Waves per work group: 8 (twice the query rows per pass over the keys,
-// and more waves to hide latency -- 51 us against 60 us with 4 on a
-// 4 x (1536 + 512) bf16 step) when two stages of 8 sub-tiles fit the LDS,
-// else 4 (fp32 at head_dim 128). Two stages: a third measured no faster.
+// and more waves to hide latency -- 39.8 us against 46.7 us with 4, two
+// such groups then sharing a CU, on a 4 x (1536 + 512) bf16 step) when two
+// stages of 8 sub-tiles fit the LDS, else 4 (fp32 at head_dim 128). Two
+// stages: a third measured no faster.
 // One 16-row MFMA tile per wave: two (half the LDS reads per key) measured
 // 76 us with 8 waves and 78 us with 4, three 103 us -- each wave's chain
 // of QK^T, softmax and PV per stage is what bounds the kernel, and more
@@ -50,6 +51,13 @@ constexpr int kPfIdCap = 2048;  // prefix block ids staged in LDS per window
 #endif
 #ifndef MV_PREFILL_ROWS
 #define MV_PREFILL_ROWS 1
+#endif
+// P V at head_dim 64 by one 16x16x32 MFMA per pair of sub-tiles: a
+// 16x16x16 bf16 MFMA issues every 18.6 cycles and a 16x16x32 one, twice
+// the work, every 16.6 (one wave, measured), so pairing halves the PV
+// MFMA time (38.2 against 40.2 us on the step above).
+#ifndef MV_PREFILL_PV32
+#define MV_PREFILL_PV32 1
 #endif
 template <int DTYPE, int D>
 struct PfTraits : TileGeom<DTYPE, D> {
@@ -64,6 +72,7 @@ struct PfTraits : TileGeom<DTYPE, D> {
   static constexpr int kIdsOffset = kStages * kStageBytes;
   static constexpr int kLdsBytes = kIdsOffset + kPfIdCap * 4;
   static_assert(kLdsBytes <= 160 * 1024, "LDS of one work group");
+  static_assert(kWaves % 2 == 0, "sub-tiles are paired for the 16x16x32 PV MFMA");
 };
 
 // Query tokens one work group covers: 16 MFMA rows per wave hold
@@ -386,7 +395,19 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         // V operands are read while this one's MFMAs run (two operand sets
         // in flight: 41.9 against 42.5 us); at 128 a second set would not
         // fit the registers.
-        if constexpr (D == 64) {
+        if constexpr (D == 64 && MV_PREFILL_PV32) {
+          // Two sub-tiles per 16x16x32 MFMA (half the MFMAs of 16x16x16).
+          // Past nu, P is 0 and every V slot holds a pool row or zeros.
+#pragma unroll
+          for (int u = 0; u < kPfWaves; u += 2) {
+            if (kWhole || u < nu) {
+              s16x4 va[D / 16], vb[D / 16];
+              read_v_operands<DTYPE, D>(stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, va);
+              read_v_operands<DTYPE, D>(stage + (u + 1) * Tr::kSubBytes + Tr::kTileBytes, g, t, vb);
+              mfma_pv2_operands<DTYPE, D, R>(pk[u], pk[u + 1], va, vb, o);
+            }
+          }
+        } else if constexpr (D == 64) {
           s16x4 vb[2][D / 16];
           read_v_operands<DTYPE, D>(stage + Tr::kTileBytes, g, t, vb[0]);
 #pragma unroll
