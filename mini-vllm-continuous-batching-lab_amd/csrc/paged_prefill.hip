@@ -13,20 +13,25 @@
 //
 // Work decomposition: one work group of W waves (8, or 4 for fp32 at
 // head_dim 128) per (sequence, kv head, block of query tokens). A wave owns
-// 16 MFMA rows; row r is query head (h * n_rep + r % n_rep) of token
-// (r / n_rep) of the wave's tpw = 16 / n_rep tokens, so one K/V pass serves
-// the whole GQA group of W * tpw tokens. The waves share one stream of keys:
-//   * a stage is 16 W keys: wave w copies sub-tile w (16 keys of K and V)
-//     from HBM straight to LDS (global_load_lds, XOR piece swizzle as in
-//     the decode kernel), two stages in flight;
-//   * after one barrier per stage every wave computes all sub-tiles for its
-//     rows: S^T = K Q^T (MFMA), per-row causal mask key <= cached + token,
-//     online softmax, O += P V (MFMA, V read by transposed LDS loads);
+// 16 R MFMA rows; row r is query head (h * n_rep + r % n_rep) of token
+// (r / n_rep) of the wave's tpw = 16 R / n_rep tokens, so one K/V pass
+// serves the whole GQA group of the work group's tokens. The waves share
+// one stream of keys:
+//   * a stage is 16 W T keys: wave w copies sub-tiles w, w + W, .. (T of
+//     them, 16 keys of K and V each) from HBM straight to LDS
+//     (global_load_lds, XOR piece swizzle as in the decode kernel), two
+//     stages in flight;
+//   * after one barrier per stage every wave computes its set's sub-tiles
+//     for its rows: S^T = K Q^T (MFMA), per-row causal mask key <= cached +
+//     token, online softmax, O += P V (MFMA, V read by transposed LDS loads);
 //   * prefix keys are addressed through the sequence's block ids, staged
 //     in LDS per window of kPfIdCap blocks; chunk keys through the chunk's
 //     row strides (q / k / v may be views of one fused QKV output).
-// Waves skip sub-tiles that lie wholly past their rows' causal limit; the
-// online softmax is updated once per stage of 64 keys.
+// 16-bit types at head_dim 64 run two sets of W/2 waves (R = 2, T = 2)
+// that split every stage's sub-tiles and merge their softmax states at the
+// end; the other instantiations one set (R = 1, T = 1). Waves skip
+// sub-tiles that lie wholly past their rows' causal limit; the online
+// softmax is updated once per stage.
 #include <algorithm>
 #include <climits>
 
@@ -52,6 +57,21 @@ constexpr int kPfIdCap = 2048;  // prefix block ids staged in LDS per window
 #ifndef MV_PREFILL_ROWS
 #define MV_PREFILL_ROWS 1
 #endif
+// 16-bit types at head_dim 64 (the Qwen2 shapes):
+// * Key split inside the work group: two sets of W/2 waves hold the same
+//   rows, two 16-row tiles per wave, and each set computes half of every
+//   stage's sub-tiles; the sets' softmax states are merged through LDS at
+//   the end. Every K/V byte staged in LDS is read by W/2 waves instead of W.
+// * Two sub-tiles copied per wave, so a stage is 256 keys: half the
+//   barriers, copy rounds and per-stage softmax exchanges per key.
+// Together 35.8 against 38.1 us on a 4 x (1536 + 512) bf16 step; either
+// alone measured no faster (38.8, 38.5 us).
+#ifndef MV_PREFILL_SETS
+#define MV_PREFILL_SETS 2
+#endif
+#ifndef MV_PREFILL_WAVE_TILES
+#define MV_PREFILL_WAVE_TILES 2
+#endif
 // P V at head_dim 64 by one 16x16x32 MFMA per pair of sub-tiles: a
 // 16x16x16 bf16 MFMA issues every 18.6 cycles and a 16x16x32 one, twice
 // the work, every 16.6 (one wave, measured), so pairing halves the PV
@@ -64,22 +84,33 @@ struct PfTraits : TileGeom<DTYPE, D> {
   using G = TileGeom<DTYPE, D>;
   static constexpr int kSubBytes = 2 * G::kTileBytes;  // K and V sub-tile of one wave
   static constexpr int kStages = 2;
-  static constexpr int kRows = MV_PREFILL_ROWS;  // 16-row MFMA tiles per wave
+  static constexpr int kWaveTiles =  // sub-tiles each wave copies per stage
+      DTYPE != MV_DTYPE_F32 && D == 64 ? MV_PREFILL_WAVE_TILES : 1;
   static constexpr int kWaves =
-      kStages * MV_PREFILL_WAVES * kSubBytes + kPfIdCap * 4 <= 160 * 1024 ? MV_PREFILL_WAVES : 4;
-  static constexpr int kStageTokens = kWaves * kTile;  // keys per stage: one sub-tile per wave
-  static constexpr int kStageBytes = kWaves * kSubBytes;
+      kStages * MV_PREFILL_WAVES * kSubBytes * kWaveTiles + kPfIdCap * 4 <= 160 * 1024 ? MV_PREFILL_WAVES : 4;
+  // sets of waves splitting each stage's sub-tiles (same rows in every set)
+  static constexpr int kSets = DTYPE != MV_DTYPE_F32 && D == 64 && kWaves % (2 * MV_PREFILL_SETS) == 0
+                                   ? MV_PREFILL_SETS : 1;
+  static constexpr int kRowWaves = kWaves / kSets;      // waves with distinct rows
+  static constexpr int kSetTiles = kWaves * kWaveTiles / kSets;  // sub-tiles per set and stage
+  static constexpr int kRows = MV_PREFILL_ROWS * kSets;  // 16-row MFMA tiles per wave
+  static constexpr int kStageTokens = kWaves * kWaveTiles * kTile;
+  static constexpr int kStageBytes = kWaves * kWaveTiles * kSubBytes;
   static constexpr int kIdsOffset = kStages * kStageBytes;
   static constexpr int kLdsBytes = kIdsOffset + kPfIdCap * 4;
   static_assert(kLdsBytes <= 160 * 1024, "LDS of one work group");
-  static_assert(kWaves % 2 == 0, "sub-tiles are paired for the 16x16x32 PV MFMA");
+  static_assert(kSetTiles % 2 == 0, "sub-tiles are paired for the 16x16x32 PV MFMA");
+  // the set merge reuses the stage buffers: m, l and O of every row wave
+  static constexpr int kMergeFloats = kRows * 16 * 2 + kRows * D * 16;
+  static_assert(kSets == 1 || kRowWaves * kMergeFloats * 4 <= kIdsOffset, "set merge in LDS");
 };
 
-// Query tokens one work group covers: 16 MFMA rows per wave hold
-// floor(16 / n_rep) tokens' GQA groups.
+// Query tokens one work group covers: 16 kRows MFMA rows per row wave hold
+// floor(16 kRows / n_rep) tokens' GQA groups.
 template <int DTYPE, int D>
 constexpr int pf_tokens_per_group(int n_rep) {
-  return n_rep > 16 ? 0 : PfTraits<DTYPE, D>::kWaves * (16 * PfTraits<DTYPE, D>::kRows / n_rep);
+  using Tr = PfTraits<DTYPE, D>;
+  return n_rep > 16 ? 0 : Tr::kRowWaves * (16 * Tr::kRows / n_rep);
 }
 
 struct PrefillArgs {
@@ -114,6 +145,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   constexpr int R = Tr::kRows;
   constexpr int kPfWaves = Tr::kWaves;
   constexpr int kPfStageTokens = Tr::kStageTokens;
+  constexpr int U = Tr::kSetTiles;
 
   __shared__ __attribute__((aligned(16))) char s_lds[Tr::kLdsBytes];
   int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
@@ -123,6 +155,8 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   const int lane = threadIdx.x & 63;
   const int t = lane & 15;  // MFMA: key row (K operand) / query row (results)
   const int g = lane >> 4;  // MFMA: dim quarter (K operand) / key quad (results)
+  const int rwave = Tr::kSets == 1 ? wave : wave % Tr::kRowWaves;  // rows
+  const int set = Tr::kSets == 1 ? 0 : wave / Tr::kRowWaves;       // sub-tiles set * U .. of every stage
 
   const int4 w = reinterpret_cast<const int4*>(a.work)[blockIdx.x];
   const int seq = w.x, h = w.y, tok0 = w.z, ntok = w.w;
@@ -133,7 +167,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   const int bs_mask = (1 << a.bs_log2) - 1;
 
   // ---- rows of this wave: limits and Q (registers, straight from HBM)
-  const int wtok0 = wave * a.tpw;
+  const int wtok0 = rwave * a.tpw;
   const int wtok_end = min(ntok, wtok0 + a.tpw);
   // the last key any row of the wave sees (-1: the wave has no rows)
   const int wave_limit = wtok0 < ntok ? cached + tok0 + wtok_end - 1 : -1;
@@ -195,10 +229,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   // and 16 chunk keys all below key_end; the rest (a sub-tile that
   // straddles the prefix end or key_end, or smaller blocks) computes each
   // lane's address.
-  auto issue = [&](int k, auto st_c) __attribute__((always_inline)) -> unsigned {
-    constexpr int ST = decltype(st_c)::value;
-    const int kb = k * kPfStageTokens + wave * kTile;
-    const uint32_t dst = lds0 + ST * Tr::kStageBytes + wave * Tr::kSubBytes;
+  auto issue_sub = [&](int kb, uint32_t dst) __attribute__((always_inline)) -> unsigned {
     // (Not for 16-bit types at head_dim 128: their registers are full, and
     // the extra live offsets spill.)
     constexpr bool kUniformPaths = D == 64 || DTYPE == MV_DTYPE_F32;
@@ -262,38 +293,55 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     return valid;
   };
 
+  // The wave's sub-tiles j * kPfWaves + wave of stage k; slot bits j * L + c.
+  auto issue = [&](int k, auto st_c) __attribute__((always_inline)) -> unsigned {
+    constexpr int ST = decltype(st_c)::value;
+    unsigned v = 0;
+#pragma unroll
+    for (int j = 0; j < Tr::kWaveTiles; ++j) {
+      const int su = j * kPfWaves + wave;
+      v |= issue_sub(k * kPfStageTokens + su * kTile, lds0 + ST * Tr::kStageBytes + su * Tr::kSubBytes)
+           << (j * L);
+    }
+    return v;
+  };
+
   // V slots of keys that were not loaded read pool row 0 instead: zero
   // them (P is 0 there, but 0 * NaN would not be).
   auto zero_invalid_v = [&](int st, unsigned valid) __attribute__((always_inline)) {
-    char* vdst = s_lds + st * Tr::kStageBytes + wave * Tr::kSubBytes + Tr::kTileBytes;
 #pragma unroll
-    for (int c = 0; c < L; ++c)
-      if (!((valid >> c) & 1u))
-        *reinterpret_cast<uint4*>(vdst + c * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < Tr::kWaveTiles; ++j) {
+      char* vdst = s_lds + st * Tr::kStageBytes + (j * kPfWaves + wave) * Tr::kSubBytes + Tr::kTileBytes;
+#pragma unroll
+      for (int c = 0; c < L; ++c)
+        if (!((valid >> (j * L + c)) & 1u))
+          *reinterpret_cast<uint4*>(vdst + c * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
+    }
   };
 
   // The smallest causal limit among the wave's rows: a stage that ends at
   // or before it is seen whole by every row (no mask).
   const int wave_first_limit = cached + tok0 + wtok0;
 
-  // One stage (kPfWaves sub-tiles of 16 keys) for this wave's rows: S^T for
-  // every sub-tile some row may see, one online-softmax update per row tile
+  // One stage for this wave's rows, over the U sub-tiles of 16 keys of its
+  // set (all kPfWaves sub-tiles with one set): S^T for every sub-tile some
+  // row may see, one online-softmax update per row tile
   // over the whole stage (one max / sum exchange and one rescale of O),
   // then O += P V per sub-tile. The 16-bit types mask only the stages that
   // cross the causal diagonal, fold the scale into the exponent's FMA
   // (exp2(s * scale - m); the max is taken on unscaled scores, as scale > 0)
   // and round P once, packed, for both the PV MFMA and the row sum.
   auto compute_stage = [&](int k, int st) __attribute__((always_inline)) {
-    const int k_first = k * kPfStageTokens;
-    if (k_first > wave_limit) return;  // causal: no row of the wave sees this stage
+    const int k_first = k * kPfStageTokens + set * U * kTile;  // the set's first key
+    if (k_first > wave_limit) return;  // causal: no row of the wave sees these keys
     // sub-tiles u < nu hold keys some row of the wave sees
-    const int nu = min(kPfWaves, (wave_limit - k_first) / kTile + 1);
-    const bool whole = k_first + kPfStageTokens - 1 <= wave_first_limit;  // then nu == kPfWaves
-    const char* stage = s_lds + st * Tr::kStageBytes;
+    const int nu = min(U, (wave_limit - k_first) / kTile + 1);
+    const bool whole = k_first + U * kTile - 1 <= wave_first_limit;  // then nu == U
+    const char* stage = s_lds + st * Tr::kStageBytes + set * U * Tr::kSubBytes;
     const int ksw = piece_swizzle<RP>(t);
-    f32x4 acc[kPfWaves][R];
+    f32x4 acc[U][R];
 #pragma unroll
-    for (int u = 0; u < kPfWaves; ++u) {
+    for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int rt = 0; rt < R; ++rt) acc[u][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
       if (u < nu) {
@@ -307,12 +355,12 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
       }
     }
     if constexpr (DTYPE == MV_DTYPE_F32) {
-      float pr[kPfWaves][R][4];
+      float pr[U][R][4];
 #pragma unroll
       for (int rt = 0; rt < R; ++rt) {
         float mc = kNegInf;
 #pragma unroll
-        for (int u = 0; u < kPfWaves; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int key = k_first + u * kTile + 4 * g + e;
@@ -327,7 +375,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
         float lc = 0.f;
 #pragma unroll
-        for (int u = 0; u < kPfWaves; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             pr[u][rt][e] = __builtin_amdgcn_exp2f(acc[u][rt][e] - m_ref);
@@ -345,24 +393,33 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         }
       }
 #pragma unroll
-      for (int u = 0; u < kPfWaves; ++u)
+      for (int u = 0; u < U; ++u)
         if (u < nu) mfma_pv_rows<DTYPE, D, R>(pr[u], stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, o);
     } else {
       // Two instantiations, chosen once per stage (a uniform branch): the
       // compiler would otherwise compute the mask and select per element.
       auto softmax_pv = [&](auto whole_c) __attribute__((always_inline)) {
         constexpr bool kWhole = decltype(whole_c)::value;
-        s16x4 pk[kPfWaves][R];
+        s16x4 pk[U][R];
 #pragma unroll
         for (int rt = 0; rt < R; ++rt) {
           float mc = kNegInf;
+          int lim = 0;
+          if constexpr (!kWhole) {
+            // the row's causal limit, recomputed in the few masked stages
+            // (opaque to hoisting: a live copy per row tile costs registers)
+            int r = rt * 16 + t;
+            asm volatile("" : "+v"(r));
+            const int rtok = wtok0 + r / a.n_rep;
+            lim = r < a.tpw * a.n_rep && rtok < ntok ? cached + tok0 + rtok : -1;
+          }
 #pragma unroll
-          for (int u = 0; u < kPfWaves; ++u)
+          for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               if constexpr (!kWhole) {
                 const int key = k_first + u * kTile + 4 * g + e;
-                acc[u][rt][e] = u < nu && key <= limit[rt] ? acc[u][rt][e] : kNegInf;
+                acc[u][rt][e] = u < nu && key <= lim ? acc[u][rt][e] : kNegInf;
               }
               mc = fmaxf(mc, acc[u][rt][e]);
             }
@@ -373,7 +430,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
           const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
           float lc = 0.f;
 #pragma unroll
-          for (int u = 0; u < kPfWaves; ++u) {
+          for (int u = 0; u < U; ++u) {
             float pe[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -399,7 +456,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
           // Two sub-tiles per 16x16x32 MFMA (half the MFMAs of 16x16x16).
           // Past nu, P is 0 and every V slot holds a pool row or zeros.
 #pragma unroll
-          for (int u = 0; u < kPfWaves; u += 2) {
+          for (int u = 0; u < U; u += 2) {
             if (kWhole || u < nu) {
               s16x4 va[D / 16], vb[D / 16];
               read_v_operands<DTYPE, D>(stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, va);
@@ -411,9 +468,9 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
           s16x4 vb[2][D / 16];
           read_v_operands<DTYPE, D>(stage + Tr::kTileBytes, g, t, vb[0]);
 #pragma unroll
-          for (int u = 0; u < kPfWaves; ++u) {
+          for (int u = 0; u < U; ++u) {
             if (kWhole || u < nu) {
-              if (u + 1 < kPfWaves && (kWhole || u + 1 < nu))
+              if (u + 1 < U && (kWhole || u + 1 < nu))
                 read_v_operands<DTYPE, D>(stage + (u + 1) * Tr::kSubBytes + Tr::kTileBytes, g, t,
                                           vb[(u + 1) & 1]);
               __builtin_amdgcn_sched_barrier(0);
@@ -422,7 +479,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
           }
         } else {
 #pragma unroll
-          for (int u = 0; u < kPfWaves; ++u)
+          for (int u = 0; u < U; ++u)
             if (kWhole || u < nu)
               mfma_pv_packed<DTYPE, D, R>(pk[u], stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, o);
         }
@@ -455,7 +512,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     auto step = [&](int i, auto st_c) __attribute__((always_inline)) {
       constexpr int ST = decltype(st_c)::value;
       constexpr int NX = (ST + S - 1) % S;
-      wait_vmcnt_groups<2 * L, S - 2>(min(S - 2, n - 1 - i));
+      wait_vmcnt_groups<2 * L * Tr::kWaveTiles, S - 2>(min(S - 2, n - 1 - i));
       asm volatile("" ::: "memory");
       zero_invalid_v(ST, valid[ST]);
       __syncthreads();
@@ -475,13 +532,60 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     __syncthreads();  // every wave is done with this window's stages and ids
   }
 
+  // Lane coordinates recomputed for the epilogue rather than kept live
+  // through the key loop (registers are full there).
+  const int lane_e = __lane_id();
+  const int te = lane_e & 15, ge = lane_e >> 4;
+
+  // ---- merge the sets' softmax states (same rows): set s > 0 leaves m, l
+  // and O in LDS (the stage buffers, free after the last barrier), set 0
+  // folds them in and stores
+  if constexpr (Tr::kSets > 1) {
+    static_assert(Tr::kSets == 2, "two sets");
+    float* xm = reinterpret_cast<float*>(s_lds) + rwave * Tr::kMergeFloats;  // m[R*16], l[R*16], O
+    float* xo = xm + R * 32 + lane_e;
+    if (set == 1) {
+#pragma unroll
+      for (int rt = 0; rt < R; ++rt) {
+        if (ge == 0) {
+          xm[rt * 16 + te] = m_run[rt];
+          xm[R * 16 + rt * 16 + te] = l_run[rt];
+        }
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xo[((rt * (D / 16) + c) * 4 + e) * 64] = o[rt][c][e];
+      }
+    }
+    __syncthreads();
+    if (set == 1) return;
+#pragma unroll
+    for (int rt = 0; rt < R; ++rt) {
+      const float m1 = xm[rt * 16 + te];
+      const float l1 = xm[R * 16 + rt * 16 + te];
+      const float m = fmaxf(m_run[rt], m1);
+      const float m_ref = m == kNegInf ? 0.f : m;
+      const float a0 = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
+      const float a1 = __builtin_amdgcn_exp2f(m1 - m_ref);
+      l_run[rt] = l_run[rt] * a0 + l1 * a1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a0r = __shfl(a0, 4 * ge + e);
+        const float a1r = __shfl(a1, 4 * ge + e);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+          o[rt][c][e] = o[rt][c][e] * a0r + xo[((rt * (D / 16) + c) * 4 + e) * 64] * a1r;
+      }
+    }
+  }
+
   // ---- normalise and store this wave's rows
 #pragma unroll
   for (int rt = 0; rt < R; ++rt) {
     const float inv = l_run[rt] > 0.f ? 1.f / l_run[rt] : 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int rr = 4 * g + e;  // row of o[rt][.][e]
+      const int rr = 4 * ge + e;  // row of o[rt][.][e]
       const float ir = __shfl(inv, rr);
       const int r = rt * 16 + rr;
       const int rtok = wtok0 + r / a.n_rep;
@@ -489,7 +593,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         raw_t* op = static_cast<raw_t*>(a.out) + (qbase + rtok) * a.o_st +
                     (h * a.n_rep + r % a.n_rep) * a.o_sh;
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c) op[16 * c + t] = from_f32<DTYPE>(o[rt][c][e] * ir);
+        for (int c = 0; c < D / 16; ++c) op[16 * c + te] = from_f32<DTYPE>(o[rt][c][e] * ir);
       }
     }
   }
@@ -498,7 +602,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
 template <int DTYPE, int D>
 int launch_prefill(PrefillArgs a, int n_rep, int groups, bool bt_i64, hipStream_t s) {
   constexpr int kThreads = PfTraits<DTYPE, D>::kWaves * 64;
-  a.tpw = pf_tokens_per_group<DTYPE, D>(n_rep) / PfTraits<DTYPE, D>::kWaves;
+  a.tpw = pf_tokens_per_group<DTYPE, D>(n_rep) / PfTraits<DTYPE, D>::kRowWaves;
   if (bt_i64) paged_prefill_kernel<DTYPE, D, int64_t><<<groups, kThreads, 0, s>>>(a);
   else paged_prefill_kernel<DTYPE, D, int32_t><<<groups, kThreads, 0, s>>>(a);
   return check_launch("mv_paged_prefill");

@@ -86,6 +86,8 @@ SHAPES = [  # (hq, hkv, d, bs, dtype)
     (8, 8, 64, 32, torch.float16),     # n_rep 1
     (16, 1, 128, 16, torch.bfloat16),  # n_rep 16
     (16, 1, 64, 64, torch.bfloat16),   # n_rep 16, block 64
+    (10, 2, 64, 16, torch.bfloat16),   # n_rep 5: 6 tokens per row wave, 2 padding rows
+    (12, 2, 64, 16, torch.float16),    # n_rep 6: 5 tokens per row wave (20 per work group)
 ]
 
 
