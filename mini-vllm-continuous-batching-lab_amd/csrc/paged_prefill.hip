@@ -47,10 +47,11 @@ constexpr int kPfIdCap = 2048;  // prefix block ids staged in LDS per window
 // such groups then sharing a CU, on a 4 x (1536 + 512) bf16 step) when two
 // stages of 8 sub-tiles fit the LDS, else 4 (fp32 at head_dim 128). Two
 // stages: a third measured no faster.
-// One 16-row MFMA tile per wave: two (half the LDS reads per key) measured
-// 76 us with 8 waves and 78 us with 4, three 103 us -- each wave's chain
-// of QK^T, softmax and PV per stage is what bounds the kernel, and more
-// rows per wave lengthen it.
+// 16-row MFMA tiles per wave in one set of waves: one. Two with 8 waves
+// (32 tokens per work group) halve the work groups: 57.6 against 38.2 us
+// on that step, though 18 % faster per sequence at 16 sequences, where
+// there are enough work groups; the two sets below keep 16 tokens per
+// work group with two tiles per wave.
 #ifndef MV_PREFILL_WAVES
 #define MV_PREFILL_WAVES 8
 #endif
