@@ -68,6 +68,23 @@ def test_abi_queries(lib):
     assert lib.mv_decode_groups_per_cu(96, 2) == 0
 
 
+def test_prefill_tokens_per_group(lib):
+    """Query tokens one prefill work group covers: 16-bit types at head_dim
+    64 run 4 row waves of two 16-row tiles (two wave sets), the others 8
+    (4 for fp32 at head_dim 128) of one tile; a wave holds
+    floor(rows / n_rep) tokens."""
+    f = lib.mv_prefill_tokens_per_group
+    assert f(14, 2, 64, 2) == 4 * (32 // 7) == 16    # Qwen2-0.5B, bf16
+    assert f(12, 2, 64, 1) == 4 * (32 // 6) == 20    # n_rep 6, fp16: 5 tokens per row wave
+    assert f(14, 2, 64, 0) == 8 * (16 // 7) == 16    # fp32: one set
+    assert f(28, 4, 128, 2) == 8 * (16 // 7) == 16   # head_dim 128: one set
+    assert f(8, 8, 64, 2) == 4 * 32 == 128           # MHA
+    assert f(14, 2, 128, 0) == 4 * (16 // 7) == 8    # fp32 at head_dim 128: 4 waves
+    assert f(17, 1, 64, 2) == 0                      # more than 16 query heads per kv head
+    assert f(14, 3, 64, 2) == 0                      # not a whole GQA group
+    assert f(14, 2, 96, 2) == 0                      # head_dim
+
+
 def test_workspace_bytes(lib):
     assert lib.mv_paged_decode_workspace_bytes(64, 14, 64, 1) == 0
     o = 64 * 14 * 8 * 64 * 4
