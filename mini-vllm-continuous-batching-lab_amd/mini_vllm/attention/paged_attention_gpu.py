@@ -92,9 +92,10 @@ class _SeenTensors:
     def matches(self, tensors: Sequence[torch.Tensor], extra: tuple) -> bool:
         if extra != self.extra or len(tensors) != len(self.refs):
             return False
-        return all(
-            r() is t and t._version == v for r, v, t in zip(self.refs, self.versions, tensors)
-        )
+        for r, v, t in zip(self.refs, self.versions, tensors):
+            if r() is not t or t._version != v:
+                return False
+        return True
 
 
 _state = threading.local()
@@ -169,15 +170,19 @@ def clear_deferred() -> None:
 # ============================================================================
 
 
-def _check_slots(slot_mapping: torch.Tensor, total_slots: int) -> None:
+def _check_slots(slot_mapping: torch.Tensor, total_slots: int,
+                 capturing: Optional[bool] = None) -> None:
     """Raise like the reference for out-of-range or duplicate slots.
 
     Out of range (``< -1`` or ``>= total_slots``): ``IndexError`` with
     "out of range" (reference cache_write.py:61-66). Duplicates among the
     non-(-1) slots: ``AssertionError`` with "Duplicate" (reference
     paged_attention_gpu.py:126-135). Both checks run in one device kernel.
+    ``capturing``: whether the current stream is being captured, when the
+    caller already knows.
     """
-    capturing = _capturing()
+    if capturing is None:
+        capturing = _capturing()
     name = "slots_graph" if capturing else "slots"
     extra = (total_slots,)
     if _cache_get(name, (slot_mapping,), extra) is not None:
@@ -319,6 +324,7 @@ def plan_decode(
     head_dim: int,
     dtype: torch.dtype,
     num_kv_heads: int,
+    capturing: Optional[bool] = None,
 ) -> DecodePlan:
     """Validate decode metadata, pick the partition size, build the work list.
 
@@ -334,11 +340,13 @@ def plan_decode(
     While the current stream is being captured into a graph the plan
     cannot be read back: it is enqueued for a launch of fixed size
     (``mv_decode_graph_bounds``), and its checks raise from
-    ``check_deferred()`` after a replay instead.
+    ``check_deferred()`` after a replay instead. ``capturing``: whether the
+    current stream is being captured, when the caller already knows.
     """
     lib = _hip.load()
     split = _groups_per_cu(device, head_dim, dtype)
-    capturing = _capturing()
+    if capturing is None:
+        capturing = _capturing()
     name = "plan_graph" if capturing else "plan"
     extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads, split)
     cached = _cache_get(name, (block_table, kv_len_after), extra)
@@ -458,8 +466,12 @@ def hip_decode_attention(
     slot lies in a block another sequence of the batch attends (what the
     block manager guarantees).
     """
+    # (The per-call checks read each attribute once: this wrapper runs once
+    # per layer, and its host time exceeds the kernel's when it does not.)
     total_decode, num_q_heads, head_dim = query.shape
-    num_kv_heads = key_cache.shape[1]
+    kshape = key_cache.shape
+    num_kv_heads = kshape[1]
+    dtype = query.dtype
     assert head_dim in SUPPORTED_HEAD_DIMS, f"head_dim {head_dim} not supported (only 64, 128)"
     assert block_size > 0 and _is_pow2(block_size), f"block_size {block_size} must be a power of 2"
     assert num_q_heads % num_kv_heads == 0, (
@@ -468,20 +480,21 @@ def hip_decode_attention(
     assert num_q_heads // num_kv_heads <= MAX_QUERY_HEADS_PER_KV_HEAD, (
         f"{num_q_heads // num_kv_heads} query heads per kv head (max {MAX_QUERY_HEADS_PER_KV_HEAD})"
     )
-    assert query.dtype in SUPPORTED_DTYPES, f"query dtype {query.dtype} not supported"
-    assert key_cache.dtype == query.dtype, f"key_cache dtype {key_cache.dtype} != {query.dtype}"
-    assert value_cache.dtype == query.dtype
-    assert query.device.type == "cuda"
-    assert key_cache.shape == value_cache.shape
-    assert key_cache.shape[2] == block_size and key_cache.shape[3] == head_dim
+    assert dtype in SUPPORTED_DTYPES, f"query dtype {dtype} not supported"
+    assert key_cache.dtype == dtype, f"key_cache dtype {key_cache.dtype} != {dtype}"
+    assert value_cache.dtype == dtype
+    assert query.is_cuda
+    assert kshape == value_cache.shape
+    assert kshape[2] == block_size and kshape[3] == head_dim
     assert key_cache.is_contiguous() and value_cache.is_contiguous()
     assert block_table.shape[0] == total_decode
     assert kv_len_after.shape == (total_decode,)
 
     device = query.device
-    num_blocks = key_cache.shape[0]
+    num_blocks = kshape[0]
+    capturing = _capturing()
     plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
-                       query.dtype, num_kv_heads)
+                       dtype, num_kv_heads, capturing=capturing)
     output = torch.empty_like(query, memory_format=torch.contiguous_format)
     if total_decode == 0 or plan.num_groups == 0:
         return output
@@ -494,11 +507,12 @@ def hip_decode_attention(
     ws = _workspace(device, ws_bytes) if ws_bytes else None
     if new_key is not None:
         assert new_value is not None and slot_mapping is not None
-        assert new_key.shape == (total_decode, num_kv_heads, head_dim), (
-            f"new_key {tuple(new_key.shape)} != ({total_decode}, {num_kv_heads}, {head_dim})"
+        nshape = new_key.shape
+        assert nshape == (total_decode, num_kv_heads, head_dim), (
+            f"new_key {tuple(nshape)} != ({total_decode}, {num_kv_heads}, {head_dim})"
         )
-        assert new_value.shape == new_key.shape
-        assert new_key.dtype == query.dtype and new_value.dtype == query.dtype
+        assert new_value.shape == nshape
+        assert new_key.dtype == dtype and new_value.dtype == dtype
         assert new_key.device == device and new_value.device == device
         assert slot_mapping.shape == (total_decode,)
         if slot_mapping.device != device:
@@ -506,7 +520,7 @@ def hip_decode_attention(
         if slot_mapping.dtype != torch.int64:
             slot_mapping = slot_mapping.to(torch.int64)
         slot_mapping = slot_mapping.contiguous()
-        _check_slots(slot_mapping, num_blocks * block_size)
+        _check_slots(slot_mapping, num_blocks * block_size, capturing=capturing)
         nk, nv = _aligned_rows(new_key), _aligned_rows(new_value)
         _hip.check(
             lib.mv_paged_decode_write(
@@ -517,7 +531,7 @@ def hip_decode_attention(
                 plan.partition_tokens, plan.max_parts, _ptr(plan.counters),
                 _ptr(output), output.stride(0), output.stride(1),
                 float(head_dim ** -0.5), total_decode, num_q_heads, num_kv_heads, head_dim,
-                block_size, num_blocks, _hip.MV_DTYPE[query.dtype],
+                block_size, num_blocks, _hip.MV_DTYPE[dtype],
                 _ptr(ws), ws.numel() if ws is not None else 0, _stream(device),
             ),
             "mv_paged_decode_write",
@@ -531,7 +545,7 @@ def hip_decode_attention(
             plan.partition_tokens, plan.max_parts, _ptr(plan.counters),
             _ptr(output), output.stride(0), output.stride(1),
             float(head_dim ** -0.5), total_decode, num_q_heads, num_kv_heads, head_dim,
-            block_size, num_blocks, _hip.MV_DTYPE[query.dtype],
+            block_size, num_blocks, _hip.MV_DTYPE[dtype],
             _ptr(ws), ws.numel() if ws is not None else 0, _stream(device),
         ),
         "mv_paged_decode",
@@ -845,8 +859,8 @@ def _prefill_plan(block_table, rows, cached, qlens, block_size, num_blocks, num_
 def _aligned_rows(x: torch.Tensor) -> torch.Tensor:
     """x with 16-byte aligned, head_dim-contiguous rows (a copy only if not)."""
     eb = x.element_size()
-    if (x.stride(-1) != 1 or (x.stride(0) * eb) % 16 or (x.stride(1) * eb) % 16
-            or x.data_ptr() % 16):
+    st = x.stride()
+    if st[-1] != 1 or (st[0] * eb) % 16 or (st[1] * eb) % 16 or x.data_ptr() % 16:
         x = x.contiguous()
     return x
 
