@@ -49,6 +49,38 @@ def test_header_declares_the_path():
         assert name in decl
 
 
+def test_c_host_compiles_and_links_against_the_header(lib, tmp_path):
+    """A plain C99 host (gcc, no HIP headers) that takes the address of
+    every function mvattn.h declares and calls the ones that need no
+    device: the header stands alone and the library resolves it all."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    decl = _declared_functions()
+    src = tmp_path / "host.c"
+    src.write_text(
+        "#include <stdio.h>\n#include \"mvattn.h\"\n"
+        "int main(void) {\n"
+        "  void* fns[] = {" + ", ".join(f"(void*){n}" for n in sorted(decl)) + "};\n"
+        "  for (unsigned i = 0; i < sizeof fns / sizeof fns[0]; ++i) if (!fns[i]) return 2;\n"
+        "  if (mv_abi_version() != 3) return 3;\n"
+        "  if (mv_decode_chunk_tokens(64, MV_DTYPE_BF16) != 64) return 4;\n"
+        "  if (mv_prefill_tokens_per_group(14, 2, 64, MV_DTYPE_BF16) != 16) return 5;\n"
+        "  printf(\"ok %u\\n\", (unsigned)(sizeof fns / sizeof fns[0]));\n"
+        "  return 0;\n}\n")
+    exe = tmp_path / "host"
+    libdir = os.path.dirname(_hip.library_path())
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src),
+                    "-L", libdir, "-lmvattn", f"-Wl,-rpath,{libdir}", "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, (out.returncode, out.stderr)
+    assert out.stdout.strip() == f"ok {len(decl)}"
+
+
 def test_every_declared_symbol_is_exported_and_typed(lib):
     decl = _declared_functions()
     for name, nparams in decl.items():
