@@ -40,7 +40,7 @@ def _decode_spec(seed):
     return WorkloadSpec(f"sweep{seed}", hq, hkv, d, bs, dt, batch, ("fixed", lens))
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(32))
 def test_decode_sweep(seed):
     spec = _decode_spec(seed)
     say("decode sweep", seed, spec.num_q_heads, spec.num_kv_heads, spec.head_dim, spec.block_size,
@@ -75,7 +75,7 @@ def _prefill_args(seed):
     return hq, hkv, d, bs, dt, cached, qlen
 
 
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(16))
 def test_prefill_sweep(seed):
     hq, hkv, d, bs, dt, cached, qlen = _prefill_args(seed)
     say("prefill sweep", seed, hq, hkv, d, bs, dt, cached, qlen)
