@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define MVATTN_ABI_VERSION 3
+#define MVATTN_ABI_VERSION 4
 
 /* Element types of query / key / value / cache / output. */
 #define MV_DTYPE_F32 0
@@ -70,6 +70,15 @@ int mv_abi_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* mv_last_error(void);
+
+/*
+ * Capture id of `stream`: *capture_id = the id of the graph capture the
+ * stream is in (nonzero), or 0 when it is not being captured. No
+ * counterpart in the reference (which has no graph capture): the host side
+ * keys its per-capture caches and deferred checks by it, so that a second
+ * capture over the same metadata tensors records its own plan and checks.
+ */
+int mv_stream_capture_id(void* stream, uint64_t* capture_id);
 
 /* Tokens one decode work group iteration covers for (head_dim, dtype):
  * partitions are multiples of it (0 for an unsupported pair). */
@@ -111,6 +120,24 @@ int mv_kv_cache_write(const void* key, int64_t key_stride_tok, int64_t key_strid
  */
 int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t total_slots,
                       int32_t* status, void* stream);
+
+/*
+ * Precondition check of mv_paged_decode_write (the fused decode + KV write;
+ * no counterpart in the reference, whose runner makes the two calls):
+ * status[0] (int32, device) = number of sequences b whose slot_mapping[b]
+ * is neither -1 nor the table position of b's token kv_len[b] - 1, i.e.
+ * block_table[b, (kv_len[b]-1) / block_size] * block_size +
+ * (kv_len[b]-1) % block_size (a sequence whose kv_len or table entry
+ * cannot address that position counts too). When it is 0 -- and no other
+ * sequence of the batch attends those slots, which the block manager
+ * guarantees (a sequence's last block is its own) -- the fused call is
+ * bit-identical to mv_kv_cache_write followed by mv_paged_decode. The
+ * block table and kv_len may each be int32 or int64.
+ */
+int mv_decode_write_check(const int64_t* slot_mapping, const void* block_table, int32_t bt_is_i64,
+                          int64_t bt_stride, const void* kv_len, int32_t kv_len_is_i64,
+                          int32_t num_seqs, int32_t max_blocks, int32_t block_size,
+                          int32_t* status, void* stream);
 
 /*
  * Per-step decode metadata: validation, work split, work list.
@@ -327,7 +354,8 @@ int mv_prefill_tokens_per_group(int32_t num_q_heads, int32_t num_kv_heads, int32
  *   work_items  int32[4] per work group: (sequence, kv head, first chunk
  *               token, tokens <= mv_prefill_tokens_per_group); the caller
  *               lists every (sequence, kv head, token block) once, in any
- *               order (longest first balances best);
+ *               order (longest first balances best); an item whose
+ *               sequence is -1 is an unused slot and does nothing;
  *   out         [rows, num_q_heads, head_dim], query dtype.
  * head_dim 64 or 128, power-of-two block_size, 16-byte aligned rows.
  */
@@ -340,6 +368,30 @@ int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_h
                      int64_t out_stride_tok, int64_t out_stride_head, float scale,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream);
+
+/*
+ * Device-side plan of mv_paged_prefill for a launch of fixed size, e.g.
+ * inside a captured graph where the step's lengths cannot be read back (no
+ * counterpart in the reference: its prefill plans on the host). Inputs are
+ * device int64 arrays of num_seqs entries: seq_rows (block-table row of each
+ * sequence), cached_len and query_len (chunk tokens; the chunks' rows follow
+ * each other in the query / key / value tensors, total_query_rows of them).
+ * Writes seqs [num_seqs][4] int64 (row, cached, first chunk row, chunk
+ * tokens) and work_items [work_capacity][4] int32 in sequence order
+ * (ceil(query_len / tokens_per_group) work groups per sequence and kv head;
+ * slots past the last one marked unused, which mv_paged_prefill skips);
+ * launch mv_paged_prefill with num_work_groups = work_capacity.
+ * status (int32[2], device): [0] = sequences whose row, lengths or prefix
+ * table entries (the first ceil(cached_len / block_size) of the row) are
+ * invalid; [1] = work groups, or -1 when the chunks exceed total_query_rows
+ * or the work groups the capacity. Any error leaves every slot unused.
+ */
+int mv_prefill_plan(const int64_t* seq_rows, const int64_t* cached_len, const int64_t* query_len,
+                    int32_t num_seqs, int64_t total_query_rows, const void* block_table,
+                    int32_t bt_is_i64, int64_t bt_stride, int32_t bt_rows, int32_t max_blocks,
+                    int32_t block_size, int64_t num_blocks, int32_t tokens_per_group,
+                    int32_t num_kv_heads, int64_t* seqs, int32_t* work_items,
+                    int32_t work_capacity, int32_t* status, void* stream);
 
 #ifdef __cplusplus
 }

@@ -123,6 +123,37 @@ __global__ __launch_bounds__(kCheckTile) void slots_check_kernel(const int64_t* 
   }
 }
 
+// The fused decode + KV write (mv_paged_decode_write) is exact when every
+// slot is -1 or the table position of its own sequence's last attended
+// token kv_len - 1 (the block manager's layout). One work group counts the
+// sequences for which that does not hold (including those with a kv_len or
+// table entry that cannot address such a position) into status[0].
+constexpr int kWriteCheckThreads = 256;
+template <typename KV, typename BT>
+__global__ __launch_bounds__(kWriteCheckThreads) void decode_write_check_kernel(
+    const int64_t* slots, const BT* bt, int64_t bt_stride, const KV* kv_len, int32_t num_seqs,
+    int32_t max_blocks, int32_t bs_log2, int32_t* status) {
+  __shared__ int s_bad;
+  if (threadIdx.x == 0) s_bad = 0;
+  __syncthreads();
+  int bad = 0;
+  for (int b = threadIdx.x; b < num_seqs; b += kWriteCheckThreads) {
+    const int64_t s = slots[b];
+    if (s == -1) continue;
+    const int64_t kv = static_cast<int64_t>(kv_len[b]);
+    const int64_t e = (kv - 1) >> bs_log2;
+    bool ok = kv >= 1 && e < max_blocks;
+    if (ok) {
+      const int64_t blk = static_cast<int64_t>(bt[b * bt_stride + e]);
+      ok = blk >= 0 && s == (blk << bs_log2) + ((kv - 1) & ((int64_t(1) << bs_log2) - 1));
+    }
+    bad += !ok;
+  }
+  if (bad) atomicAdd(&s_bad, bad);
+  __syncthreads();
+  if (threadIdx.x == 0) status[0] = s_bad;
+}
+
 __global__ void zero_status(int32_t* status, int n) {
   if (threadIdx.x < n) status[threadIdx.x] = 0;
 }
@@ -216,4 +247,42 @@ extern "C" int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens
     slots_check_kernel<<<grid, kCheckTile, 0, s>>>(slot_mapping, num_tokens, total_slots, status);
   }
   return check_launch("mv_kv_slots_check");
+}
+
+extern "C" int mv_decode_write_check(const int64_t* slot_mapping, const void* block_table,
+                                     int32_t bt_is_i64, int64_t bt_stride, const void* kv_len,
+                                     int32_t kv_len_is_i64, int32_t num_seqs, int32_t max_blocks,
+                                     int32_t block_size, int32_t* status, void* stream) {
+  using namespace mv;
+  if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_write_check: null status");
+  if (num_seqs < 0 || max_blocks < 0)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_write_check: negative size");
+  if (!is_pow2(block_size))
+    return fail(MV_ERR_UNSUPPORTED, "mv_decode_write_check: block_size %d is not a power of 2",
+                block_size);
+  if (num_seqs > 0 && (!slot_mapping || !kv_len || (max_blocks > 0 && !block_table)))
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_write_check: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int bl = ilog2_exact(block_size);
+  const int mb = block_table ? max_blocks : 0;
+  if (kv_len_is_i64) {
+    if (bt_is_i64)
+      decode_write_check_kernel<int64_t, int64_t><<<1, kWriteCheckThreads, 0, s>>>(
+          slot_mapping, static_cast<const int64_t*>(block_table), bt_stride,
+          static_cast<const int64_t*>(kv_len), num_seqs, mb, bl, status);
+    else
+      decode_write_check_kernel<int64_t, int32_t><<<1, kWriteCheckThreads, 0, s>>>(
+          slot_mapping, static_cast<const int32_t*>(block_table), bt_stride,
+          static_cast<const int64_t*>(kv_len), num_seqs, mb, bl, status);
+  } else {
+    if (bt_is_i64)
+      decode_write_check_kernel<int32_t, int64_t><<<1, kWriteCheckThreads, 0, s>>>(
+          slot_mapping, static_cast<const int64_t*>(block_table), bt_stride,
+          static_cast<const int32_t*>(kv_len), num_seqs, mb, bl, status);
+    else
+      decode_write_check_kernel<int32_t, int32_t><<<1, kWriteCheckThreads, 0, s>>>(
+          slot_mapping, static_cast<const int32_t*>(block_table), bt_stride,
+          static_cast<const int32_t*>(kv_len), num_seqs, mb, bl, status);
+  }
+  return check_launch("mv_decode_write_check");
 }

@@ -31,3 +31,14 @@ int check_launch(const char* what) {
 extern "C" int mv_abi_version(void) { return MVATTN_ABI_VERSION; }
 
 extern "C" const char* mv_last_error(void) { return g_last_error; }
+
+extern "C" int mv_stream_capture_id(void* stream, uint64_t* capture_id) {
+  if (!capture_id) return mv::fail(MV_ERR_INVALID_ARGUMENT, "mv_stream_capture_id: null capture_id");
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  const hipError_t err = hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &status, &id);
+  if (err != hipSuccess)
+    return mv::fail(MV_ERR_HIP, "mv_stream_capture_id: %s", hipGetErrorString(err));
+  *capture_id = status == hipStreamCaptureStatusActive ? static_cast<uint64_t>(id) : 0;
+  return MV_OK;
+}

@@ -1046,8 +1046,11 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const bool listed = used_groups == num_groups && n_ids <= a.ids_cap &&
                       n_ids <= INT_MAX - kIdsPerPass &&
                       (!fixed || part_tokens <= a.fixed_part_tokens);
-  if (fixed) {
-    for (int64_t slot = used_groups + tid; slot < a.work_cap; slot += kPlanThreads) {
+  // A plan whose id lists do not fit is unusable: every slot is marked
+  // unused, so a launch of it does nothing (no piece runs without its ids).
+  __syncthreads();  // the entries of steps 3-4 are written
+  if (fixed || !listed) {
+    for (int64_t slot = listed ? used_groups + tid : tid; slot < a.work_cap; slot += kPlanThreads) {
       int4* w = reinterpret_cast<int4*>(a.work + 8 * slot);
       w[0] = make_int4(-1, 0, 0, 0);
       w[1] = make_int4(0, 0, 0, 0);

@@ -160,6 +160,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   const int set = Tr::kSets == 1 ? 0 : wave / Tr::kRowWaves;       // sub-tiles set * U .. of every stage
 
   const int4 w = reinterpret_cast<const int4*>(a.work)[blockIdx.x];
+  if (w.x < 0) return;  // an unused slot of a launch of fixed size
   const int seq = w.x, h = w.y, tok0 = w.z, ntok = w.w;
   const int64_t row = a.seqs[4 * seq];
   const int cached = static_cast<int>(a.seqs[4 * seq + 1]);
@@ -631,6 +632,119 @@ int launch_prefill_d(const PrefillArgs& a, int d, int n_rep, int groups, bool bt
 
 }  // namespace
 }  // namespace mv
+
+namespace mv {
+namespace {
+
+// Device-side prefill plan for a launch of fixed size (graph capture, where
+// the lengths cannot be read back): one work group validates each
+// sequence's prefix entries, scans the chunk lengths into chunk rows, and
+// writes the work list in sequence order, every slot past the last work
+// group marked unused. status[0] = sequences with a bad row, length or
+// prefix table entry; status[1] = work groups (or -1 when they exceed the
+// capacity, or the chunk lengths the query rows: then every slot is unused).
+constexpr int kPfPlanThreads = 256;
+template <typename BT>
+__global__ __launch_bounds__(kPfPlanThreads) void prefill_plan_kernel(
+    const int64_t* rows, const int64_t* cached, const int64_t* qlen, int32_t num_seqs,
+    int64_t total_rows, const BT* bt, int64_t bt_stride, int32_t bt_rows, int32_t max_blocks,
+    int32_t bs_log2, int64_t num_blocks, int32_t tpg, int32_t num_kv_heads, int64_t* seqs,
+    int32_t* work, int32_t work_cap, int32_t* status) {
+  __shared__ int s_bad;
+  __shared__ int64_t s_rows_total, s_groups;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    s_bad = 0;
+    s_rows_total = 0;
+    s_groups = 0;
+  }
+  __syncthreads();
+  // 1. validate, sequence by sequence (prefill batches hold few sequences)
+  for (int i = 0; i < num_seqs; ++i) {
+    const int64_t r = rows[i], c = cached[i], q = qlen[i];
+    const int64_t need = (c + (int64_t(1) << bs_log2) - 1) >> bs_log2;
+    const bool shape_ok = r >= 0 && r < bt_rows && c >= 0 && q >= 0 && c <= INT_MAX / 2 &&
+                          q <= INT_MAX / 2 && need <= max_blocks;
+    int bad = 0;
+    if (shape_ok) {
+      for (int64_t j = tid; j < need; j += kPfPlanThreads) {
+        const int64_t blk = static_cast<int64_t>(bt[r * bt_stride + j]);
+        bad |= blk < 0 || blk >= num_blocks;
+      }
+    }
+    bad = __syncthreads_or(bad);
+    if (tid == 0) {
+      if (!shape_ok || bad) ++s_bad;
+      s_rows_total += q >= 0 ? q : 0;
+      s_groups += q > 0 ? ((q + tpg - 1) / tpg) * num_kv_heads : 0;
+    }
+    __syncthreads();
+  }
+  const bool ok = s_bad == 0 && s_rows_total <= total_rows && s_groups <= work_cap;
+  // 2. per-sequence rows and work groups (thread 0: a short sequential scan)
+  if (tid == 0 && ok) {
+    int64_t start = 0, slot = 0;
+    for (int i = 0; i < num_seqs; ++i) {
+      const int64_t q = qlen[i];
+      seqs[4 * i] = rows[i];
+      seqs[4 * i + 1] = cached[i];
+      seqs[4 * i + 2] = start;
+      seqs[4 * i + 3] = q;
+      for (int64_t t0 = 0; t0 < q; t0 += tpg) {
+        const int nt = static_cast<int>(q - t0 < tpg ? q - t0 : tpg);
+        for (int h = 0; h < num_kv_heads; ++h, ++slot)
+          reinterpret_cast<int4*>(work)[slot] = make_int4(i, h, static_cast<int>(t0), nt);
+      }
+      start += q;
+    }
+  }
+  // 3. the unused slots (all of them for an unusable plan)
+  const int64_t used = ok ? s_groups : 0;
+  for (int64_t slot = used + tid; slot < work_cap; slot += kPfPlanThreads)
+    reinterpret_cast<int4*>(work)[slot] = make_int4(-1, 0, 0, 0);
+  if (tid == 0) {
+    status[0] = s_bad;
+    status[1] = ok ? static_cast<int32_t>(s_groups) : -1;
+  }
+}
+
+}  // namespace
+}  // namespace mv
+
+extern "C" int mv_prefill_plan(const int64_t* seq_rows, const int64_t* cached_len,
+                               const int64_t* query_len, int32_t num_seqs, int64_t total_query_rows,
+                               const void* block_table, int32_t bt_is_i64, int64_t bt_stride,
+                               int32_t bt_rows, int32_t max_blocks, int32_t block_size,
+                               int64_t num_blocks, int32_t tokens_per_group, int32_t num_kv_heads,
+                               int64_t* seqs, int32_t* work_items, int32_t work_capacity,
+                               int32_t* status, void* stream) {
+  using namespace mv;
+  if (!status || !work_items || (num_seqs > 0 && (!seq_rows || !cached_len || !query_len || !seqs)))
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_prefill_plan: null pointer");
+  if (num_seqs < 0 || work_capacity < 0 || tokens_per_group <= 0 || num_kv_heads <= 0 ||
+      total_query_rows < 0 || bt_rows < 0 || max_blocks < 0)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_prefill_plan: bad sizes");
+  if (!is_pow2(block_size))
+    return fail(MV_ERR_UNSUPPORTED, "mv_prefill_plan: block_size %d is not a power of 2", block_size);
+  if (bt_rows > 0 && max_blocks > 0 && !block_table)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_prefill_plan: null block table");
+  if (reinterpret_cast<uintptr_t>(work_items) % 16)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_prefill_plan: work_items not 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int bl = ilog2_exact(block_size);
+  const int rows_ok = block_table ? bt_rows : 0;
+  if (bt_is_i64)
+    prefill_plan_kernel<int64_t><<<1, kPfPlanThreads, 0, s>>>(
+        seq_rows, cached_len, query_len, num_seqs, total_query_rows,
+        static_cast<const int64_t*>(block_table), bt_stride, rows_ok, max_blocks, bl, num_blocks,
+        tokens_per_group, num_kv_heads, seqs, work_items, work_capacity, status);
+  else
+    prefill_plan_kernel<int32_t><<<1, kPfPlanThreads, 0, s>>>(
+        seq_rows, cached_len, query_len, num_seqs, total_query_rows,
+        static_cast<const int32_t*>(block_table), bt_stride, rows_ok, max_blocks, bl, num_blocks,
+        tokens_per_group, num_kv_heads, seqs, work_items, work_capacity, status);
+  return check_launch("mv_prefill_plan");
+}
 
 extern "C" int mv_prefill_tokens_per_group(int32_t num_q_heads, int32_t num_kv_heads,
                                            int32_t head_dim, int32_t dtype) {

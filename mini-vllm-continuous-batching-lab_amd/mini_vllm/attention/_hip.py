@@ -14,7 +14,7 @@ import threading
 
 import torch  # noqa: F401  (must be loaded before the kernel library)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MV_OK = 0
 MV_ERR_INVALID_ARGUMENT = -1
@@ -49,6 +49,7 @@ _F = ctypes.c_float
 SIGNATURES = {
     "mv_abi_version": (ctypes.c_int, []),
     "mv_last_error": (ctypes.c_char_p, []),
+    "mv_stream_capture_id": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64)]),
     "mv_decode_chunk_tokens": (ctypes.c_int, [_I32, _I32]),
     "mv_decode_groups_per_cu": (ctypes.c_int, [_I32, _I32]),
     "mv_kv_cache_write": (ctypes.c_int, [
@@ -59,6 +60,11 @@ SIGNATURES = {
         _I64, _I32, _P,            # num_blocks, dtype, stream
     ]),
     "mv_kv_slots_check": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "mv_decode_write_check": (ctypes.c_int, [
+        _P, _P, _I32, _I64,        # slot_mapping, block_table, bt_is_i64, bt_stride
+        _P, _I32, _I32, _I32,      # kv_len, kv_len_is_i64, num_seqs, max_blocks
+        _I32, _P, _P,              # block_size, status, stream
+    ]),
     "mv_decode_plan": (ctypes.c_int, [
         _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride
         _I32, _I32, _I32, _I64,    # num_seqs, max_blocks, block_size, num_blocks
@@ -110,6 +116,12 @@ SIGNATURES = {
         _P, _SZ, _P,               # workspace, workspace_bytes, stream
     ]),
     "mv_prefill_tokens_per_group": (ctypes.c_int, [_I32, _I32, _I32, _I32]),
+    "mv_prefill_plan": (ctypes.c_int, [
+        _P, _P, _P, _I32, _I64,    # seq_rows, cached_len, query_len, num_seqs, total_query_rows
+        _P, _I32, _I64, _I32, _I32,  # block_table, bt_is_i64, bt_stride, bt_rows, max_blocks
+        _I32, _I64, _I32, _I32,    # block_size, num_blocks, tokens_per_group, num_kv_heads
+        _P, _P, _I32, _P, _P,      # seqs, work_items, work_capacity, status, stream
+    ]),
     "mv_paged_prefill": (ctypes.c_int, [
         _P, _I64, _I64,            # query, strides
         _P, _I64, _I64,            # key, strides

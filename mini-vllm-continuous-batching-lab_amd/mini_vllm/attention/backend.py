@@ -12,8 +12,12 @@ The model runner talks to attention only through this ABC, created by
 This package implements one backend, the HIP backend for gfx950
 (``AttentionBackendGPU``). ``"hip"`` is its name and ``"triton"`` — the name
 the reference's configs and tests use for the GPU backend — selects the same
-class. There is no fallback: an unknown name raises ``ValueError`` and a
-missing GPU or kernel library raises ``RuntimeError`` at creation.
+class. ``"reference"`` / ``"ref"`` keep the reference's meaning: the PyTorch
+test backend ``AttentionBackendRef``, imported lazily from the sibling module
+``paged_attention_ref`` that the reference tree provides (this package does
+not ship that module; where it is absent the import error propagates).
+There is no fallback: an unknown name raises ``ValueError`` and a missing GPU
+or kernel library raises ``RuntimeError`` at creation.
 """
 
 from __future__ import annotations
@@ -78,14 +82,20 @@ class AttentionBackend(ABC):
 
     @staticmethod
     def create(config: "ModelConfig", backend: str = "hip") -> "AttentionBackend":
-        """Backend factory (reference backend.py:95-113)."""
+        """Backend factory (reference backend.py:95-118).
+
+        ``"reference"`` / ``"ref"``: the reference's PyTorch backend, from the
+        module ``paged_attention_ref`` beside this one (reference :106-108;
+        ``Config.attention_backend`` defaults to it, reference config.py:76).
+        ``"hip"`` / ``"triton"``: the HIP backend. Anything else:
+        ``ValueError`` (reference :117-118).
+        """
+        if backend in REFERENCE_BACKEND_NAMES:
+            from .paged_attention_ref import AttentionBackendRef  # the reference tree's module
+
+            return AttentionBackendRef(config)
         if backend in GPU_BACKEND_NAMES:
             from .paged_attention_gpu import AttentionBackendGPU
 
             return AttentionBackendGPU(config)
-        if backend in REFERENCE_BACKEND_NAMES:
-            raise ValueError(
-                f"AttentionBackend {backend!r} is the upstream PyTorch test backend; "
-                f"this package ships only the HIP backend ({', '.join(GPU_BACKEND_NAMES)})"
-            )
         raise ValueError(f"Unknown AttentionBackend: {backend!r}")

@@ -46,6 +46,7 @@ __all__ = [
     "DecodePlan",
     "check_deferred",
     "clear_deferred",
+    "last_capture_id",
     "gather_prefix_kv",
     "hip_cache_write",
     "hip_decode_attention",
@@ -112,15 +113,30 @@ def _cache_put(name: str, tensors: Sequence[torch.Tensor], extra: tuple, value) 
     setattr(_state, name, (_SeenTensors(tensors, extra), value))
 
 
+# Decode merge workspaces, per device: the current one and every one it
+# replaced. A captured graph holds the raw address of the buffer it was
+# captured with, so a workspace is never released once a kernel has used it:
+# a larger batch gets a new buffer and the old one stays allocated for the
+# graphs that still point at it (its replays keep writing their partials
+# there, never into memory that has become another tensor's).
+_WORKSPACES: dict = {}
+_RETIRED_WORKSPACES: List[torch.Tensor] = []
+_WORKSPACE_LOCK = threading.Lock()
+
+
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Grow-only per-device fp32 partial-result buffer of the decode reduce."""
-    cache = getattr(_state, "workspace", None)
-    if cache is None:
-        cache = _state.workspace = {}
-    ws = cache.get(device)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        cache[device] = ws
+    """Grow-only, never-freed per-device fp32 partial buffer of the decode
+    merge."""
+    ws = _WORKSPACES.get(device)
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
+    with _WORKSPACE_LOCK:
+        ws = _WORKSPACES.get(device)
+        if ws is None or ws.numel() < nbytes:
+            if ws is not None:
+                _RETIRED_WORKSPACES.append(ws)
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _WORKSPACES[device] = ws
     return ws
 
 
@@ -130,39 +146,69 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 # While a stream is being captured into a HIP graph nothing may wait for the
 # device, so the slot, position and plan checks cannot read their status
 # words back. They are captured like every other kernel; each records its
-# status tensor here, and check_deferred() reads them after a replay.
+# status tensor under the capture's id, and check_deferred() reads them
+# after a replay. The per-step caches of plans and checks are keyed by the
+# capture id too: a second capture over the same (unmodified) metadata
+# tensors records its own plan and check kernels instead of reusing the
+# first graph's buffers.
 # ----------------------------------------------------------------------------
 
 
-def _capturing() -> bool:
-    return torch.cuda.is_current_stream_capturing()
+def _capture_id(device: torch.device) -> int:
+    """Id of the graph capture the current stream of ``device`` is in (HIP's
+    capture id, nonzero), or 0 when it is not being captured."""
+    if not torch.cuda.is_current_stream_capturing():
+        return 0
+    cid = ctypes.c_uint64(0)
+    _hip.check(_hip.load().mv_stream_capture_id(_stream(device), ctypes.byref(cid)),
+               "mv_stream_capture_id")
+    return cid.value or -1  # capturing: never 0
 
 
-def _defer(raise_fn, status: torch.Tensor) -> None:
+def _defer(capture: int, raise_fn, status: torch.Tensor) -> None:
     deferred = getattr(_state, "deferred", None)
     if deferred is None:
-        deferred = _state.deferred = []
-    deferred.append((raise_fn, status))
+        deferred = _state.deferred = {}
+    deferred.setdefault(capture, []).append((raise_fn, status))
+    _state.last_capture = capture
 
 
-def check_deferred() -> None:
+def last_capture_id() -> int:
+    """Id of the most recent graph capture (on this thread) that recorded
+    deferred checks, 0 if none: read it right after a capture to check that
+    graph's replays by id when several graphs are alive."""
+    return getattr(_state, "last_capture", 0)
+
+
+def check_deferred(capture_id: Optional[int] = None) -> None:
     """Raise the first error found by the checks captured into a graph.
 
     Call after replaying a captured step (it synchronises once): the same
     exceptions as the eager calls (``IndexError`` / ``AssertionError`` for
     slots, ``IndexError`` for positions, ``ValueError`` / ``IndexError`` /
     ``RuntimeError`` for the decode metadata) describe the data of the last
-    replay. The kernels themselves skip what the checks report (slots and
-    block ids outside the pool, sequences without a valid length), so a bad
-    replay produces wrong rows, never an out-of-bounds access.
+    replay. Only the checks of one capture are read: ``capture_id``
+    (``last_capture_id()`` taken right after that capture), by default the
+    most recent capture. The kernels themselves skip what the checks report
+    (slots and block ids outside the pool, sequences without a valid
+    length), so a bad replay produces wrong rows, never an out-of-bounds
+    access.
     """
-    for raise_fn, status in getattr(_state, "deferred", None) or []:
+    deferred = getattr(_state, "deferred", None) or {}
+    cid = last_capture_id() if capture_id is None else capture_id
+    for raise_fn, status in deferred.get(cid, ()):
         raise_fn(status.tolist())
 
 
-def clear_deferred() -> None:
-    """Forget the recorded checks (e.g. when a captured graph is dropped)."""
-    _state.deferred = []
+def clear_deferred(capture_id: Optional[int] = None) -> None:
+    """Forget the recorded checks of one capture (e.g. when its graph is
+    dropped), or of every capture."""
+    deferred = getattr(_state, "deferred", None) or {}
+    if capture_id is None:
+        _state.deferred = {}
+        _state.last_capture = 0
+    else:
+        deferred.pop(capture_id, None)
 
 
 # ============================================================================
@@ -171,24 +217,24 @@ def clear_deferred() -> None:
 
 
 def _check_slots(slot_mapping: torch.Tensor, total_slots: int,
-                 capturing: Optional[bool] = None) -> None:
+                 capture: Optional[int] = None) -> None:
     """Raise like the reference for out-of-range or duplicate slots.
 
     Out of range (``< -1`` or ``>= total_slots``): ``IndexError`` with
     "out of range" (reference cache_write.py:61-66). Duplicates among the
     non-(-1) slots: ``AssertionError`` with "Duplicate" (reference
     paged_attention_gpu.py:126-135). Both checks run in one device kernel.
-    ``capturing``: whether the current stream is being captured, when the
-    caller already knows.
+    ``capture``: the current stream's capture id (0: not capturing), when
+    the caller already knows it.
     """
-    if capturing is None:
-        capturing = _capturing()
-    name = "slots_graph" if capturing else "slots"
-    extra = (total_slots,)
+    device = slot_mapping.device
+    if capture is None:
+        capture = _capture_id(device)
+    name = "slots_graph" if capture else "slots"
+    extra = (total_slots, capture)
     if _cache_get(name, (slot_mapping,), extra) is not None:
         return
     lib = _hip.load()
-    device = slot_mapping.device
     status = torch.empty(2, dtype=torch.int32, device=device)
     _hip.check(
         lib.mv_kv_slots_check(
@@ -210,8 +256,8 @@ def _check_slots(slot_mapping: torch.Tensor, total_slots: int,
                 f"The HIP cache write forbids duplicate slots."
             )
 
-    if capturing:
-        _defer(raise_slots, status)
+    if capture:
+        _defer(capture, raise_slots, status)
     else:
         raise_slots(status.tolist())
     _cache_put(name, (slot_mapping,), extra, True)
@@ -315,6 +361,69 @@ def _groups_per_cu(device: torch.device, head_dim: int, dtype: torch.dtype) -> T
     return split
 
 
+def _decode_metadata(block_table: torch.Tensor, kv_len_after: torch.Tensor,
+                     device: torch.device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Block table ``[B, max_blocks]`` and kv lengths ``[B]`` on ``device``
+    as int32 or int64 with contiguous rows (copies only where needed)."""
+    bt = block_table
+    if bt.dim() != 2:
+        bt = bt.reshape(kv_len_after.shape[0], -1)
+    if bt.device != device:
+        bt = bt.to(device)
+    if bt.dtype not in (torch.int32, torch.int64):
+        bt = bt.to(torch.int64)
+    if bt.numel() and bt.stride(1) != 1:
+        bt = bt.contiguous()
+    kv = kv_len_after
+    if kv.device != device:
+        kv = kv.to(device)
+    if kv.dtype not in (torch.int32, torch.int64):
+        kv = kv.to(torch.int64)
+    return bt, kv.contiguous()
+
+
+def _fused_write_ok(slot_mapping: torch.Tensor, block_table: torch.Tensor,
+                    kv_len_after: torch.Tensor, block_size: int, device: torch.device,
+                    capture: int) -> bool:
+    """Whether the decode with the KV write fused is exact for this batch:
+    every slot is -1 or the table position of its own sequence's token
+    ``kv_len_after - 1`` (``mv_decode_write_check``), as the block manager
+    lays them out. Eager: one device check per distinct (unmodified) slots /
+    table / lengths, read back. While capturing: True, with the check
+    recorded for ``check_deferred()`` (``AssertionError``)."""
+    name = "fused_graph" if capture else "fused"
+    extra = (block_size, device, capture)
+    hit = _cache_get(name, (slot_mapping, block_table, kv_len_after), extra)
+    if hit is not None:
+        return hit
+    bt, kv = _decode_metadata(block_table, kv_len_after, device)
+    status = torch.empty(1, dtype=torch.int32, device=device)
+    _hip.check(
+        _hip.load().mv_decode_write_check(
+            _ptr(slot_mapping), _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
+            bt.stride(0) if bt.dim() == 2 else 0, _ptr(kv), int(kv.dtype == torch.int64),
+            kv.shape[0], bt.shape[1] if bt.dim() == 2 else 0, block_size, _ptr(status),
+            _stream(device),
+        ),
+        "mv_decode_write_check",
+    )
+
+    def raise_fused(st) -> None:
+        if st[0]:
+            raise AssertionError(
+                f"decode with the KV write fused: {st[0]} slot(s) are not their sequence's "
+                f"position kv_len_after - 1; write the cache and decode in two calls"
+            )
+
+    if capture:
+        _defer(capture, raise_fused, status)
+        ok = True
+    else:
+        ok = status.tolist()[0] == 0
+    _cache_put(name, (slot_mapping, block_table, kv_len_after), extra, ok)
+    return ok
+
+
 def plan_decode(
     block_table: torch.Tensor,
     kv_len_after: torch.Tensor,
@@ -324,7 +433,7 @@ def plan_decode(
     head_dim: int,
     dtype: torch.dtype,
     num_kv_heads: int,
-    capturing: Optional[bool] = None,
+    capture: Optional[int] = None,
 ) -> DecodePlan:
     """Validate decode metadata, pick the partition size, build the work list.
 
@@ -340,38 +449,24 @@ def plan_decode(
     While the current stream is being captured into a graph the plan
     cannot be read back: it is enqueued for a launch of fixed size
     (``mv_decode_graph_bounds``), and its checks raise from
-    ``check_deferred()`` after a replay instead. ``capturing``: whether the
-    current stream is being captured, when the caller already knows.
+    ``check_deferred()`` after a replay instead. ``capture``: the current
+    stream's capture id (0: not capturing), when the caller already knows it.
     """
     lib = _hip.load()
     split = _groups_per_cu(device, head_dim, dtype)
-    if capturing is None:
-        capturing = _capturing()
-    name = "plan_graph" if capturing else "plan"
-    extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads, split)
+    if capture is None:
+        capture = _capture_id(device)
+    name = "plan_graph" if capture else "plan"
+    extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads, split, capture)
     cached = _cache_get(name, (block_table, kv_len_after), extra)
     if cached is not None:
         return cached
-    bt = block_table
-    if bt.dim() != 2:
-        bt = bt.reshape(kv_len_after.shape[0], -1)
-    if bt.device != device:
-        bt = bt.to(device)
-    if bt.dtype not in (torch.int32, torch.int64):
-        bt = bt.to(torch.int64)
-    if bt.numel() and bt.stride(1) != 1:
-        bt = bt.contiguous()
-    kv = kv_len_after
-    if kv.device != device:
-        kv = kv.to(device)
-    if kv.dtype not in (torch.int32, torch.int64):
-        kv = kv.to(torch.int64)
-    kv = kv.contiguous()
+    bt, kv = _decode_metadata(block_table, kv_len_after, device)
 
     num_seqs = kv.shape[0]
     max_blocks = bt.shape[1] if bt.dim() == 2 else 0
     fixed = 0
-    if capturing and num_seqs > 0 and max_blocks > 0:
+    if capture and num_seqs > 0 and max_blocks > 0:
         bounds = (ctypes.c_int64 * 3)()
         _hip.check(lib.mv_decode_graph_bounds(num_seqs, max_blocks, block_size, num_kv_heads,
                                               *split, bounds), "mv_decode_graph_bounds")
@@ -421,7 +516,7 @@ def plan_decode(
             )
 
     if fixed:
-        _defer(raise_plan, status)
+        _defer(capture, raise_plan, status)
         plan = DecodePlan(work, block_ids, counters, cap, fixed_parts, fixed)
     else:
         st = status.tolist()
@@ -461,10 +556,14 @@ def hip_decode_attention(
     With ``new_key`` / ``new_value`` ``[total_decode, num_kv_heads,
     head_dim]`` and ``slot_mapping`` ``[total_decode]`` the call also does
     the step's KV write of those rows (``triton_cache_write``, with its
-    checks) in the same launch: pool and output are bit-identical to
-    ``hip_cache_write`` followed by this call without them, provided no
-    slot lies in a block another sequence of the batch attends (what the
-    block manager guarantees).
+    checks): pool and output are those of ``hip_cache_write`` followed by
+    this call without them. It is one launch when every slot is -1 or its
+    own sequence's position ``kv_len_after - 1`` and no other sequence of
+    the batch attends that slot -- the block manager's layout (a
+    sequence's last block is its own). A batch whose slots are elsewhere is
+    detected on the device and runs as the two calls; inside a captured
+    graph it is reported by ``check_deferred()`` (``AssertionError``)
+    instead. The cross-sequence condition is not checked.
     """
     # (The per-call checks read each attribute once: this wrapper runs once
     # per layer, and its host time exceeds the kernel's when it does not.)
@@ -492,9 +591,9 @@ def hip_decode_attention(
 
     device = query.device
     num_blocks = kshape[0]
-    capturing = _capturing()
+    capture = _capture_id(device)
     plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
-                       dtype, num_kv_heads, capturing=capturing)
+                       dtype, num_kv_heads, capture=capture)
     output = torch.empty_like(query, memory_format=torch.contiguous_format)
     if total_decode == 0 or plan.num_groups == 0:
         return output
@@ -520,7 +619,12 @@ def hip_decode_attention(
         if slot_mapping.dtype != torch.int64:
             slot_mapping = slot_mapping.to(torch.int64)
         slot_mapping = slot_mapping.contiguous()
-        _check_slots(slot_mapping, num_blocks * block_size, capturing=capturing)
+        _check_slots(slot_mapping, num_blocks * block_size, capture=capture)
+        if not _fused_write_ok(slot_mapping, block_table, kv_len_after, block_size, device,
+                               capture):
+            hip_cache_write(new_key, new_value, key_cache, value_cache, slot_mapping, block_size)
+            return hip_decode_attention(query, key_cache, value_cache, block_table, kv_len_after,
+                                        block_size)
         nk, nv = _aligned_rows(new_key), _aligned_rows(new_value)
         _hip.check(
             lib.mv_paged_decode_write(
@@ -568,13 +672,13 @@ def _check_positions(positions: torch.Tensor, max_positions: int) -> None:
     reference's lookup ``self._cos[positions]`` raises
     (mini_vllm/model/rotary.py:64-65). One device check per distinct
     positions tensor (the layers of a step share it)."""
-    capturing = _capturing()
-    name = "positions_graph" if capturing else "positions"
-    extra = (max_positions,)
+    device = positions.device
+    capture = _capture_id(device)
+    name = "positions_graph" if capture else "positions"
+    extra = (max_positions, capture)
     if _cache_get(name, (positions,), extra) is not None:
         return
     lib = _hip.load()
-    device = positions.device
     status = torch.empty(1, dtype=torch.int32, device=device)
     _hip.check(
         lib.mv_positions_check(_ptr(positions), positions.numel(), max_positions, _ptr(status),
@@ -586,8 +690,8 @@ def _check_positions(positions: torch.Tensor, max_positions: int) -> None:
         if st[0]:
             raise IndexError(f"{st[0]} position(s) outside the rotary tables [0, {max_positions})")
 
-    if capturing:
-        _defer(raise_positions, status)
+    if capture:
+        _defer(capture, raise_positions, status)
     else:
         raise_positions(status.tolist())
     _cache_put(name, (positions,), extra, True)
@@ -865,6 +969,96 @@ def _aligned_rows(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
+def _device_i64(x, n: int, device: torch.device) -> torch.Tensor:
+    """``x`` (a tensor or a sequence of ints, n entries) as a contiguous
+    int64 tensor on ``device``, made by device operations only (usable while
+    capturing: a host sequence becomes fill kernels, not a copy)."""
+    if isinstance(x, torch.Tensor):
+        if x.device != device:
+            if torch.cuda.is_current_stream_capturing():
+                x = x.tolist()  # a host tensor: its values are known here
+            else:
+                return x.to(device=device, dtype=torch.int64).contiguous()
+        else:
+            return x.to(torch.int64).contiguous()
+    vals = [int(v) for v in x]
+    assert len(vals) == n
+    if vals == list(range(n)):
+        return torch.arange(n, dtype=torch.int64, device=device)
+    t = torch.empty(n, dtype=torch.int64, device=device)
+    for i, v in enumerate(vals):
+        t[i].fill_(v)
+    return t
+
+
+def _prefill_device_plan(block_table, seq_indices, cached_len_before, query_len, total_rows,
+                         block_size, num_blocks, num_q_heads, num_kv_heads, head_dim, dtype,
+                         device, capture):
+    """Prefill work list built on the device (``mv_prefill_plan``) for a
+    launch of fixed size: ``(bt, seqs, work, capacity)``. Used while
+    capturing, where the step's lengths cannot be read back; its checks
+    raise from ``check_deferred()`` (``IndexError`` "insufficient" for a
+    table that cannot cover a prefix, ``ValueError`` for chunk lengths that
+    exceed the query rows). Cached per capture and (unmodified) metadata."""
+    lib = _hip.load()
+    n = len(seq_indices)
+    tensors = tuple(x for x in (block_table, cached_len_before, query_len)
+                    if isinstance(x, torch.Tensor))
+    extra = (tuple(int(r) for r in seq_indices), n, total_rows, block_size, num_blocks,
+             num_q_heads, num_kv_heads, head_dim, dtype, device, capture,
+             None if isinstance(cached_len_before, torch.Tensor) else tuple(cached_len_before),
+             None if isinstance(query_len, torch.Tensor) else tuple(query_len))
+    hit = _cache_get("prefill_graph", tensors, extra)
+    if hit is not None:
+        return hit
+    tpg = lib.mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim,
+                                          _hip.MV_DTYPE[dtype])
+    if tpg == 0:
+        raise RuntimeError(
+            f"prefill: {num_q_heads} query heads over {num_kv_heads} kv heads not supported"
+        )
+    bt = block_table
+    if bt.dim() != 2:
+        bt = bt.reshape(-1, bt.shape[-1] if bt.dim() else 0)
+    if bt.dtype not in (torch.int32, torch.int64):
+        bt = bt.to(torch.int64)
+    if bt.numel() and bt.stride(1) != 1:
+        bt = bt.contiguous()
+    rows = _device_i64(list(seq_indices), n, device)
+    cached = _device_i64(cached_len_before, n, device)
+    qlen = _device_i64(query_len, n, device)
+    cap = (-(-total_rows // tpg) + n) * num_kv_heads
+    seqs = torch.empty(max(4 * n, 4), dtype=torch.int64, device=device)
+    work = torch.empty(4 * max(cap, 1), dtype=torch.int32, device=device)
+    status = torch.empty(2, dtype=torch.int32, device=device)
+    _hip.check(
+        lib.mv_prefill_plan(
+            _ptr(rows), _ptr(cached), _ptr(qlen), n, total_rows,
+            _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
+            bt.stride(0) if bt.numel() else 0, bt.shape[0] if bt.numel() else 0,
+            bt.shape[1] if bt.numel() else 0, block_size, num_blocks, tpg, num_kv_heads,
+            _ptr(seqs), _ptr(work), cap, _ptr(status), _stream(device),
+        ),
+        "mv_prefill_plan",
+    )
+
+    def raise_prefill(st) -> None:
+        if st[0]:
+            raise IndexError(
+                f"prefill: {st[0]} sequence(s) with a block_table row insufficient to cover "
+                f"their cached prefix (or invalid lengths)"
+            )
+        if st[1] < 0:
+            raise ValueError(
+                f"prefill: the chunk lengths exceed the {total_rows} query rows of the launch"
+            )
+
+    _defer(capture, raise_prefill, status)
+    plan = (bt, seqs, work, cap)
+    _cache_put("prefill_graph", tensors, extra, plan)
+    return plan
+
+
 def hip_prefill_attention(
     query: torch.Tensor,
     key: torch.Tensor,
@@ -873,8 +1067,8 @@ def hip_prefill_attention(
     value_cache: torch.Tensor,
     block_table: torch.Tensor,
     seq_indices: Sequence[int],
-    cached_len_before: Sequence[int],
-    query_len: Sequence[int],
+    cached_len_before,
+    query_len,
     block_size: int,
 ) -> torch.Tensor:
     """Chunked-prefill attention over the paged pool in one HIP launch.
@@ -889,7 +1083,14 @@ def hip_prefill_attention(
     head h reads kv head ``h // n_rep``. Returns ``[sum(query_len), Hq, D]``
     in the query dtype. ``IndexError`` (message "insufficient") for a table
     that cannot cover a prefix, as the reference's gather raises. q / k / v
-    may be column views of one fused QKV output.
+    may be column views of one fused QKV output. ``cached_len_before`` and
+    ``query_len`` are sequences of ints or int tensors.
+
+    While the current stream is being captured into a graph the lengths
+    may stay on the device: the work list is then built by a device kernel
+    for a launch of fixed size (``query.shape[0]`` rows, which the chunks
+    must fill), and the checks raise from ``check_deferred()`` after a
+    replay. ``seq_indices`` is fixed by the capture.
     """
     total_q, num_q_heads, head_dim = query.shape
     num_blocks, num_kv_heads, bs, _ = key_cache.shape
@@ -902,22 +1103,35 @@ def hip_prefill_attention(
     assert key_cache.shape == value_cache.shape
     assert key_cache.is_contiguous() and value_cache.is_contiguous()
     assert query.device.type == "cuda"
-    rows = [int(r) for r in seq_indices]
-    cached = [int(c) for c in cached_len_before]
-    qlens = [int(q) for q in query_len]
-    assert len(rows) == len(cached) == len(qlens)
-    total = sum(qlens)
-    assert total <= total_q and total <= key.shape[0], (
-        f"{total} chunk tokens, query has {total_q} rows, key {key.shape[0]}"
-    )
     device = query.device
     lib = _hip.load()
-    out = torch.empty(total, num_q_heads, head_dim, dtype=query.dtype, device=device)
-    if total == 0:
-        return out
-    bt, meta, work, n_work = _prefill_plan(block_table, rows, cached, qlens, block_size,
-                                           num_blocks, num_q_heads, num_kv_heads, head_dim,
-                                           query.dtype, device)
+    capture = _capture_id(device)
+    rows = [int(r) for r in seq_indices]
+    if capture:
+        assert key.shape[0] >= total_q and value.shape[0] >= total_q
+        out = torch.empty(total_q, num_q_heads, head_dim, dtype=query.dtype, device=device)
+        if total_q == 0 or not rows:
+            return out
+        bt, meta, work, n_work = _prefill_device_plan(
+            block_table, rows, cached_len_before, query_len, total_q, block_size, num_blocks,
+            num_q_heads, num_kv_heads, head_dim, query.dtype, device, capture)
+    else:
+        def host_ints(x):
+            return x.tolist() if isinstance(x, torch.Tensor) else x
+
+        cached = [int(c) for c in host_ints(cached_len_before)]
+        qlens = [int(q) for q in host_ints(query_len)]
+        assert len(rows) == len(cached) == len(qlens)
+        total = sum(qlens)
+        assert total <= total_q and total <= key.shape[0], (
+            f"{total} chunk tokens, query has {total_q} rows, key {key.shape[0]}"
+        )
+        out = torch.empty(total, num_q_heads, head_dim, dtype=query.dtype, device=device)
+        if total == 0:
+            return out
+        bt, meta, work, n_work = _prefill_plan(block_table, rows, cached, qlens, block_size,
+                                               num_blocks, num_q_heads, num_kv_heads, head_dim,
+                                               query.dtype, device)
 
     q = _aligned_rows(query)
     k = _aligned_rows(key)
@@ -1103,17 +1317,19 @@ class AttentionBackendGPU(AttentionBackend):
         """
         if query.shape[0] == 0:
             return query
-        rows: List[int] = []
-        cached: List[int] = []
-        qlens: List[int] = []
-        for group in attn_metadata.groups:
-            if group.attention_type not in ("prefill_gpu", "prefill_ref"):
-                continue
-            rows += [int(s) for s in group.seq_indices]
-            cached += [int(c) for c in group.cached_len_before.tolist()]
-            qlens += [int(q) for q in group.query_len.tolist()]
+        groups = [g for g in attn_metadata.groups
+                  if g.attention_type in ("prefill_gpu", "prefill_ref")]
+        rows: List[int] = [int(s) for g in groups for s in g.seq_indices]
         if not rows:
             return query
+        # Lengths stay tensors: read on the host per step (eager), or planned
+        # on the device inside a captured graph. One group's tensors are
+        # passed as they are, so the layers of a step share one plan.
+        if len(groups) == 1:
+            cached, qlens = groups[0].cached_len_before, groups[0].query_len
+        else:
+            cached = torch.cat([g.cached_len_before.reshape(-1) for g in groups])
+            qlens = torch.cat([g.query_len.reshape(-1) for g in groups])
         return hip_prefill_attention(
             query, key, value, pool.key_caches[layer_idx], pool.value_caches[layer_idx],
             attn_metadata.prefill_block_tables, rows, cached, qlens, pool.block_size,

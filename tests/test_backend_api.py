@@ -25,9 +25,32 @@ def test_unknown_backend_raises_value_error():
         AttentionBackend.create(_cfg(), backend="nonexistent")
 
 
-def test_reference_backend_is_not_shipped():
-    with pytest.raises(ValueError, match="upstream"):
-        AttentionBackend.create(_cfg(), backend="reference")
+def test_reference_backend_not_shipped_here_import_error_propagates():
+    # This package does not ship the reference's PyTorch backend module, so
+    # the reference's lazy import fails loudly (no fallback to the GPU).
+    for name in ("reference", "ref"):
+        with pytest.raises(ImportError, match="paged_attention_ref"):
+            AttentionBackend.create(_cfg(), backend=name)
+
+
+def test_reference_backend_branch_imports_sibling_module(monkeypatch):
+    # Dropped into the reference tree, create("reference") returns the
+    # reference's AttentionBackendRef (reference backend.py:106-108,
+    # tests/test_no_silent_fallback.py:88-94): stand in a module for it.
+    import sys
+    import types
+
+    class AttentionBackendRef:
+        def __init__(self, config):
+            self.config = config
+
+    mod = types.ModuleType("mini_vllm.attention.paged_attention_ref")
+    mod.AttentionBackendRef = AttentionBackendRef
+    monkeypatch.setitem(sys.modules, "mini_vllm.attention.paged_attention_ref", mod)
+    cfg = _cfg()
+    for name in ("reference", "ref"):
+        be = AttentionBackend.create(cfg, backend=name)
+        assert isinstance(be, AttentionBackendRef) and be.config is cfg
 
 
 @pytest.mark.parametrize("hd", [32, 96, 256])

@@ -66,7 +66,7 @@ def test_c_host_compiles_and_links_against_the_header(lib, tmp_path):
         "int main(void) {\n"
         "  void* fns[] = {" + ", ".join(f"(void*){n}" for n in sorted(decl)) + "};\n"
         "  for (unsigned i = 0; i < sizeof fns / sizeof fns[0]; ++i) if (!fns[i]) return 2;\n"
-        "  if (mv_abi_version() != 3) return 3;\n"
+        "  if (mv_abi_version() != MVATTN_ABI_VERSION) return 3;\n"
         "  if (mv_decode_chunk_tokens(64, MV_DTYPE_BF16) != 64) return 4;\n"
         "  if (mv_prefill_tokens_per_group(14, 2, 64, MV_DTYPE_BF16) != 16) return 5;\n"
         "  printf(\"ok %u\\n\", (unsigned)(sizeof fns / sizeof fns[0]));\n"
@@ -91,7 +91,7 @@ def test_every_declared_symbol_is_exported_and_typed(lib):
 
 
 def test_abi_queries(lib):
-    assert lib.mv_abi_version() == _hip.ABI_VERSION == 3
+    assert lib.mv_abi_version() == _hip.ABI_VERSION == 4
     assert lib.mv_decode_chunk_tokens(64, 2) == 64       # 4 waves x one 16-token tile
     assert lib.mv_decode_chunk_tokens(128, 0) == 64
     assert lib.mv_decode_chunk_tokens(96, 2) == 0

@@ -231,6 +231,24 @@ def test_split_merges_in_a_row_are_deterministic():
         _check(out, ref, dtype, f"split merges seed {seed}")
         again, _ = _step_on_gpu(c)  # whichever work group merges, the same bits
         assert torch.equal(bits(out), bits(again))
+        _assert_counters_at_rest(c)
+
+
+def _assert_counters_at_rest(c):
+    """Every merge put its (sequence, kv head) counter back to zero: the
+    plan's counters are zero between calls, as the next call of the step
+    (which does not replan) needs them."""
+    from mini_vllm.attention import paged_attention_gpu as pg
+
+    d = to_device(c)
+    spec = c.layout.spec
+    plan = pg.plan_decode(d.block_table, d.kv_len, spec.block_size, d.key_cache.shape[0], DEV,
+                          spec.head_dim, spec.dtype, spec.num_kv_heads)
+    for _ in range(2):
+        hip_decode_attention(d.query, d.key_cache, d.value_cache, d.block_table, d.kv_len,
+                             spec.block_size)
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(plan.counters)) == 0
 
 
 def test_block_size_one_long_id_lists():

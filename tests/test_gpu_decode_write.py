@@ -101,3 +101,61 @@ def test_backend_method():
     ref, _ = _both(case)
     torch.cuda.synchronize()
     _same(ref, (out, pool.key_caches[0], pool.value_caches[0]))
+
+
+def test_slot_at_an_earlier_position_of_its_own_sequence():
+    """Sequence 0's slot is one of its own earlier attended positions (token
+    5), sequence 2's another sequence's attended row: the fused launch would
+    read those rows while it writes them, so the call detects the layout on
+    the device and runs as the two calls. Pool and output equal the two
+    calls bit for bit, and the oracle's write-then-decode within tolerance."""
+    say("decode+write: slot at an earlier attended position")
+    case = make_case("c2", seed=4, nan_fill=False)
+    bs = case.layout.spec.block_size
+    slots = case.slot_mapping.clone()
+    slots[0] = int(case.block_table[0, 5 // bs]) * bs + 5 % bs
+    slots[2] = int(case.block_table[3, 0]) * bs + 1
+    case.slot_mapping = slots
+    ref, fused = _both(case)
+    _same(ref, fused)
+    want, kc_ref, vc_ref = oracle_step(case)
+    assert (fused[0].float().cpu() - want).abs().max().item() <= TOL[case.layout.spec.dtype]
+    assert torch.equal(bits(fused[1].float().cpu()), bits(kc_ref))
+
+
+def test_fused_precondition_is_checked_in_a_captured_graph():
+    """Captured, the fused call cannot fall back: its check is recorded and
+    check_deferred() raises AssertionError after a replay whose slots break
+    the layout; a replay with the block manager's slots passes."""
+    from mini_vllm.attention import paged_attention_gpu as pg
+
+    say("decode+write: captured precondition check")
+    case = make_case("c1", seed=5, nan_fill=False)
+    d = to_device(case)
+    bs = case.layout.spec.block_size
+    kc, vc = d.key_cache.clone(), d.value_cache.clone()
+    slots = d.slot_mapping.clone()
+    pg.clear_deferred()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # eager warm-up
+        hip_decode_attention(d.query, kc.clone(), vc.clone(), d.block_table, d.kv_len, bs,
+                             new_key=d.new_key, new_value=d.new_value, slot_mapping=slots)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        hip_decode_attention(d.query, kc, vc, d.block_table, d.kv_len, bs,
+                             new_key=d.new_key, new_value=d.new_value, slot_mapping=slots)
+    gid = pg.last_capture_id()
+    assert gid != 0
+    graph.replay()
+    torch.cuda.synchronize()
+    pg.check_deferred(gid)
+    slots[1] = int(case.block_table[1, 0]) * bs  # sequence 1's first token, not its last
+    graph.replay()
+    torch.cuda.synchronize()
+    with pytest.raises(AssertionError, match="kv_len_after - 1"):
+        pg.check_deferred(gid)
+    del graph
+    pg.clear_deferred()

@@ -204,3 +204,97 @@ def test_captured_long_pieces_fetch_the_rest_of_their_ids():
         assert err <= TOL[DT], (tag, err)
     del graph
     pg.clear_deferred()
+
+
+def _current_workspace():
+    return next(iter(pg._WORKSPACES.values()), None)
+
+
+def test_workspace_growth_after_capture_keeps_the_graphs_buffer():
+    """A graph captured with a small merge workspace, then an eager decode
+    big enough to need a larger one: the library keeps the buffer the graph
+    was captured with (the merge keeps state in it between calls), so
+    tensors allocated afterwards cannot land in it. Replays stay exact and
+    the new tensors keep their contents."""
+    say("graph: workspace growth after capture")
+    pg.clear_deferred()
+    for dev in list(pg._WORKSPACES):  # start from a small workspace, as a fresh process
+        pg._RETIRED_WORKSPACES.append(pg._WORKSPACES.pop(dev))
+    case = _case(11, 300, MB * BS)
+    ref = _oracle(case)
+    st = _Static()
+    st.load(case)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        st.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = st.step()
+    small = _current_workspace()
+    assert small is not None
+    # an eager decode whose partials need more workspace (32 query heads of
+    # head_dim 128, 16 sequences of 2048 tokens cut into ~8 pieces each)
+    spec = WorkloadSpec("ws-grow", 32, 2, 128, 16, DT, 16, ("fixed", [2048] * 16))
+    big = make_case(spec, seed=0, nan_fill=False)
+    q, kc, vc = big.query.to(DEV), big.key_cache.to(DEV), big.value_cache.to(DEV)
+    pg.hip_decode_attention(q, kc, vc, big.block_table.to(DEV), big.kv_len.to(DEV), 16)
+    torch.cuda.synchronize()
+    assert _current_workspace().numel() > small.numel(), "the eager call did not grow the workspace"
+    fillers = [torch.full((1 << 20,), 7, dtype=torch.int32, device=DEV) for _ in range(32)]
+    for rep in range(3):
+        st.load(case)
+        graph.replay()
+        torch.cuda.synchronize()
+        pg.check_deferred()
+        _check(st, outs, ref, f"replay {rep}")
+    for f in fillers:
+        assert int((f != 7).sum()) == 0
+    del graph
+    pg.clear_deferred()
+
+
+def test_second_capture_over_the_same_metadata_plans_on_its_own():
+    """Two graphs captured over the same static (unmodified) metadata
+    tensors: the second records its own plan and check kernels (caches are
+    keyed by capture id), so replaying only the second one with new lengths
+    is exact; each graph's deferred checks are read by its id only."""
+    say("graph: second capture over the same metadata")
+    pg.clear_deferred()
+    case_a, case_b = _case(21, 1, MB * BS), _case(22, 200, 900)
+    st = _Static()
+    st.load(case_a)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        st.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        outs1 = st.step()
+    id1 = pg.last_capture_id()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        outs2 = st.step()
+    id2 = pg.last_capture_id()
+    assert id1 and id2 and id1 != id2
+    st.load(case_b)
+    g2.replay()
+    torch.cuda.synchronize()
+    pg.check_deferred(id2)
+    _check(st, outs2, _oracle(case_b), "second graph, new lengths")
+    # a bad replay of the first graph is reported for it, not for the second
+    bad = dict(case_b)
+    bad["kv"] = case_b["kv"].clone()
+    bad["kv"][0] = 0
+    st.load(bad)
+    g1.replay()
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError, match="kv_len"):
+        pg.check_deferred(id1)
+    pg.check_deferred(id2)
+    del outs1, g1, g2
+    pg.clear_deferred()
