@@ -246,6 +246,33 @@ int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t q_stride_he
                     int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the static scratch buffer of mv_paged_decode_noalloc (per GPU). */
+#define MV_DECODE_SCRATCH_BYTES (16 << 20)
+
+/*
+ * mv_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under graph capture, serving loops that
+ * forbid allocation). No counterpart in the reference. The split-K partials
+ * live in a static device array of MV_DECODE_SCRATCH_BYTES per GPU, shared
+ * by every call on that GPU: calls that overlap on one GPU race, so order
+ * them on one stream. The call allocates nothing (no hipMalloc / hipFree,
+ * no allocating library routine); its first call on a device looks the
+ * array's address up once. Batches whose merge needs more
+ * (mv_paged_decode_workspace_bytes > MV_DECODE_SCRATCH_BYTES) are rejected
+ * with MV_ERR_INVALID_ARGUMENT; so is a stream of another device than the
+ * current one. Otherwise identical to mv_paged_decode (same kernels, same
+ * results).
+ */
+int mv_paged_decode_noalloc(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                            const void* key_cache, const void* value_cache,
+                            const int32_t* work_items, const int32_t* block_ids,
+                            int64_t block_ids_capacity, int32_t num_work_groups,
+                            int32_t partition_tokens, int32_t max_partitions, int32_t* counters,
+                            void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                            float scale, int32_t num_seqs, int32_t num_q_heads,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                            int64_t num_blocks, int32_t dtype, void* stream);
+
 /*
  * Prefix gather (prefill support).
  * Replaces the launch of `_gather_prefix_kv_kernel` in `gather_prefix_kv`

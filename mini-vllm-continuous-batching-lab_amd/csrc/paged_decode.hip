@@ -56,7 +56,9 @@
 // XCD in every wave, which costs ~10x the kernel.) Counters are zeroed by
 // the plan kernel, so every call that shares a plan must run on one stream.
 #include <algorithm>
+#include <atomic>
 #include <climits>
+#include <mutex>
 
 #include "mv_common.h"
 #include "mv_tile.h"
@@ -1472,6 +1474,82 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
                            max_partitions, counters, out, out_stride_tok, out_stride_head, scale,
                            num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
                            dtype, workspace, workspace_bytes, nullptr, stream);
+}
+
+// ---------------------------------------------------- no-allocation decode ---
+// mv_paged_decode for callers that cannot allocate (graph capture, serving
+// loops that forbid it): the fp32 partials of the split-K merge live in this
+// file-scope array instead of a caller's workspace. Every GPU the library
+// runs on holds one copy (MV_DECODE_SCRATCH_BYTES) until the process ends;
+// all calls on that GPU share it, so calls that overlap on one GPU race.
+// The merge writes every partial it reads in the same launch, so nothing in
+// it has to start at zero.
+static __device__ __align__(256) char scratch[MV_DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchMaxDevices = 256;
+std::atomic<void*> g_scratch_ptr[kScratchMaxDevices];
+std::mutex g_scratch_mutex;
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current (hipGetSymbolAddress): the array's name in
+// host code is only a host-side stand-in.
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return mv::fail(MV_ERR_HIP, "mv_paged_decode_noalloc: hipGetDevice: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kScratchMaxDevices)
+    return mv::fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode_noalloc: device %d out of range", dev);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (err != hipSuccess || !p)
+        return mv::fail(MV_ERR_HIP, "mv_paged_decode_noalloc: hipGetSymbolAddress: %s",
+                        hipGetErrorString(err));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return MV_OK;
+}
+}  // namespace
+
+extern "C" int mv_paged_decode_noalloc(const void* query, int64_t q_stride_tok,
+                                       int64_t q_stride_head, const void* key_cache,
+                                       const void* value_cache, const int32_t* work_items,
+                                       const int32_t* block_ids, int64_t block_ids_capacity,
+                                       int32_t num_work_groups, int32_t partition_tokens,
+                                       int32_t max_partitions, int32_t* counters, void* out,
+                                       int64_t out_stride_tok, int64_t out_stride_head,
+                                       float scale, int32_t num_seqs, int32_t num_q_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                       int64_t num_blocks, int32_t dtype, void* stream) {
+  if (num_seqs < 0 || num_q_heads < 0 || head_dim < 0 || max_partitions < 0)
+    return mv::fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode_noalloc: bad sizes");
+  const size_t need =
+      mv_paged_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_partitions);
+  if (need > static_cast<size_t>(MV_DECODE_SCRATCH_BYTES))
+    return mv::fail(MV_ERR_INVALID_ARGUMENT,
+                    "mv_paged_decode_noalloc: the merge needs %zu bytes of scratch, more than "
+                    "its %d-byte static buffer (%d sequences x %d query heads x %d partitions); "
+                    "use mv_paged_decode with a workspace",
+                    need, MV_DECODE_SCRATCH_BYTES, num_seqs, num_q_heads, max_partitions);
+  int stream_dev = -1, cur = -1;
+  if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &stream_dev) != hipSuccess ||
+      hipGetDevice(&cur) != hipSuccess || stream_dev != cur)
+    return mv::fail(MV_ERR_INVALID_ARGUMENT,
+                    "mv_paged_decode_noalloc: the stream must belong to the current device");
+  void* ws = nullptr;
+  if (const int rc = scratch_on_current_device(&ws)) return rc;
+  return mv::decode_launch(query, q_stride_tok, q_stride_head, key_cache, value_cache, work_items,
+                           block_ids, block_ids_capacity, num_work_groups, partition_tokens,
+                           max_partitions, counters, out, out_stride_tok, out_stride_head, scale,
+                           num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                           dtype, ws, MV_DECODE_SCRATCH_BYTES, nullptr, stream);
 }
 
 extern "C" int mv_paged_decode_write(

@@ -35,6 +35,7 @@ MV_PLAN_MIN_KV_LEN = 5
 MV_PLAN_PARTITION_TOKENS = 6
 MV_PLAN_IDS_PER_ITEM = 7
 MV_PLAN_WORDS = 8
+MV_DECODE_SCRATCH_BYTES = 16 << 20
 
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 DEFAULT_LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libmvattn.so")
@@ -84,6 +85,15 @@ SIGNATURES = {
         _F, _I32, _I32, _I32, _I32,  # scale, num_seqs, num_q_heads, num_kv_heads, head_dim
         _I32, _I64, _I32,          # block_size, num_blocks, dtype
         _P, _SZ, _P,               # workspace, workspace_bytes, stream
+    ]),
+    "mv_paged_decode_noalloc": (ctypes.c_int, [
+        _P, _I64, _I64,            # query, strides
+        _P, _P,                    # key_cache, value_cache
+        _P, _P, _I64, _I32,        # work_items, block_ids, block_ids_capacity, num_work_groups
+        _I32, _I32, _P,            # partition_tokens, max_partitions, counters
+        _P, _I64, _I64,            # out, strides
+        _F, _I32, _I32, _I32, _I32,  # scale, num_seqs, num_q_heads, num_kv_heads, head_dim
+        _I32, _I64, _I32, _P,      # block_size, num_blocks, dtype, stream
     ]),
     "mv_gather_paged_kv": (ctypes.c_int, [
         _P, _P, _P, _I32, _I64,    # key_cache, value_cache, block_table, bt_is_i64, bt_stride
