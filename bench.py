@@ -5,30 +5,39 @@ headline workload (c2: 14 query / 2 kv heads, head_dim 64, block 16, bf16,
 batch 64, kv_len ~ U{128..2048}): the KV write of the step's 64 new tokens
 and the paged decode over every sequence's blocks, as one launch (the write
 fused into the decode kernel; pool and output bit-identical to the two
-separate calls, which are timed beside it). Successive steps
-use successive layers of a pool that holds >= 1 GiB in total (the same step
-metadata, a different layer's K/V, as in a real engine step), so the
-256 MB Infinity Cache cannot serve the reads and the measured bandwidth is
-HBM bandwidth. All inputs are resident in HBM before timing starts.
+separate calls, which are timed beside it). Successive steps use successive
+layers of a pool that holds >= 1 GiB in total (the same step metadata, a
+different layer's K/V, as in a real engine step). One rotation runs through
+the warm-up and every timed loop, so each launch reads a layer that at least
+1 GiB of other reads has passed since it was last read: the 256 MB Infinity
+Cache cannot serve it, and the measured bandwidth is HBM bandwidth. All
+inputs are resident in HBM before timing starts.
 
 Printed (one JSON line): ``value`` = algorithmic bytes of the layer call
 (decode + write) / µs per layer call, in GB/s; ``roofline`` for that one
-kernel (KV write and cross-partition merge fused) against 8 TB/s; and
-``cpu_baseline`` = the oracle's PyTorch CPU path (the reference's
-per-sequence gather + SDPA loop) timed on this host's cores on the same
-workload in fp32.
+kernel (KV write and cross-partition merge fused) against 8 TB/s;
+``workloads`` = the same layer call on the other configurations (c3-c5),
+timed the same way; and ``cpu_baseline`` = the oracle's PyTorch CPU path
+(the reference's per-token write and per-sequence gather + SDPA loops)
+timed on this host's cores in fp32, write and decode apart, on c1 in full
+and on c2's shape.
 
     python bench.py [--steps K] [--warmup W] [--workload c2] [--no-cpu-baseline]
+                    [--no-workloads]
     python bench.py --copy-calibration   # plain 256 MiB copies, for PMC byte scaling
 
 ``roofline.traffic`` (HBM bytes per layer-call launch) comes from the
-rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under profiles/ for
-the workload, when there is one; otherwise it is null.
+rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under profiles/ for the
+workload (``traffic_source`` names it). It is reported only when that
+summary was taken on the current decode kernel source (its
+``source_sha256`` line matches); otherwise it is null and
+``traffic_note`` says why.
 """
 
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -37,16 +46,19 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-sys.path[:0] = [ROOT, os.path.join(ROOT, "mini-vllm-continuous-batching-lab_amd")]
+PKG = os.path.join(ROOT, "mini-vllm-continuous-batching-lab_amd")
+sys.path[:0] = [ROOT, PKG]
 
 import torch  # noqa: E402
 
 from benchmarks.paged_decode_workloads import (  # noqa: E402
-    HEADLINE, SPECS, decode_bytes, make_layout, write_bytes)
+    HEADLINE, SPECS, WorkloadSpec, decode_bytes, make_layout, write_bytes)
 
 METRIC = "paged decode µs/layer-call + achieved HBM GB/s (% peak), Qwen2-0.5B bs64"
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
 MIN_WORKING_SET = 1 << 30
+OTHER_WORKLOADS = ("c3", "c4", "c5")
 
 
 def log(*a):
@@ -54,7 +66,8 @@ def log(*a):
 
 
 def build_layers(spec, layout, n_layers, device, seed):
-    """Per-layer pools (K, V), queries and new-token K/V, N(0,1) in bf16, made on the GPU."""
+    """Per-layer pools (K, V), queries and new-token K/V, N(0,1) in the
+    workload's dtype, made on the GPU."""
     g = torch.Generator(device=device).manual_seed(seed)
     nb, hkv, bs, d = layout.num_blocks, spec.num_kv_heads, spec.block_size, spec.head_dim
     b = len(layout.kv_lens)
@@ -68,6 +81,27 @@ def build_layers(spec, layout, n_layers, device, seed):
             nv=torch.randn(b, hkv, d, generator=g, device=device).to(spec.dtype),
         ))
     return layers
+
+
+def layers_for_working_set(spec, layout):
+    pool_bytes = 2 * layout.num_blocks * spec.num_kv_heads * spec.block_size * spec.head_dim * \
+        torch.tensor([], dtype=spec.dtype).element_size()
+    return max(2, math.ceil(MIN_WORKING_SET / pool_bytes)), pool_bytes
+
+
+class Rotation:
+    """The layer each launch reads, in one sequence over the whole run
+    (warm-up and every timed loop): the layer read next is always the one
+    read longest ago."""
+
+    def __init__(self, layers):
+        self.layers = layers
+        self.n = 0
+
+    def take(self):
+        L = self.layers[self.n % len(self.layers)]
+        self.n += 1
+        return L
 
 
 _SLEEP_CYCLES_PER_MS = None
@@ -90,7 +124,7 @@ def _hold_gpu(stream, ms):
 def time_loop(fn, n, stream, host_us=60.0):
     """GPU time per iteration: the launches run back to back on the GPU
     (host overhead, up to ``host_us`` per iteration, hidden behind a held
-    GPU), bracketed by HIP events."""
+    GPU), bracketed by HIP events recorded on the launch stream."""
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -142,9 +176,6 @@ def torch_rope(x, pos, cos, sin):
     c, s = cos[pos].unsqueeze(-2), sin[pos].unsqueeze(-2)
     h = x.shape[-1] // 2
     return x * c + torch.cat((-x[..., h:], x[..., :h]), dim=-1) * s
-
-
-PEAK_BF16_TFLOPS = 2500.0
 
 
 def prefill_measure(dev, steps, warmup):
@@ -230,64 +261,195 @@ def plan_step_us(bt, kv, bs, num_blocks, dev, spec, plan_decode, reps=20):
     return statistics.median(times)
 
 
-def cpu_baseline(spec, layout, layer, budget_s=12.0):
-    """The oracle's CPU path (reference loops, fp32) on a bounded sample:
-    whole layer calls (write + decode of the full batch) repeated until
-    ``budget_s`` of CPU time or 7 calls, median reported."""
+def measure_workload(name, steps, warmup, dev, stream, seed):
+    """The fused layer call (KV write + decode, one launch) and decode alone
+    on another configuration, timed as the headline: >= 1 GiB of per-layer
+    pools in one rotation, event-timed back-to-back launches."""
+    from mini_vllm.attention.paged_attention_gpu import hip_decode_attention, plan_decode
+
+    spec = SPECS[name]
+    layout = make_layout(spec, seed)
+    n_layers, _ = layers_for_working_set(spec, layout)
+    layers = build_layers(spec, layout, n_layers, dev, seed)
+    bt = layout.block_table().to(dev)
+    kv = torch.tensor(layout.kv_lens, dtype=torch.int64, device=dev)
+    slots = layout.new_token_slots().to(dev)
+    bs = spec.block_size
+    plan = plan_decode(bt, kv, bs, layout.num_blocks, dev, spec.head_dim, spec.dtype,
+                       spec.num_kv_heads)
+    rot = Rotation(layers)
+
+    def layer_call(i):
+        L = rot.take()
+        hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs, new_key=L["nk"],
+                             new_value=L["nv"], slot_mapping=slots)
+
+    def decode_only(i):
+        L = rot.take()
+        hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs)
+
+    for i in range(max(warmup, n_layers)):
+        layer_call(i)
+    us = time_loop(layer_call, steps, stream)
+    us_dec = time_loop(decode_only, steps, stream)
+    dec_bytes = decode_bytes(layout, spec.dtype)
+    wr_bytes = write_bytes(layout, spec.dtype)
+    res = {
+        "shape": f"{spec.num_q_heads} q / {spec.num_kv_heads} kv heads, head_dim {spec.head_dim}, "
+                 f"block {bs}, batch {len(layout.kv_lens)}, kv_len {spec.ctx}",
+        "mean_kv_len": round(sum(layout.kv_lens) / len(layout.kv_lens), 1),
+        "us_per_layer_call": round(us, 3),
+        "decode_us": round(us_dec, 3),
+        "algorithmic_bytes": dec_bytes + wr_bytes,
+        "gbs": round((dec_bytes + wr_bytes) / us / 1e3, 1),
+        "frac": round((dec_bytes + wr_bytes) / us / 1e3 / PEAK_HBM_GBS, 4),
+        "work_groups": plan.num_groups,
+        "partition_tokens": plan.partition_tokens,
+        "layers_rotated": n_layers,
+    }
+    if layout.shared_blocks:
+        uniq = decode_bytes(layout, spec.dtype, unique=True) + wr_bytes
+        res["unique_bytes"] = uniq
+        res["frac_unique"] = round(uniq / us / 1e3 / PEAK_HBM_GBS, 4)
+    del layers, rot
+    torch.cuda.empty_cache()
+    return res
+
+
+def reference_shapes(dev, stream, steps):
+    """The reference's own micro-benchmark shapes (Qwen2-0.5B heads: 14 q /
+    2 kv, head_dim 64, block 16, fp16; batch 1 and 4 at context 16, 128 and
+    512; benchmarks/benchmark_paged_attention.py:273-503): decode alone, by
+    events over back-to-back launches and host-inclusive (the wrapper's
+    Python, as the reference's timing includes). Context for the published
+    Triton rows only: those come from another GPU."""
+    from mini_vllm.attention.paged_attention_gpu import hip_decode_attention
+
+    published = {(1, 16): 101.84, (1, 128): 121.11, (1, 512): 287.16,
+                 (4, 16): 78.95, (4, 128): 121.67, (4, 512): 300.03}
+    rows = []
+    for (b, ctx), ref_us in published.items():
+        spec = WorkloadSpec(f"ref-b{b}-c{ctx}", 14, 2, 64, 16, torch.float16, b,
+                            ("fixed", [ctx] * b), pool_blocks=max(512, b * (-(-ctx // 16)) * 2))
+        layout = make_layout(spec, 0)
+        L = build_layers(spec, layout, 1, dev, 1)[0]
+        bt = layout.block_table().to(dev)
+        kv = torch.tensor(layout.kv_lens, dtype=torch.int64, device=dev)
+
+        def call(i):
+            hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, 16)
+
+        for i in range(10):
+            call(i)
+        us = time_loop(call, steps, stream)
+        us_wall = wall_loop(call, steps)
+        rows.append({"batch": b, "ctx": ctx, "us": round(us, 2),
+                     "host_inclusive_us": round(us_wall, 2),
+                     "reference_triton_us_rtx3060": ref_us})
+    return rows
+
+
+def _cpu_median(fn, budget_s, max_n=7):
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < max_n and (len(times) < 2 or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times) * 1e6, len(times)
+
+
+def cpu_baseline(spec, layout, layer, budget_s=8.0):
+    """The oracle's CPU path (the reference's loops, fp32) on all host cores,
+    write and decode timed apart: c2's shape (the headline's layer, full
+    batch) on a bounded sample, and c1 in full."""
+    from benchmarks.paged_decode_workloads import make_case
     from oracle import paged_ref
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    kc = layer["k"].float().cpu()
-    vc = layer["v"].float().cpu()
-    q, nk, nv = layer["q"].float().cpu(), layer["nk"].float().cpu(), layer["nv"].float().cpu()
-    bt = layout.block_table()
-    kv = torch.tensor(layout.kv_lens, dtype=torch.int64)
-    slots = layout.new_token_slots()
 
-    def call():
-        paged_ref.write_to_paged_cache(nk, nv, kc, vc, slots, spec.block_size)
-        return paged_ref.decode_from_tables(q, kc, vc, bt, kv, spec.block_size)
+    def timings(kc, vc, q, nk, nv, bt, kv, slots, bs, budget):
+        def write():
+            paged_ref.write_to_paged_cache(nk, nv, kc, vc, slots, bs)
 
-    call()  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 7 and (len(times) < 2 or time.perf_counter() < t_end):
-        t0 = time.perf_counter()
-        call()
-        times.append(time.perf_counter() - t0)
-    us = statistics.median(times) * 1e6
+        def decode():
+            return paged_ref.decode_from_tables(q, kc, vc, bt, kv, bs)
+
+        w_us, w_n = _cpu_median(write, budget / 4)
+        d_us, d_n = _cpu_median(decode, budget)
+        return w_us, d_us, min(w_n, d_n)
+
+    # c2's shape: the bench's own layer, in fp32 on the CPU
+    w_us, d_us, n = timings(layer["k"].float().cpu(), layer["v"].float().cpu(),
+                            layer["q"].float().cpu(), layer["nk"].float().cpu(),
+                            layer["nv"].float().cpu(), layout.block_table(),
+                            torch.tensor(layout.kv_lens, dtype=torch.int64),
+                            layout.new_token_slots(), spec.block_size, budget_s)
     nbytes = decode_bytes(layout, spec.dtype) + write_bytes(layout, spec.dtype)
+    us = w_us + d_us
+    c1 = make_case("c1", seed=0)
+    c1_w, c1_d, c1_n = timings(c1.key_cache.clone(), c1.value_cache.clone(), c1.query,
+                               c1.new_key, c1.new_value, c1.block_table, c1.kv_len,
+                               c1.slot_mapping, 16, 2.0)
     return {
         "value": round(nbytes / us / 1e3, 4),
         "unit": "GB/s",
         "us_per_layer_call": round(us, 1),
+        "write_us": round(w_us, 1),
+        "decode_us": round(d_us, 1),
         "cores": cores,
         "kind": "port",
-        "sample": (f"{len(times)} full layer calls (write of {len(layout.kv_lens)} tokens + "
-                   f"decode of {len(layout.kv_lens)} sequences, {spec.name} shape) in fp32 with "
-                   f"torch.set_num_threads({cores}); median; GB/s on the bf16 workload's "
-                   f"algorithmic bytes"),
+        "sample": (f"median of {n} write calls ({len(layout.kv_lens)} tokens) and {n} decode "
+                   f"calls ({len(layout.kv_lens)} sequences) at {spec.name}'s shape in fp32 with "
+                   f"torch.set_num_threads({cores}); GB/s on the bf16 workload's algorithmic "
+                   f"bytes over write + decode"),
+        "c1": {"write_us": round(c1_w, 1), "decode_us": round(c1_d, 1),
+               "us_per_layer_call": round(c1_w + c1_d, 1),
+               "sample": f"c1 in full (4 tokens written, 4 sequences decoded, fp32), "
+                         f"median of {c1_n}"},
     }
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "paged_decode_write_kernel_{workload}_traffic.md")
+KERNEL_SOURCES = ("csrc/paged_decode.hip", "csrc/mv_tile.h", "csrc/mv_common.h")
 COPY_BYTES = 256 << 20
+
+
+def kernel_source_sha256():
+    """Hash of the decode kernel's sources (the files a PMC profile of it
+    depends on), as written into the traffic summaries."""
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(PKG, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
 
 
 def measured_traffic(workload):
     """HBM bytes per layer-call launch (the decode kernel with the KV write
-    fused) from the committed PMC summary (a line
-    ``traffic_bytes_per_launch: N``), or None."""
+    fused) from the committed PMC summary: (bytes, source, note). The bytes
+    are None when there is no summary or it was taken on other kernel
+    sources than the current ones."""
     path = TRAFFIC_SUMMARY.format(workload=workload)
+    rel = os.path.relpath(path, ROOT)
+    fields = {}
     try:
         with open(path) as f:
             for line in f:
-                if line.strip().startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip())
+                key, sep, val = line.strip().partition(":")
+                if sep and key in ("traffic_bytes_per_launch", "source_sha256"):
+                    fields[key] = val.strip()
     except OSError:
-        pass
-    return None
+        return None, None, f"no PMC summary at {rel}"
+    if "traffic_bytes_per_launch" not in fields:
+        return None, rel, f"{rel} has no traffic_bytes_per_launch line"
+    if fields.get("source_sha256") != kernel_source_sha256():
+        return None, rel, f"{rel} was profiled on other decode kernel sources than these"
+    return int(fields["traffic_bytes_per_launch"]), rel, (
+        "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel source, scaled by a plain copy's "
+        "counts (committed summary, not measured in this run)")
 
 
 def copy_calibration(steps):
@@ -311,6 +473,8 @@ def main(argv=None) -> int:
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(SPECS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the other configurations' layer calls")
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args(argv)
 
@@ -336,15 +500,14 @@ def main(argv=None) -> int:
     spec = SPECS[args.workload]
     layout = make_layout(spec, args.seed)
     bs = spec.block_size
-    pool_bytes = 2 * layout.num_blocks * spec.num_kv_heads * bs * spec.head_dim * 2
-    n_layers = max(2, math.ceil(MIN_WORKING_SET / pool_bytes))
+    n_layers, pool_bytes = layers_for_working_set(spec, layout)
     log(f"[bench] workload {spec.name}: B={len(layout.kv_lens)} blocks={layout.num_blocks} "
         f"layers={n_layers} ({n_layers * pool_bytes / 2**30:.2f} GiB of K/V)")
     layers = build_layers(spec, layout, n_layers, dev, args.seed)
+    rot = Rotation(layers)
     bt = layout.block_table().to(dev)
     kv = torch.tensor(layout.kv_lens, dtype=torch.int64, device=dev)
     slots = layout.new_token_slots().to(dev)
-    outs = [torch.empty_like(L["q"]) for L in layers]
     stream = torch.cuda.current_stream(dev)
 
     # per-step validation/planning (once per engine step, shared by all layers)
@@ -353,25 +516,24 @@ def main(argv=None) -> int:
     plan_us = plan_step_us(bt, kv, bs, layout.num_blocks, dev, spec, plan_decode)
 
     def layer_call(i):  # one launch: the step's KV write fused into the decode
-        L = layers[i % n_layers]
-        outs[i % n_layers] = hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs,
-                                                  new_key=L["nk"], new_value=L["nv"],
-                                                  slot_mapping=slots)
+        L = rot.take()
+        hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs, new_key=L["nk"],
+                             new_value=L["nv"], slot_mapping=slots)
 
     def layer_call_two(i):  # the reference's two calls: write, then decode
-        L = layers[i % n_layers]
+        L = rot.take()
         hip_cache_write(L["nk"], L["nv"], L["k"], L["v"], slots, bs)
-        outs[i % n_layers] = hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs)
+        hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs)
 
     def decode_only(i):
-        L = layers[i % n_layers]
+        L = rot.take()
         hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs)
 
     def write_only(i):
-        L = layers[i % n_layers]
+        L = rot.take()
         hip_cache_write(L["nk"], L["nv"], L["k"], L["v"], slots, bs)
 
-    for i in range(args.warmup):
+    for i in range(max(args.warmup, n_layers)):
         layer_call_two(i)
         layer_call(i)
     torch.cuda.synchronize()
@@ -388,16 +550,17 @@ def main(argv=None) -> int:
     # A whole decode step captured into one HIP graph: the plan (replanned
     # from the static metadata at every replay) and Qwen2-0.5B's 24 layer
     # calls; no host work per layer.
-    from mini_vllm.attention.paged_attention_gpu import check_deferred, clear_deferred
+    from mini_vllm.attention.paged_attention_gpu import check_deferred, clear_deferred, last_capture_id
     graph_layers = 24
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(graph_layers):
             layer_call(i)
+    gid = last_capture_id()
     for _ in range(3):
         graph.replay()
     torch.cuda.synchronize()
-    check_deferred()
+    check_deferred(gid)
     g_steps = max(5, args.steps // graph_layers)
     us_graph = time_loop(lambda i: graph.replay(), g_steps, stream, host_us=100.0)
     us_graph_wall = wall_loop(lambda i: graph.replay(), g_steps)
@@ -416,12 +579,12 @@ def main(argv=None) -> int:
     pos = kv - 1  # the new token's position in each sequence
 
     def rope_fused(i):
-        L = layers[i % n_layers]
+        L = rot.take()
         hip_rope_kv_cache_write(L["q"], L["nk"], L["nv"], pos, cos, sin, L["k"], L["v"], slots, bs,
                                 return_key=False)
 
     def rope_unfused(i):
-        L = layers[i % n_layers]
+        L = rot.take()
         torch_rope(L["q"], pos, cos, sin)
         k = torch_rope(L["nk"], pos, cos, sin)
         hip_cache_write(k, L["nv"], L["k"], L["v"], slots, bs)
@@ -440,6 +603,10 @@ def main(argv=None) -> int:
     wr_bytes = write_bytes(layout, spec.dtype)
     us_copy = same_bytes_copy_us(dec_bytes + wr_bytes, dev, args.steps, stream)
     log(f"[bench] plain copy of the same HBM bytes: {us_copy:.2f} us")
+    ref_shapes = reference_shapes(dev, stream, max(20, args.steps // 4))
+    log("[bench] reference shapes: " + ", ".join(
+        f"b{r['batch']} ctx{r['ctx']} {r['us']:.1f} us" for r in ref_shapes))
+    traffic, traffic_source, traffic_note = measured_traffic(spec.name)
     gbs = (dec_bytes + wr_bytes) / us_step / 1e3
     result = {
         "metric": METRIC,
@@ -490,6 +657,7 @@ def main(argv=None) -> int:
             "fused_host_inclusive_us": round(us_rope_wall, 2),
             "unfused_host_inclusive_us": round(us_rope_unfused_wall, 2),
         },
+        "reference_shapes": ref_shapes,
         "partition_tokens": plan.partition_tokens,
         "work_groups": plan.num_groups,
         "roofline": {
@@ -504,17 +672,32 @@ def main(argv=None) -> int:
             "decode_only_frac": round(dec_bytes / us_decode / 1e3 / PEAK_HBM_GBS, 4),
             "same_bytes_copy_us": round(us_copy, 3),
             "same_bytes_copy_frac": round((dec_bytes + wr_bytes) / us_copy / 1e3 / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic(spec.name),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
+            "traffic_note": traffic_note,
         },
+        "workloads": {},
         "cpu_baseline": None,
     }
     if layout.shared_blocks:  # shared prefixes: the roofline on the bytes that must move
         uniq = decode_bytes(layout, spec.dtype, unique=True) + wr_bytes
         result["roofline"]["unique_bytes"] = uniq
         result["roofline"]["frac_unique"] = round(uniq / us_step / 1e3 / PEAK_HBM_GBS, 4)
+    cpu_layer = layers[0]
+    del layers, rot
+    torch.cuda.empty_cache()
+    if not args.no_workloads:
+        for name in OTHER_WORKLOADS:
+            if name == spec.name:
+                continue
+            w = measure_workload(name, max(50, args.steps // 2), args.warmup, dev, stream,
+                                 args.seed)
+            result["workloads"][name] = w
+            log(f"[bench] {name}: layer call {w['us_per_layer_call']:.2f} us, frac {w['frac']}"
+                + (f" (unique bytes {w['frac_unique']})" if "frac_unique" in w else ""))
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(spec, layout, layers[0])
+        result["cpu_baseline"] = cpu_baseline(spec, layout, cpu_layer)
     print(json.dumps(result), flush=True)
     return 0
 
