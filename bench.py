@@ -547,27 +547,67 @@ def main(argv=None) -> int:
     log(f"[bench] layer call {us_step:.2f} us (write fused); write + decode calls {us_two:.2f} us "
         f"(decode {us_decode:.2f}, write {us_write:.2f})")
 
+    # The decode attention sub-layer (qwen_runner.py:164-190 for the decode
+    # rows): RoPE of q and the new k, the KV write and the decode, in one
+    # launch, against the two launches of fused RoPE + write, then decode.
+    cos, sin = rope_tables(spec.head_dim, 1000000.0, 32768, spec.dtype, dev)
+    pos = kv - 1  # the new token's position in each sequence
+
+    def sublayer(i):
+        L = rot.take()
+        hip_decode_attention(L["q"], L["k"], L["v"], bt, kv, bs, new_key=L["nk"],
+                             new_value=L["nv"], slot_mapping=slots, positions=pos, cos=cos,
+                             sin=sin)
+
+    def sublayer_two(i):
+        L = rot.take()
+        q_rot, _ = hip_rope_kv_cache_write(L["q"], L["nk"], L["nv"], pos, cos, sin, L["k"], L["v"],
+                                           slots, bs, return_key=False)
+        hip_decode_attention(q_rot, L["k"], L["v"], bt, kv, bs)
+
+    for i in range(args.warmup):
+        sublayer(i)
+        sublayer_two(i)
+    us_sub = time_loop(sublayer, args.steps, stream)
+    us_sub_two = time_loop(sublayer_two, args.steps, stream)
+    log(f"[bench] attention sub-layer (RoPE + write + decode) {us_sub:.2f} us in one launch, "
+        f"{us_sub_two:.2f} us as RoPE+write then decode")
+
     # A whole decode step captured into one HIP graph: the plan (replanned
-    # from the static metadata at every replay) and Qwen2-0.5B's 24 layer
-    # calls; no host work per layer.
+    # from the static metadata at every replay), the RoPE rows, and
+    # Qwen2-0.5B's 24 attention sub-layers; no host work per layer.
     from mini_vllm.attention.paged_attention_gpu import check_deferred, clear_deferred, last_capture_id
     graph_layers = 24
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(graph_layers):
-            layer_call(i)
-    gid = last_capture_id()
-    for _ in range(3):
-        graph.replay()
-    torch.cuda.synchronize()
-    check_deferred(gid)
-    g_steps = max(5, args.steps // graph_layers)
-    us_graph = time_loop(lambda i: graph.replay(), g_steps, stream, host_us=100.0)
-    us_graph_wall = wall_loop(lambda i: graph.replay(), g_steps)
-    del graph
-    clear_deferred()
-    log(f"[bench] captured step ({graph_layers} layers + plan): {us_graph:.1f} us GPU, "
-        f"{us_graph_wall:.1f} us host-inclusive")
+    graphs = {}
+    for name, fn in (("sublayer", sublayer), ("write_decode", layer_call)):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(graph_layers):
+                fn(i)
+        gid = last_capture_id()
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        check_deferred(gid)
+        g_steps = max(5, args.steps // graph_layers)
+        us_graph = time_loop(lambda i: graph.replay(), g_steps, stream, host_us=100.0)
+        us_graph_wall = wall_loop(lambda i: graph.replay(), g_steps)
+        graphs[name] = (us_graph, us_graph_wall)
+        del graph
+        clear_deferred()
+        log(f"[bench] captured step {name} ({graph_layers} layers + plan): {us_graph:.1f} us GPU, "
+            f"{us_graph_wall:.1f} us host-inclusive")
+
+    # o_proj of the decode rows (qwen_runner.py:190-193): a [B, Hq*D] x
+    # [Hq*D, hidden] GEMM (torch / hipBLASLt), for the fusion decision
+    hidden = spec.num_q_heads * spec.head_dim
+    w_o = torch.randn(hidden, hidden, device=dev).to(spec.dtype)
+    a_o = torch.randn(len(layout.kv_lens), hidden, device=dev).to(spec.dtype)
+    for _ in range(5):
+        torch.matmul(a_o, w_o.t())
+    us_oproj = time_loop(lambda i: torch.matmul(a_o, w_o.t()), args.steps, stream)
+    log(f"[bench] o_proj GEMM [{len(layout.kv_lens)} x {hidden}] x [{hidden} x {hidden}]: "
+        f"{us_oproj:.2f} us")
 
     prefill = prefill_measure(dev, args.steps, min(args.warmup, 5))
     log(f"[bench] prefill {prefill['us']:.1f} us ({prefill['tflops']:.1f} TFLOP/s), "
@@ -575,9 +615,6 @@ def main(argv=None) -> int:
 
     # RoPE of the step's q and new k + KV write: fused kernel against the
     # reference's sequence (two eager rotaries, then the cache write)
-    cos, sin = rope_tables(spec.head_dim, 1000000.0, 32768, spec.dtype, dev)
-    pos = kv - 1  # the new token's position in each sequence
-
     def rope_fused(i):
         L = rot.take()
         hip_rope_kv_cache_write(L["q"], L["nk"], L["nv"], pos, cos, sin, L["k"], L["v"], slots, bs,
@@ -642,13 +679,22 @@ def main(argv=None) -> int:
         "two_call_host_inclusive_us": round(us_two_wall, 3),
         "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "plan_us_per_step": round(plan_us, 1),
-        "graph_step": {
-            "what": "one HIP graph: decode plan + 24 layer calls (KV write + decode)",
-            "layers": graph_layers,
-            "us_per_step": round(us_graph, 2),
-            "us_per_layer_call": round(us_graph / graph_layers, 3),
-            "host_inclusive_us_per_step": round(us_graph_wall, 2),
+        "sublayer": {
+            "what": "decode attention sub-layer (qwen_runner.py:164-190, decode rows): RoPE of q "
+                    "and new k + KV write + decode",
+            "one_launch_us": round(us_sub, 3),
+            "rope_write_then_decode_us": round(us_sub_two, 3),
         },
+        "graph_step": {
+            "what": "one HIP graph: decode plan + RoPE rows + 24 attention sub-layers (RoPE + "
+                    "KV write + decode, one launch each)",
+            "layers": graph_layers,
+            "us_per_step": round(graphs["sublayer"][0], 2),
+            "us_per_layer": round(graphs["sublayer"][0] / graph_layers, 3),
+            "host_inclusive_us_per_step": round(graphs["sublayer"][1], 2),
+            "without_rope_us_per_step": round(graphs["write_decode"][0], 2),
+        },
+        "o_proj_gemm_us": round(us_oproj, 3),
         "prefill": prefill,
         "rope_write": {
             "what": "RoPE of the step's q and new k + KV write (qwen_runner.py:164-170)",

@@ -345,14 +345,28 @@ int mv_positions_check(const int64_t* positions, int64_t num_tokens, int64_t max
  * duplicates first). Sequence b's last token (kv_len - 1) is taken from
  * the new rows when its slot is that token's table position, which is
  * what the block manager produces; otherwise it is read from the pool.
- * Precondition, as the block manager guarantees: no slot lies in a block
- * that another sequence of the batch attends. The output and the pool are
- * then bit-identical to mv_kv_cache_write followed by mv_paged_decode.
+ * Precondition (the block manager's layout): every slot is -1 or its
+ * sequence's position kv_len - 1 (mv_decode_write_check counts the
+ * others), and no other sequence of the batch attends it. The output and
+ * the pool are then bit-identical to mv_kv_cache_write followed by
+ * mv_paged_decode.
+ *
+ * With rope_cos_rows / rope_sin_rows ([num_seqs][head_dim] rows of the
+ * rotary cos / sin tables at each sequence's position, query dtype,
+ * contiguous, 16-byte aligned; both or neither), the launch also applies
+ * the rotary embedding to the query and to new_key before using and
+ * storing them: `RotaryEmbedding.__call__` (mini_vllm/model/rotary.py:
+ * 44-82) with the reference's rounding, so output and pool are
+ * bit-identical to mv_rope_kv_cache_write followed by mv_paged_decode on
+ * the rotated query. This replaces the runner's rope(q), rope(k),
+ * write_kv_cache and decode_attention for the decode rows
+ * (qwen_runner.py:164-190) with one launch.
  */
 int mv_paged_decode_write(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
                           const void* new_key, int64_t nk_stride_tok, int64_t nk_stride_head,
                           const void* new_value, int64_t nv_stride_tok, int64_t nv_stride_head,
-                          const int64_t* slot_mapping, void* key_cache, void* value_cache,
+                          const int64_t* slot_mapping, const void* rope_cos_rows,
+                          const void* rope_sin_rows, void* key_cache, void* value_cache,
                           const int32_t* work_items, const int32_t* block_ids,
                           int64_t block_ids_capacity, int32_t num_work_groups,
                           int32_t partition_tokens, int32_t max_partitions, int32_t* counters,

@@ -97,6 +97,20 @@ __device__ __forceinline__ float rows_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// The value lane ^ 32 holds (the other half of the wave), for 16 bytes per
+// lane: one permlane32 swap per dword (VALU, no LDS). permlane32_swap of
+// (x, x) yields (rows 0 1 0 1, rows 2 3 2 3) as above, so lanes 0-31 find
+// lanes 32-63's values in the second result and lanes 32-63 lanes 0-31's
+// in the first.
+__device__ __forceinline__ uint32_t swap_wave_halves_u32(uint32_t x, int lane) {
+  const auto a = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return (lane & 32) ? a[0] : a[1];
+}
+__device__ __forceinline__ uint4 swap_wave_halves(uint4 x, int lane) {
+  return make_uint4(swap_wave_halves_u32(x.x, lane), swap_wave_halves_u32(x.y, lane),
+                    swap_wave_halves_u32(x.z, lane), swap_wave_halves_u32(x.w, lane));
+}
+
 // P values of one lane (4 per 16-token tile, fp32) rounded to the 16-bit
 // MFMA input type in two packed conversions, returned as the PV MFMA's A
 // operand; `sum` accumulates the rounded values (two dot2 with (1, 1)), so

@@ -61,6 +61,7 @@
 #include <mutex>
 
 #include "mv_common.h"
+#include "mv_rope.h"
 #include "mv_tile.h"
 
 namespace mv {
@@ -102,7 +103,8 @@ struct Traits : TileGeom<DTYPE, D> {
   static constexpr int kWaveLds = kStages * kStageBytes;
   // LDS is one union, laid out per phase:
   //   tile loop: [kWaves][kStages][K, V][kTileBytes], then the partition's
-  //              block ids (int32, kIdCap), then the group's 16 Q rows;
+  //              block ids (int32, kIdCap), then the group's 16 Q rows, then
+  //              the cos and sin rows of the sequence's position (fused RoPE);
   //   epilogue:  each wave's o rows and (max, sum) in its own tile buffers;
   //              the last-group flag where the block ids were.
   static constexpr int kIdsOffset = kWaves * kWaveLds;
@@ -114,7 +116,8 @@ struct Traits : TileGeom<DTYPE, D> {
   static constexpr int kORowStride = D + 4;
   static constexpr int kWaveEpilogueBytes = (kMaxGroup * kORowStride + 2 * kMaxGroup) * 4;
   static constexpr int kFlagOffset = kIdsOffset;
-  static constexpr int kLdsBytes = kTilesEnd;
+  static constexpr int kRopeOffset = kTilesEnd;  // cos row, then sin row (kRowBytes each)
+  static constexpr int kLdsBytes = kRopeOffset + 2 * kRowBytes;
   static_assert(kWaveEpilogueBytes <= kWaveLds, "a wave's epilogue fits its tile buffers");
   static_assert(kStages >= 2 && kStages <= 4, "tile stages");
   // Work groups one CU holds (160 KiB of LDS on gfx950), and the matching
@@ -156,6 +159,10 @@ struct DecodeArgs {
   int64_t nk_st, nk_sh, nv_st, nv_sh;  // bytes
   const int64_t* slots;
   int64_t total_slots;
+  // Fused RoPE of the query and the new key (FUSED kernels, optional): the
+  // cos / sin table rows at each sequence's position, [num_seqs][D].
+  const char* rope_cos;
+  const char* rope_sin;
 };
 
 // --------------------------------------------------------------- MFMA ----
@@ -178,9 +185,10 @@ __device__ __forceinline__ float unpack_hi(uint64_t v) { return __uint_as_float(
 
 // ----------------------------------------------------------- the kernel ---
 
-template <int DTYPE, int D, bool FUSED>
+template <int DTYPE, int D, bool FUSED, bool ROPE>
 __global__ __launch_bounds__(kWaves * 64)
 __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged_decode_kernel(DecodeArgs a) {
+  static_assert(FUSED || !ROPE, "the fused RoPE comes with the fused write");
   using Tr = Traits<DTYPE, D>;
   using raw_t = typename Elem<DTYPE>::raw;
   constexpr int L = Tr::kLoads;
@@ -297,6 +305,13 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
                          (h * a.n_rep + min(row, a.n_rep - 1)) * a.q_stride_head + col;
       copy_to_lds_16B(reinterpret_cast<const char*>(src),
                       __builtin_amdgcn_readfirstlane(lds0 + Tr::kQOffset + c * 1024));
+    }
+    // the sequence's cos and sin rows (fused RoPE): lanes [0, RP) the cos
+    // row's 16-byte pieces, [RP, 2 RP) the sin row's, to the LDS rows after Q
+    if (ROPE && lane < 2 * RP) {
+      const char* src = (lane < RP ? a.rope_cos : a.rope_sin) + static_cast<int64_t>(b) * Tr::kRowBytes +
+                        (lane < RP ? lane : lane - RP) * 16;
+      copy_to_lds_16B(src, __builtin_amdgcn_readfirstlane(lds0 + Tr::kRopeOffset));
     }
   }
 
@@ -444,6 +459,21 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       // replaced when the slot is the token's table position (checked here,
       // long after the slot's load was issued)
       if (last_piece && k == n_chunks - 1 && wave == new_wave) {
+        if constexpr (ROPE) {
+          // RoPE of the new key row (lanes [0, RP)): chunk pc pairs with
+          // chunk pc ^ RP/2 of the other half; cos / sin at its own dims
+          uint4 partner;
+          partner.x = __shfl_xor(new_piece.x, RP / 2);
+          partner.y = __shfl_xor(new_piece.y, RP / 2);
+          partner.z = __shfl_xor(new_piece.z, RP / 2);
+          partner.w = __shfl_xor(new_piece.w, RP / 2);
+          if (lane < RP) {
+            const char* rope = s_lds + Tr::kRopeOffset;
+            const uint4 c = *reinterpret_cast<const uint4*>(rope + lane * 16);
+            const uint4 sn = *reinterpret_cast<const uint4*>(rope + Tr::kRowBytes + lane * 16);
+            new_piece = rotate_chunk<DTYPE>(new_piece, partner, c, sn, lane < RP / 2);
+          }
+        }
         const int lt = tok_end - 1;
         const int id = s_ids[min((lt >> a.bs_log2) - first_blk, kIdCap - 1)];
         if (id >= 0 && new_slot == (static_cast<int64_t>(id) << a.bs_log2) + (lt & bs_mask) &&
@@ -473,6 +503,21 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     const char* q_row = s_lds + Tr::kQOffset + t * Tr::kRowBytes;
 #pragma unroll
     for (int c = 0; c < QP; ++c) qr[c] = *reinterpret_cast<const uint4*>(q_row + (g * QP + c) * 16);
+  }
+  if constexpr (ROPE) {
+    // RoPE of the Q operand in registers, by every wave: lane (g, t) holds
+    // dims [g D/4, (g+1) D/4) of row t, and the other half of the row
+    // (dims +D/2) sits in lane (g ^ 2, t) = lane ^ 32, one permlane32 swap
+    // away; the cos / sin rows landed in LDS with the Q rows.
+    const char* rope = s_lds + Tr::kRopeOffset;
+#pragma unroll
+    for (int c = 0; c < QP; ++c) {
+      const int pc = g * QP + c;  // the 16-byte piece of the row
+      const uint4 partner = swap_wave_halves(qr[c], lane);
+      const uint4 cs = *reinterpret_cast<const uint4*>(rope + pc * 16);
+      const uint4 sn = *reinterpret_cast<const uint4*>(rope + Tr::kRowBytes + pc * 16);
+      qr[c] = rotate_chunk<DTYPE>(qr[c], partner, cs, sn, g < 2);
+    }
   }
   for (int k = 0; k < n_chunks; k += S) {
     step(k, IntC<0>{});
@@ -1176,8 +1221,10 @@ int chunk_tokens(int head_dim, int dtype) { return trait_value<ChunkOf>(head_dim
 
 template <int DTYPE, int D>
 int launch_decode(const DecodeArgs& a, int num_groups, hipStream_t s) {
-  if (a.new_k) paged_decode_kernel<DTYPE, D, true><<<static_cast<unsigned>(num_groups), kWaves * 64, 0, s>>>(a);
-  else paged_decode_kernel<DTYPE, D, false><<<static_cast<unsigned>(num_groups), kWaves * 64, 0, s>>>(a);
+  const unsigned grid = static_cast<unsigned>(num_groups);
+  if (a.rope_cos) paged_decode_kernel<DTYPE, D, true, true><<<grid, kWaves * 64, 0, s>>>(a);
+  else if (a.new_k) paged_decode_kernel<DTYPE, D, true, false><<<grid, kWaves * 64, 0, s>>>(a);
+  else paged_decode_kernel<DTYPE, D, false, false><<<grid, kWaves * 64, 0, s>>>(a);
   return check_launch("mv_paged_decode");
 }
 
@@ -1193,6 +1240,8 @@ struct NewRows {
   const void* value;
   int64_t value_stride_tok, value_stride_head;  // elements
   const int64_t* slots;
+  const void* rope_cos;  // [num_seqs][head_dim] rows, or null (no RoPE)
+  const void* rope_sin;
 };
 
 }  // namespace
@@ -1435,6 +1484,8 @@ int decode_launch(const void* query, int64_t q_stride_tok, int64_t q_stride_head
   a.nk_st = a.nk_sh = a.nv_st = a.nv_sh = 0;
   a.slots = nullptr;
   a.total_slots = num_blocks * block_size;
+  a.rope_cos = nullptr;
+  a.rope_sin = nullptr;
   if (nr) {
     if (!nr->key || !nr->value || !nr->slots)
       return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode_write: null new rows or slots");
@@ -1449,6 +1500,12 @@ int decode_launch(const void* query, int64_t q_stride_tok, int64_t q_stride_head
     a.nv_st = nr->value_stride_tok * eb;
     a.nv_sh = nr->value_stride_head * eb;
     a.slots = nr->slots;
+    if ((nr->rope_cos == nullptr) != (nr->rope_sin == nullptr))
+      return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode_write: give both RoPE rows or neither");
+    if ((reinterpret_cast<uintptr_t>(nr->rope_cos) | reinterpret_cast<uintptr_t>(nr->rope_sin)) % 16)
+      return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_decode_write: RoPE rows not 16-byte aligned");
+    a.rope_cos = static_cast<const char*>(nr->rope_cos);
+    a.rope_sin = static_cast<const char*>(nr->rope_sin);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
@@ -1555,14 +1612,15 @@ extern "C" int mv_paged_decode_noalloc(const void* query, int64_t q_stride_tok,
 extern "C" int mv_paged_decode_write(
     const void* query, int64_t q_stride_tok, int64_t q_stride_head, const void* new_key,
     int64_t nk_stride_tok, int64_t nk_stride_head, const void* new_value, int64_t nv_stride_tok,
-    int64_t nv_stride_head, const int64_t* slot_mapping, void* key_cache, void* value_cache,
+    int64_t nv_stride_head, const int64_t* slot_mapping, const void* rope_cos_rows,
+    const void* rope_sin_rows, void* key_cache, void* value_cache,
     const int32_t* work_items, const int32_t* block_ids, int64_t block_ids_capacity,
     int32_t num_work_groups, int32_t partition_tokens, int32_t max_partitions, int32_t* counters,
     void* out, int64_t out_stride_tok, int64_t out_stride_head, float scale, int32_t num_seqs,
     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
     int64_t num_blocks, int32_t dtype, void* workspace, size_t workspace_bytes, void* stream) {
   const mv::NewRows nr{new_key, nk_stride_tok, nk_stride_head, new_value, nv_stride_tok,
-                       nv_stride_head, slot_mapping};
+                       nv_stride_head, slot_mapping, rope_cos_rows, rope_sin_rows};
   return mv::decode_launch(query, q_stride_tok, q_stride_head, key_cache, value_cache, work_items,
                            block_ids, block_ids_capacity, num_work_groups, partition_tokens,
                            max_partitions, counters, out, out_stride_tok, out_stride_head, scale,

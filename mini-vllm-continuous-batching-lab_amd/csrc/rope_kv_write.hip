@@ -12,12 +12,7 @@
 // asks (prefill attention reads the new keys).
 //
 // Numerics are those of the reference's eager PyTorch ops in the tensors'
-// dtype. `x * cos + rotate_half(x) * sin` is three rounded operations,
-//   t1 = fl(x * c), t2 = fl(r * s), out = fl(t1 + t2),
-// each evaluated in fp32 and rounded to the storage type (what torch does
-// for bf16 / fp16 elementwise ops; for fp32 they are single IEEE operations,
-// with no fused multiply-add), where r = rotate_half(x) = [-x2, x1]. The
-// outputs are therefore bit-identical to the reference's.
+// dtype (mv_rope.h): the outputs are bit-identical to the reference's.
 //
 // Work split: a thread owns E = 16 / sizeof(elem) rotary pairs (d, d + D/2)
 // of one (token, head): two 16-byte chunks of x, the matching chunks of the
@@ -25,6 +20,7 @@
 // key_out). Query heads, key heads, then 16-byte value chunks (a bitwise
 // copy into the cache) share one grid.
 #include "mv_common.h"
+#include "mv_rope.h"
 
 namespace mv {
 namespace {
@@ -47,31 +43,6 @@ struct RopeArgs {
   int64_t total_slots;
   int32_t num_tokens, num_q_heads, num_kv_heads, head_dim, block_size, bs_log2;
 };
-
-template <typename T> struct Chunk16 { T e[16 / sizeof(T)]; };
-
-template <int DTYPE>
-__device__ __forceinline__ Chunk16<typename Elem<DTYPE>::raw> load16(const char* p) {
-  const uint4 v = *reinterpret_cast<const uint4*>(p);
-  return __builtin_bit_cast(Chunk16<typename Elem<DTYPE>::raw>, v);
-}
-
-template <int DTYPE>
-__device__ __forceinline__ void store16(char* p, const Chunk16<typename Elem<DTYPE>::raw>& c) {
-  *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, c);
-}
-
-// fl(fl(a * b) +/- fl(c * d)) in the storage type, without contraction.
-// The first half's term fl(fl(x1 c) + fl(-x2 s)) is taken as
-// fl(fl(x1 c) - fl(x2 s)): round-to-nearest-even is symmetric, so
-// fl(-x2 s) = -fl(x2 s), and t1 + (-t2) is t1 - t2 exactly.
-template <int DTYPE, bool SUB>
-__device__ __forceinline__ typename Elem<DTYPE>::raw rot_term(float a, float b, float c, float d) {
-#pragma clang fp contract(off)
-  const float t1 = to_f32<DTYPE>(from_f32<DTYPE>(a * b));
-  const float t2 = to_f32<DTYPE>(from_f32<DTYPE>(c * d));
-  return from_f32<DTYPE>(SUB ? t1 - t2 : t1 + t2);
-}
 
 __device__ __forceinline__ int64_t cache_row(const RopeArgs& a, int64_t slot, int h) {
   const int64_t blk = slot >> a.bs_log2;

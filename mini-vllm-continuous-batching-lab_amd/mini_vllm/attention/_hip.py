@@ -117,7 +117,8 @@ SIGNATURES = {
         _P, _I64, _I64,            # query, strides
         _P, _I64, _I64,            # new_key, strides
         _P, _I64, _I64,            # new_value, strides
-        _P, _P, _P,                # slot_mapping, key_cache, value_cache
+        _P, _P, _P,                # slot_mapping, rope_cos_rows, rope_sin_rows
+        _P, _P,                    # key_cache, value_cache
         _P, _P, _I64, _I32,        # work_items, block_ids, block_ids_capacity, num_work_groups
         _I32, _I32, _P,            # partition_tokens, max_partitions, counters
         _P, _I64, _I64,            # out, strides

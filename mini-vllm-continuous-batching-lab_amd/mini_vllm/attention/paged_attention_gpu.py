@@ -527,6 +527,40 @@ def plan_decode(
     return plan
 
 
+def _rope_rows(positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, head_dim: int,
+               dtype: torch.dtype, device: torch.device,
+               capture: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The cos / sin table rows at each decode token's position,
+    ``[B, head_dim]`` contiguous, for the decode kernel's fused RoPE;
+    gathered once per distinct (unmodified) positions / tables (the layers
+    of a step share them) after the positions check (``IndexError``, as the
+    reference's table lookup raises)."""
+    name = "rope_rows_graph" if capture else "rope_rows"
+    extra = (head_dim, dtype, device, capture)
+    hit = _cache_get(name, (positions, cos, sin), extra)
+    if hit is not None:
+        return hit
+    assert cos.dim() == 2 and cos.shape == sin.shape and cos.shape[1] >= head_dim, (
+        f"rotary tables {tuple(cos.shape)} / {tuple(sin.shape)} do not cover head_dim {head_dim}"
+    )
+    assert cos.dtype == dtype and sin.dtype == dtype, f"rotary tables {cos.dtype} != {dtype}"
+    assert cos.device == device and sin.device == device
+    pos = positions
+    if pos.device != device:
+        pos = pos.to(device)
+    if pos.dtype != torch.int64:
+        pos = pos.to(torch.int64)
+    pos = pos.contiguous()
+    _check_positions(pos, cos.shape[0])
+    # out-of-range positions are reported by the check; clamped here so the
+    # gather itself stays inside the tables
+    idx = pos.clamp(0, cos.shape[0] - 1)
+    rows = (cos.index_select(0, idx)[:, :head_dim].contiguous(),
+            sin.index_select(0, idx)[:, :head_dim].contiguous())
+    _cache_put(name, (positions, cos, sin), extra, rows)
+    return rows
+
+
 def hip_decode_attention(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -538,6 +572,9 @@ def hip_decode_attention(
     new_key: Optional[torch.Tensor] = None,
     new_value: Optional[torch.Tensor] = None,
     slot_mapping: Optional[torch.Tensor] = None,
+    positions: Optional[torch.Tensor] = None,
+    cos: Optional[torch.Tensor] = None,
+    sin: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Paged decode attention on the HIP kernels.
 
@@ -564,6 +601,15 @@ def hip_decode_attention(
     detected on the device and runs as the two calls; inside a captured
     graph it is reported by ``check_deferred()`` (``AssertionError``)
     instead. The cross-sequence condition is not checked.
+
+    With ``positions`` ``[total_decode]`` and the rotary tables ``cos`` /
+    ``sin`` (``[max_positions, >= head_dim]``, the query dtype) as well, the
+    same launch first applies the rotary embedding to ``query`` and
+    ``new_key`` (reference rotary.py:44-82, the reference's rounding): the
+    runner's ``q = rope(q); k = rope(k); write_kv_cache(k, v);
+    decode_attention(q)`` for the decode rows (qwen_runner.py:164-190), with
+    output and pool bit-identical to ``hip_rope_kv_cache_write`` followed by
+    this call on the rotated query.
     """
     # (The per-call checks read each attribute once: this wrapper runs once
     # per layer, and its host time exceeds the kernel's when it does not.)
@@ -620,17 +666,31 @@ def hip_decode_attention(
             slot_mapping = slot_mapping.to(torch.int64)
         slot_mapping = slot_mapping.contiguous()
         _check_slots(slot_mapping, num_blocks * block_size, capture=capture)
+        rope = positions is not None
+        if rope:
+            assert cos is not None and sin is not None
+            assert positions.shape == (total_decode,)
         if not _fused_write_ok(slot_mapping, block_table, kv_len_after, block_size, device,
                                capture):
-            hip_cache_write(new_key, new_value, key_cache, value_cache, slot_mapping, block_size)
+            if rope:  # the unfused sequence: rope + write, then decode of the rotated query
+                query, _ = hip_rope_kv_cache_write(query, new_key, new_value, positions, cos, sin,
+                                                   key_cache, value_cache, slot_mapping,
+                                                   block_size, return_key=False)
+            else:
+                hip_cache_write(new_key, new_value, key_cache, value_cache, slot_mapping,
+                                block_size)
             return hip_decode_attention(query, key_cache, value_cache, block_table, kv_len_after,
                                         block_size)
+        rope_cos = rope_sin = None
+        if rope:
+            rope_cos, rope_sin = _rope_rows(positions, cos, sin, head_dim, dtype, device, capture)
         nk, nv = _aligned_rows(new_key), _aligned_rows(new_value)
         _hip.check(
             lib.mv_paged_decode_write(
                 _ptr(query), query.stride(0), query.stride(1),
                 _ptr(nk), nk.stride(0), nk.stride(1), _ptr(nv), nv.stride(0), nv.stride(1),
-                _ptr(slot_mapping), _ptr(key_cache), _ptr(value_cache),
+                _ptr(slot_mapping), _ptr(rope_cos), _ptr(rope_sin), _ptr(key_cache),
+                _ptr(value_cache),
                 _ptr(plan.work), _ptr(plan.block_ids), plan.block_ids.numel(), plan.num_groups,
                 plan.partition_tokens, plan.max_parts, _ptr(plan.counters),
                 _ptr(output), output.stride(0), output.stride(1),
@@ -1296,6 +1356,39 @@ class AttentionBackendGPU(AttentionBackend):
             query, pool.key_caches[layer_idx], pool.value_caches[layer_idx],
             attn_metadata.decode_block_tables, group.kv_len_after, pool.block_size,
             new_key=key, new_value=value, slot_mapping=slot_mapping,
+        )
+
+    def decode_attention_with_rope_write(
+        self,
+        layer_idx: int,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        positions: torch.Tensor,
+        rope: Any,
+        slot_mapping: torch.Tensor,
+        attn_metadata: AttentionMetadata,
+        pool: KVCachePool,
+    ) -> torch.Tensor:
+        """The whole attention sub-layer of the decode rows in one launch:
+        ``q = rope(q, positions); k = rope(k, positions);
+        write_kv_cache(layer, k, v, slot_mapping); decode_attention(layer,
+        q, ...)`` (the runner's calls, qwen_runner.py:164-190, for the decode
+        rows ``q[P:]``, ``k[P:]`` ... with their positions and slots). ``query``
+        and ``key`` are not yet rotated; ``rope`` is the runner's
+        ``RotaryEmbedding`` (its ``cos`` / ``sin`` tables). Output and pool
+        are bit-identical to those calls."""
+        if query.shape[0] == 0:
+            return query
+        group = _find_group(attn_metadata, ("decode_gpu",))
+        if group is None:
+            self.rope_write_kv_cache(layer_idx, query, key, value, positions, rope, slot_mapping)
+            return query
+        return hip_decode_attention(
+            query, pool.key_caches[layer_idx], pool.value_caches[layer_idx],
+            attn_metadata.decode_block_tables, group.kv_len_after, pool.block_size,
+            new_key=key, new_value=value, slot_mapping=slot_mapping,
+            positions=positions, cos=rope.cos, sin=rope.sin,
         )
 
     def prefill_attention(

@@ -147,3 +147,103 @@ def test_backend_method_replaces_runner_calls():
     assert torch.equal(bits(k_rot.cpu()), bits(k_ref))
     assert torch.equal(bits(pool.key_caches[1].cpu()), bits(kc_ref))
     assert torch.equal(bits(pool.value_caches[1].cpu()), bits(vc_ref))
+
+
+# ---- the whole decode sub-layer in one launch: RoPE + KV write + decode ----
+
+@pytest.mark.parametrize("name,dtype", [("c1", torch.float32), ("c2", torch.bfloat16),
+                                        ("c2", torch.float16), ("c3", torch.bfloat16),
+                                        ("c4", torch.bfloat16), ("c5", torch.bfloat16),
+                                        ("c5", torch.float32)])
+def test_decode_with_fused_rope_equals_rope_write_then_decode(name, dtype):
+    """hip_decode_attention with new rows, slots and positions/cos/sin does
+    RoPE of q and the new k, the KV write and the decode in one launch; pool
+    and output are bit-identical to hip_rope_kv_cache_write followed by the
+    decode of the rotated query, and the decode matches the oracle (rotate,
+    write, decode on the CPU) within the dtype tolerance. q, k and v are
+    column views of one fused QKV buffer; unread and about-to-be-written
+    pool rows hold NaN."""
+    from benchmarks.paged_decode_workloads import make_case
+    from gpu_util import TOL, to_device
+    from mini_vllm.attention.paged_attention_gpu import hip_decode_attention
+    from oracle import paged_ref
+
+    say("decode + fused rope + write", name, dtype)
+    case = make_case(name, seed=6, dtype=dtype, nan_fill=True)
+    d = to_device(case)
+    spec = case.layout.spec
+    b, hq, hd = d.query.shape
+    hkv = spec.num_kv_heads
+    qkv = torch.cat([d.query.reshape(b, -1), d.new_key.reshape(b, -1),
+                     d.new_value.reshape(b, -1)], dim=1)
+    q = qkv[:, : hq * hd].view(b, hq, hd)
+    k = qkv[:, hq * hd:(hq + hkv) * hd].view(b, hkv, hd)
+    v = qkv[:, (hq + hkv) * hd:].view(b, hkv, hd)
+    pos = (d.kv_len - 1).clamp(max=MAX_POS - 1)
+    tables = _tables(hd, dtype)
+    cos, sin = tables.cos.to(DEV), tables.sin.to(DEV)
+    bs = spec.block_size
+    # two calls: fused RoPE + write, then decode of the rotated query
+    kc1, vc1 = d.key_cache.clone(), d.value_cache.clone()
+    q_rot, _ = hip_rope_kv_cache_write(q, k, v, pos, cos, sin, kc1, vc1, d.slot_mapping, bs,
+                                       return_key=False)
+    out1 = hip_decode_attention(q_rot, kc1, vc1, d.block_table, d.kv_len, bs)
+    # one launch
+    kc2, vc2 = d.key_cache.clone(), d.value_cache.clone()
+    out2 = hip_decode_attention(q, kc2, vc2, d.block_table, d.kv_len, bs, new_key=k, new_value=v,
+                                slot_mapping=d.slot_mapping, positions=pos, cos=cos, sin=sin)
+    torch.cuda.synchronize()
+    for x, y in ((out1, out2), (kc1, kc2), (vc1, vc2)):
+        assert torch.equal(bits(x.cpu()), bits(y.cpu()))
+    # the oracle: the runner's rotate / rotate / write / decode on the CPU
+    kc_ref, vc_ref = case.key_cache.float().clone(), case.value_cache.float().clone()
+    cpu_tab = _tables(hd, dtype)
+    q_r = rotary(case.query, pos.cpu(), cpu_tab).float()
+    k_r = rotary(case.new_key, pos.cpu(), cpu_tab).float()
+    paged_ref.write_to_paged_cache(k_r, case.new_value.float(), kc_ref, vc_ref, case.slot_mapping,
+                                   bs)
+    want = paged_ref.decode_from_tables(q_r, kc_ref, vc_ref, case.block_table, case.kv_len, bs)
+    got = out2.float().cpu()
+    assert not torch.isnan(got).any()
+    assert (got - want).abs().max().item() <= TOL[dtype]
+    assert torch.equal(bits(kc2.cpu().float()), bits(kc_ref))
+
+
+def test_backend_sub_layer_method():
+    """AttentionBackendGPU.decode_attention_with_rope_write: the runner's
+    rope / rope / write / decode of the decode rows in one call."""
+    from benchmarks.paged_decode_workloads import make_case
+    from gpu_util import to_device
+    from mini_vllm.attention.paged_attention_gpu import hip_decode_attention
+    from mini_vllm.model_runner.base import AttentionGroup, AttentionMetadata
+
+    say("backend decode_attention_with_rope_write")
+    case = make_case("c1", seed=7, dtype=torch.bfloat16, nan_fill=True)
+    d = to_device(case)
+    spec = case.layout.spec
+    dt = case.query.dtype
+    cfg = ModelConfig(num_layers=1, num_heads=spec.num_q_heads, num_kv_heads=spec.num_kv_heads,
+                      head_dim=spec.head_dim, dtype=dt)
+    be = AttentionBackend.create(cfg, backend="hip")
+    pool = be.allocate_pool(1, case.layout.num_blocks, spec.block_size, spec.num_kv_heads,
+                            spec.head_dim, dt, DEV)
+    pool.key_caches[0].copy_(d.key_cache)
+    pool.value_caches[0].copy_(d.value_cache)
+    kv = d.kv_len
+    meta = AttentionMetadata(
+        groups=[AttentionGroup(list(range(len(kv))), "decode_gpu", kv - 1, torch.ones_like(kv), kv)],
+        decode_block_tables=d.block_table, decode_slot_mapping=d.slot_mapping,
+        block_size=spec.block_size, num_kv_heads=spec.num_kv_heads, head_dim=spec.head_dim)
+    tables = _tables(spec.head_dim, dt)
+    tables.cos, tables.sin = tables.cos.to(DEV), tables.sin.to(DEV)
+    pos = kv - 1
+    out = be.decode_attention_with_rope_write(0, d.query, d.new_key, d.new_value, pos, tables,
+                                              d.slot_mapping, meta, pool)
+    kc, vc = d.key_cache.clone(), d.value_cache.clone()
+    q_rot, _ = hip_rope_kv_cache_write(d.query, d.new_key, d.new_value, pos, tables.cos,
+                                       tables.sin, kc, vc, d.slot_mapping, spec.block_size,
+                                       return_key=False)
+    ref = hip_decode_attention(q_rot, kc, vc, d.block_table, kv, spec.block_size)
+    torch.cuda.synchronize()
+    for x, y in ((ref, out), (kc, pool.key_caches[0]), (vc, pool.value_caches[0])):
+        assert torch.equal(bits(x.cpu()), bits(y.cpu()))

@@ -8,12 +8,15 @@ layer, on one step's token rows [prefill tokens | decode tokens]:
   3. decode_attention(layer, q[P:], decode_meta, pool) with the metadata
      _build_decode_meta rebases to 0-based decode rows (:213-251);
   4. attn_out[:P], attn_out[P:] = the two results.
-Here three layers of one pool run that sequence in three forms:
+Here three layers of one pool run that sequence in four forms:
   * "write": write_kv_cache of all rows (q, k already rotated), as listed;
   * "rope": rope_write_kv_cache (fused RoPE of q and k + the write);
   * "fused": write_kv_cache of the prefill rows, then
     decode_attention_with_write of the decode rows (the decode write inside
-    the decode launch).
+    the decode launch);
+  * "sublayer": rope_write_kv_cache of the prefill rows, then
+    decode_attention_with_rope_write of the decode rows (RoPE, write and
+    decode of the decode rows in one launch).
 Every layer's attention output is checked against the oracle (the
 reference's CPU backend restated: write, then prefill from the pool, then
 decode) within the dtype tolerance, and its pool bit for bit. Pool rows no
@@ -151,7 +154,7 @@ def _oracle(lay, layers, tables, form):
     for L in layers:
         kc, vc = L["kc"].float().clone(), L["vc"].float().clone()
         q, k, v = (x.float() for x in _split(L["qkv"]))
-        if form == "rope":
+        if form in ("rope", "sublayer"):
             dt = L["qkv"].dtype
             # the reference rounds after every op in the model dtype
             tab = rotary_ref.RotaryTables(D, THETA, MAX_POS, dtype=dt)
@@ -205,6 +208,17 @@ class _Step:
         outs = []
         for layer in range(LAYERS):
             q, k, v = _split(self.qkv[layer])
+            if self.form == "sublayer":
+                q_pre, k_pre = be.rope_write_kv_cache(
+                    layer, q[:p], k[:p], v[:p], self.positions[:p], self.rope, self.slots[:p],
+                    return_key=True)
+                attn_out = torch.zeros_like(q)
+                attn_out[:p] = be.prefill_attention(layer, q_pre, k_pre, v[:p], self.meta, pool)
+                attn_out[p:] = be.decode_attention_with_rope_write(
+                    layer, q[p:], k[p:], v[p:], self.positions[p:], self.rope, self.slots[p:],
+                    self.decode_meta, pool)
+                outs.append(attn_out)
+                continue
             if self.form == "rope":
                 q, k = be.rope_write_kv_cache(layer, q, k, v, self.positions, self.rope,
                                               self.slots, return_key=True)
@@ -231,7 +245,7 @@ class _Step:
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("form", ["write", "rope", "fused"])
+@pytest.mark.parametrize("form", ["write", "rope", "fused", "sublayer"])
 def test_mixed_step_eager(dtype, form):
     say("runner mixed step eager", form, dtype)
     lay = _layout(7, 64)
@@ -245,7 +259,7 @@ def test_mixed_step_eager(dtype, form):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("form", ["write", "rope", "fused"])
+@pytest.mark.parametrize("form", ["write", "rope", "fused", "sublayer"])
 def test_mixed_step_captured(dtype, form):
     """The whole 3-layer mixed step captured in one HIP graph (prefill
     planned on the device, decode plan of fixed size, checks deferred), then
