@@ -2,7 +2,9 @@
 
 Usage: ``python build_lib.py`` (or ``build()`` from Python). The library
 lands in ``lib/libmvattn.so`` next to this file, where
-``mini_vllm.attention._hip`` loads it.
+``mini_vllm.attention._hip`` loads it. A measurement variant builds
+elsewhere: ``python build_lib.py --define MV_DECODE_QK_VALU --out
+/tmp/libmvattn_valu.so``, loaded with ``MVATTN_LIB=/tmp/libmvattn_valu.so``.
 """
 
 from __future__ import annotations
@@ -48,15 +50,27 @@ def hipcc() -> str:
     return found
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source into lib/libmvattn.so; returns the library path."""
-    os.makedirs(LIB_DIR, exist_ok=True)
+# Build-time variants (``--define NAME``), each measured against the default:
+#   MV_DECODE_QK_VALU  the decode's K Q^T on VALU dot products instead of MFMA
+VARIANT_DEFINES = ("MV_DECODE_QK_VALU",)
+
+
+def build(verbose: bool = False, defines=(), out: str = LIB_PATH) -> str:
+    """Compile every source into ``out`` (default lib/libmvattn.so); returns
+    its path. ``defines``: names from ``VARIANT_DEFINES``; a variant library
+    is loaded through ``MVATTN_LIB``."""
+    for d in defines:
+        if d not in VARIANT_DEFINES:
+            raise ValueError(f"unknown build variant {d!r} (known: {', '.join(VARIANT_DEFINES)})")
+    out_dir = os.path.dirname(os.path.abspath(out))
+    os.makedirs(out_dir, exist_ok=True)
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
     # Build to a temporary name, then rename: a process that already mapped
     # the old library keeps a consistent file.
-    fd, tmp = tempfile.mkstemp(prefix="libmvattn.", suffix=".so.tmp", dir=LIB_DIR)
+    fd, tmp = tempfile.mkstemp(prefix="libmvattn.", suffix=".so.tmp", dir=out_dir)
     os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, *srcs, "-o", tmp]
+    cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), "-I", INCLUDE, "-I", CSRC,
+           *srcs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -69,9 +83,18 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    import argparse
+
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--define", action="append", default=[], choices=VARIANT_DEFINES,
+                    help="build a variant (load it with MVATTN_LIB=<out>)")
+    ap.add_argument("--out", default=LIB_PATH)
+    args = ap.parse_args()
+    if args.define and os.path.abspath(args.out) == LIB_PATH:
+        ap.error("a variant needs --out: lib/libmvattn.so is the default build")
+    print(build(verbose=True, defines=args.define, out=args.out))

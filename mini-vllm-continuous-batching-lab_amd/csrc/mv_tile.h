@@ -9,6 +9,10 @@
 namespace mv {
 namespace {
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 constexpr int kTile = 16;       // tokens per K/V tile (MFMA M of S^T)
 constexpr int kMaxGroup = 16;   // MFMA N: query rows per tile
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -56,6 +60,27 @@ __device__ __forceinline__ f32x4 mfma_qk<MV_DTYPE_F32>(const uint4& k, const uin
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.y), __uint_as_float(q.y), acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.z), __uint_as_float(q.z), acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(k.w), __uint_as_float(q.w), acc, 0, 0, 0);
+  return acc;
+}
+
+// acc + the dot product of two 16-byte pieces (8 16-bit or 4 fp32 elements)
+// on the VALU: v_dot2 with fp32 accumulation for the 16-bit types, plain
+// FMAs for fp32.
+template <int DTYPE>
+__device__ __forceinline__ float dot_piece(const uint4& a, const uint4& b, float acc) {
+  const uint32_t x[4] = {a.x, a.y, a.z, a.w}, y[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (DTYPE == MV_DTYPE_BF16) {
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x[i]),
+                                             __builtin_bit_cast(bf16x2_t, y[i]), acc, false);
+    } else if constexpr (DTYPE == MV_DTYPE_F16) {
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x[i]), __builtin_bit_cast(f16x2_t, y[i]),
+                                   acc, false);
+    } else {
+      acc = fmaf(__uint_as_float(x[i]), __uint_as_float(y[i]), acc);
+    }
+  }
   return acc;
 }
 
@@ -115,9 +140,6 @@ __device__ __forceinline__ uint4 swap_wave_halves(uint4 x, int lane) {
 // MFMA input type in two packed conversions, returned as the PV MFMA's A
 // operand; `sum` accumulates the rounded values (two dot2 with (1, 1)), so
 // O / l stays an exact convex combination of V rows.
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 template <int DTYPE>
 __device__ __forceinline__ s16x4 pack_p(float p0, float p1, float p2, float p3, float& sum) {
   static_assert(DTYPE != MV_DTYPE_F32, "16-bit types only");

@@ -386,13 +386,39 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   auto compute_tile = [&](int k, int st) __attribute__((always_inline)) {
     const char* k_tile = wave_tiles + st * Tr::kStageBytes;
     const char* v_tile = k_tile + Tr::kTileBytes;
-    // S^T = K Q^T: lane (g, t) reads row t, pieces g*QP .. g*QP+QP-1
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const int ksw = piece_swizzle<RP>(t);
+#if defined(MV_DECODE_QK_VALU)
+    if constexpr (!ROPE) {
+      // Build-time alternative for measurement (MFMA against VALU): S^T by
+      // VALU dot products, lane (g, t) computing tokens 4g..4g+3 of head t
+      // over all D dims, Q row t read from LDS, K rows through the swizzle.
+      // Lane t starts at piece t mod RP: the 16 Q rows sit 128 bytes apart,
+      // so reading one piece of every row at once hits the same banks (8-way
+      // at D = 64). Unrolled by 4 pieces: a full unroll hoists every LDS
+      // read of the tile ahead of the dot products and spills (468 B/lane at
+      // bf16 D=64), and so does holding the Q row in registers.
+      const char* q_row = s_lds + Tr::kQOffset + t * Tr::kRowBytes;
+#pragma unroll 4
+      for (int pi = 0; pi < RP; ++pi) {
+        const int pc = (pi + t) & (RP - 1);
+        const uint4 qv = *reinterpret_cast<const uint4*>(q_row + pc * 16);
 #pragma unroll
-    for (int c = 0; c < QP; ++c) {
-      const uint4 kp = *reinterpret_cast<const uint4*>(k_tile + (t * RP + ((g * QP + c) ^ ksw)) * 16);
-      acc = mfma_qk<DTYPE>(kp, qr[c], acc);
+        for (int e = 0; e < 4; ++e) {
+          const int row = 4 * g + e;
+          const uint4 kv = *reinterpret_cast<const uint4*>(k_tile + (row * RP + (pc ^ piece_swizzle<RP>(row))) * 16);
+          acc[e] = dot_piece<DTYPE>(kv, qv, acc[e]);
+        }
+      }
+    } else
+#endif
+    {
+      // S^T = K Q^T on MFMA: lane (g, t) reads row t, pieces g*QP .. g*QP+QP-1
+      const int ksw = piece_swizzle<RP>(t);
+#pragma unroll
+      for (int c = 0; c < QP; ++c) {
+        const uint4 kp = *reinterpret_cast<const uint4*>(k_tile + (t * RP + ((g * QP + c) ^ ksw)) * 16);
+        acc = mfma_qk<DTYPE>(kp, qr[c], acc);
+      }
     }
     const int tile_tok = tok_begin + k * Tr::kChunk + wave * kTile;
     float s[4];
