@@ -453,6 +453,8 @@ def plan_decode(
     stream's capture id (0: not capturing), when the caller already knows it.
     """
     lib = _hip.load()
+    if device.index is None:  # "cuda" and "cuda:<current>" are one device: one cached plan
+        device = torch.device(device.type, torch.cuda.current_device())
     split = _groups_per_cu(device, head_dim, dtype)
     if capture is None:
         capture = _capture_id(device)

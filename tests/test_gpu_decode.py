@@ -248,6 +248,9 @@ def _assert_counters_at_rest(c):
         hip_decode_attention(d.query, d.key_cache, d.value_cache, d.block_table, d.kv_len,
                              spec.block_size)
         torch.cuda.synchronize()
+        # the call ran on this plan (the same cached object)
+        assert pg.plan_decode(d.block_table, d.kv_len, spec.block_size, d.key_cache.shape[0], DEV,
+                              spec.head_dim, spec.dtype, spec.num_kv_heads) is plan
         assert int(torch.count_nonzero(plan.counters)) == 0
 
 
