@@ -746,7 +746,7 @@ constexpr int kWaveSearchSeqs = 256; // one wave runs the piece-bound search up 
 constexpr int kIdsThreads = 256;     // block-id kernel: threads per work group
 constexpr int kIdsQuads = 4;         // block-id kernel: 4-id quads per thread per pass
 constexpr int kIdsPerPass = kIdsThreads * kIdsQuads * 4;
-static_assert(kPlanThreads == kDealMax, "the sort holds one key per thread");
+static_assert(kPlanThreads == kDealMax, "the deal holds one group (and one bucket) per thread");
 
 // Value-returning min / max: std::min / std::max return a reference, and
 // a reference to one of two temporaries makes the compiler keep both on
@@ -805,21 +805,6 @@ __device__ inline int64_t wave_sum64(int64_t v) {
   const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), 63);
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
-// The partner's key in a bitonic compare-exchange at distance j < 64.
-__device__ inline uint32_t xor_partner(uint32_t x, int j, int lane) {
-  const int v = static_cast<int>(x);
-  switch (j) {
-    case 1: return static_cast<uint32_t>(dpp<0xB1>(v, v));  // quad_perm [1,0,3,2]
-    case 2: return static_cast<uint32_t>(dpp<0x4E>(v, v));  // quad_perm [2,3,0,1]
-    case 4: {
-      const int up = dpp<0x104>(v, v), down = dpp<0x114>(v, v);  // lane i+4, lane i-4
-      return static_cast<uint32_t>((lane & 4) ? down : up);
-    }
-    case 8: return static_cast<uint32_t>(dpp<0x128>(v, v));  // row_ror:8 = lane i ^ 8
-    default: return static_cast<uint32_t>(__shfl_xor(v, j));
-  }
-}
-
 // Work-group sum of one value per thread. The trailing barrier lets the
 // next call reuse the scratch.
 __device__ int64_t block_sum64(int64_t v, int64_t* scratch) {
@@ -842,11 +827,18 @@ __host__ __device__ inline int ids_per_item(int64_t part_tokens, int bs_log2) {
 }
 
 // Token range of piece j of a sequence of kv tokens cut into np pieces:
-// equal shares of its 16-token tiles.
+// equal shares of its 16-token tiles (32-bit arithmetic when j * tiles
+// fits, which holds for every table of fewer than 2^16 tiles).
 __device__ inline int2 piece_range(int kv, int np, int j) {
   const int tiles = (kv + kTile - 1) / kTile;
-  const int t0 = static_cast<int>(static_cast<int64_t>(j) * tiles / np) * kTile;
-  const int t1 = static_cast<int>(static_cast<int64_t>(j + 1) * tiles / np) * kTile;
+  int t0, t1;
+  if (tiles < (1 << 16)) {
+    t0 = static_cast<int>(static_cast<uint32_t>(j) * tiles / static_cast<uint32_t>(np)) * kTile;
+    t1 = static_cast<int>(static_cast<uint32_t>(j + 1) * tiles / static_cast<uint32_t>(np)) * kTile;
+  } else {
+    t0 = static_cast<int>(static_cast<int64_t>(j) * tiles / np) * kTile;
+    t1 = static_cast<int>(static_cast<int64_t>(j + 1) * tiles / np) * kTile;
+  }
   return make_int2(t0, min(kv, t1));
 }
 
@@ -884,7 +876,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   __shared__ int s_max_parts;
   __shared__ int s_lb;
   __shared__ int64_t s_groups;
-  __shared__ uint32_t s_key[2][kDealMax];                 // bitonic exchange buffers
+  __shared__ uint32_t s_key[2][kDealMax];                 // the deal's bucket counts and starts
   __shared__ int s_item_b[kDealMax], s_item_j[kDealMax];  // items (sequence, piece) when dealt
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -1052,52 +1044,51 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   }
   __syncthreads();  // items complete
 
-  // ---- 4. deal: sort groups by size (descending, then index) and place
-  // sorted position j in slot r * cu_count + c (round r = j / cu_count),
-  // forward or backward over c by round parity, ending forward so the last
+  // ---- 4. deal: order the groups by size (descending) and place sorted
+  // position p in slot r * cu_count + c (round r = p / cu_count), forward
+  // or backward over c by round parity, ending forward so the last
   // partial round fills slots [r * cu_count, r * cu_count + rem).
+  // Counting sort: bucket k = (L - size) >> shift of at most kDealMax
+  // buckets (exact sizes for L < kDealMax tiles), position = the bucket's
+  // start + the group's arrival order in it (groups of one size are
+  // interchangeable here; the results never depend on the placement).
   if (deal) {
-    uint32_t x = 0xFFFFFFFFu;
+    int* s_count = reinterpret_cast<int*>(s_key[0]);  // groups per bucket
+    int* s_start = reinterpret_cast<int*>(s_key[1]);  // first position of each bucket
+    int shift = 0;
+    while ((lb >> shift) >= kDealMax) ++shift;
+    s_count[tid] = 0;
+    __syncthreads();
+    int bucket = 0, within = 0, b = 0, h = 0, j = 0, np = 0;
+    int2 r = make_int2(0, 0);
     if (tid < num_groups) {
       const int item = tid / hkv;
-      const int b = s_item_b[item];
-      const int np = (tiles_of(b) + lb - 1) / lb;
-      const int2 r = piece_range(kv_of(b), np, s_item_j[item]);
-      const uint32_t t = static_cast<uint32_t>(vmin((r.y - r.x + kTile - 1) / kTile, 0xFFFFF));
-      x = ((0xFFFFFu - t) << 11) | static_cast<uint32_t>(tid);
+      h = tid - item * hkv;
+      b = s_item_b[item];
+      j = s_item_j[item];
+      np = (tiles_of(b) + lb - 1) / lb;
+      r = piece_range(kv_of(b), np, j);
+      const int size = vmin((r.y - r.x + kTile - 1) / kTile, lb);
+      bucket = (lb - size) >> shift;
+      within = atomicAdd(&s_count[bucket], 1);
     }
-    // bitonic sort of kDealMax keys, ascending, one key per thread:
-    // partners in the same wave exchange by DPP or shuffle, farther ones
-    // through alternating shared buffers (one barrier per exchange)
-    int buf = 0;
+    __syncthreads();
+    {  // exclusive scan of the bucket counts, one bucket per thread
+      const int cnt = s_count[tid];
+      const int incl = wave_scan_sum(cnt);
+      if (lane == 63) s_wsum[0][wave] = incl;
+      __syncthreads();
+      int before = 0;
 #pragma unroll
-    for (int k = 2; k <= kDealMax; k <<= 1) {
-#pragma unroll
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        uint32_t y;
-        if (j >= 64) {
-          s_key[buf][tid] = x;
-          __syncthreads();
-          y = s_key[buf][tid ^ j];
-          buf ^= 1;
-        } else {
-          y = xor_partner(x, j, lane);
-        }
-        const bool up = (tid & k) == 0, lower = (tid & j) == 0;
-        x = (lower == up) ? min(x, y) : max(x, y);
-      }
+      for (int w = 0; w < kPlanWaves; ++w) before += w < wave ? s_wsum[0][w] : 0;
+      s_start[tid] = before + incl - cnt;
     }
-    const int gs = static_cast<int>(x & 2047u);
-    if (tid < num_groups && gs < num_groups) {  // gs < num_groups: always, for a sorted list
-      const int item = gs / hkv;
-      const int h = gs - item * hkv;
-      const int b = s_item_b[item];
-      const int j = s_item_j[item];
-      const int np = (tiles_of(b) + lb - 1) / lb;
-      const int2 r = piece_range(kv_of(b), np, j);
+    __syncthreads();
+    if (tid < num_groups) {
+      const int pos = s_start[bucket] + within;
       const int cus = a.cu_count;
       const int rounds = static_cast<int>((num_groups + cus - 1) / cus);
-      const int rd = tid / cus, c = tid - rd * cus;
+      const int rd = pos / cus, c = pos - rd * cus;
       const bool forward = ((rounds - 1 - rd) & 1) == 0;
       const int slot = rd * cus + (forward ? c : cus - 1 - c);
       if (slot < a.work_cap) {

@@ -479,16 +479,21 @@ def plan_decode(
     else:
         cap = num_seqs * num_kv_heads * max(1, math.ceil(max_blocks * block_size / 16))
         ids_cap = lib.mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, cap)
-    work = torch.empty(8 * max(cap, 1), dtype=torch.int32, device=device)
-    block_ids = torch.empty(max(ids_cap, 4), dtype=torch.int32, device=device)
-    counters = torch.empty(max(num_seqs * num_kv_heads, 1), dtype=torch.int32, device=device)
-    status = torch.empty(_hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
+    # one allocation, cut into the work list, block ids, counters and
+    # status words (each part 16-byte aligned)
+    n_work, n_ids = 8 * max(cap, 1), -(-max(ids_cap, 4) // 4) * 4
+    n_cnt = -(-max(num_seqs * num_kv_heads, 1) // 4) * 4
+    buf = torch.empty(n_work + n_ids + n_cnt + _hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
+    work = buf[:n_work]
+    block_ids = buf[n_work:n_work + n_ids]
+    counters = buf[n_work + n_ids:n_work + n_ids + max(num_seqs * num_kv_heads, 1)]
+    status = buf[n_work + n_ids + n_cnt:]
     _hip.check(
         lib.mv_decode_plan(
             _ptr(kv), int(kv.dtype == torch.int64), _ptr(bt), int(bt.dtype == torch.int64),
             bt.stride(0) if bt.dim() == 2 else 0, num_seqs, max_blocks, block_size,
             num_blocks, num_kv_heads, *split, fixed,
-            _ptr(work), cap, _ptr(block_ids), block_ids.numel(),
+            _ptr(work), cap, _ptr(block_ids), n_ids,
             _ptr(counters), _ptr(status), _stream(device),
         ),
         "mv_decode_plan",
