@@ -744,8 +744,6 @@ constexpr int kDealMax = 1024;       // work groups sorted and dealt to CUs in s
 constexpr int kPlanSeqCache = 4096;  // kv lengths held in shared memory
 constexpr int kWaveSearchSeqs = 256; // one wave runs the piece-bound search up to this batch
 constexpr int kIdsThreads = 256;     // block-id kernel: threads per work group
-constexpr int kIdsQuads = 4;         // block-id kernel: 4-id quads per thread per pass
-constexpr int kIdsPerPass = kIdsThreads * kIdsQuads * 4;
 static_assert(kPlanThreads == kDealMax, "the deal holds one group (and one bucket) per thread");
 
 // Value-returning min / max: std::min / std::max return a reference, and
@@ -958,29 +956,70 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const int l_top = vmin(l_cap, vmax(l_min, most_tiles));
   const int l_fair = static_cast<int>(vmin<int64_t>(
       l_cap, vmax<int64_t>(l_min, (total_tiles * hkv + target - 1) / target)));
-  // smallest l in [l_min, l_top] whose groups fit the target (see above)
-  auto pick = [&](auto&& groups_at) -> int {
-    if (groups_at(l_top) > target) return l_fair;  // more sequences than slots: several rounds
-    int lo = l_min, hi = l_top;
+  // smallest l in [l_min, l_top] whose groups fit the target (see above).
+  // groups(l) = hkv * sum ceil(tiles_b / l) lies in [hkv * total / l,
+  // hkv * total / l + units), so no l below ceil(hkv * total / target)
+  // fits and every l from ceil(hkv * total / (target - units)) on does:
+  // the search runs between the two (a handful of steps, not log2(l_top)).
+  // `known` holds groups(hi) once evaluated (-1 before), so it returns
+  // groups(l) when the search evaluated it.
+  auto pick = [&](auto&& groups_at, int64_t& known) -> int {
+    known = -1;
+    int lo = vmin(l_fair, l_top), hi = l_top;
+    bool top_fits = false;
+    if (target > units) {
+      const int64_t l_fit = (total_tiles * hkv + (target - units) - 1) / (target - units);
+      if (l_fit <= l_top) {
+        hi = vmax(lo, static_cast<int>(l_fit));
+        top_fits = true;
+      }
+    }
+    if (!top_fits) {
+      known = groups_at(l_top);
+      if (known > target) {  // more sequences than slots: several rounds
+        known = -1;
+        return l_fair;
+      }
+    }
     while (lo < hi) {
       const int mid = lo + (hi - lo) / 2;
-      if (groups_at(mid) <= target) hi = mid;
-      else lo = mid + 1;
+      const int64_t g = groups_at(mid);
+      if (g <= target) {
+        hi = mid;
+        known = g;
+      } else {
+        lo = mid + 1;
+      }
     }
-    return lo > 2 * l_fair ? vmax(l_min, vmin(l_cap, 2 * l_fair)) : lo;
+    if (lo > 2 * l_fair) {
+      known = -1;
+      return vmax(l_min, vmin(l_cap, 2 * l_fair));
+    }
+    return lo;
   };
   int lb;
   int64_t num_groups;
   if (cached && a.num_seqs <= kWaveSearchSeqs) {
-    // one wave, lengths from shared memory, no barriers in the search
+    // one wave, no barriers in the search; the lane's (at most 4) tile
+    // counts stay in registers, and the count sums in 32 bits while it fits
+    // (a search step is then a few divisions and one 32-bit wave sum)
     if (wave == 0) {
+      static_assert(kWaveSearchSeqs <= 4 * 64, "4 sequences per lane");
+      int t4[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) t4[k] = lane + 64 * k < a.num_seqs ? tiles_of(lane + 64 * k) : 0;
+      const bool narrow = static_cast<int64_t>(a.num_seqs) * most_tiles < (int64_t(1) << 30);
+      const int per_lane = (a.num_seqs + 63) / 64;  // wave-uniform, at most 4
       auto groups_wave = [&](int l) -> int64_t {
-        int64_t n = 0;
-        for (int b = lane; b < a.num_seqs; b += 64) n += (tiles_of(b) + l - 1) / l;
-        return wave_sum64(n) * hkv;
+        int n = (t4[0] + l - 1) / l;
+#pragma unroll
+        for (int k = 1; k < 4; ++k)
+          if (k < per_lane) n += (t4[k] + l - 1) / l;
+        return (narrow ? static_cast<int64_t>(wave_sum(n)) : wave_sum64(n)) * hkv;
       };
-      const int l = pick(groups_wave);
-      const int64_t g = groups_wave(l);
+      int64_t g;
+      const int l = pick(groups_wave, g);
+      if (g < 0) g = groups_wave(l);
       if (lane == 0) {
         s_lb = l;
         s_groups = g;
@@ -995,8 +1034,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
       for (int b = tid; b < a.num_seqs; b += kPlanThreads) n += (tiles_of(b) + l - 1) / l;
       return block_sum64(n, s_red) * hkv;
     };
-    lb = pick(groups_block);
-    num_groups = groups_block(lb);
+    lb = pick(groups_block, num_groups);
+    if (num_groups < 0) num_groups = groups_block(lb);
   }
   const int part_tokens = lb * kTile;
 
@@ -1022,13 +1061,19 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
       chunk += t;
     }
     const int64_t start = running + before + incl - np;
-    for (int j = 0; j < np; ++j) {
-      const int64_t item = start + j;
-      if (deal) {
-        if (item >= kDealMax) break;  // cannot happen: items <= num_groups <= kDealMax
-        s_item_b[item] = b;
-        s_item_j[item] = j;
-      } else {
+    if (deal) {
+      // items < num_groups / hkv <= kDealMax; the wave-uniform trip count
+      // (the wave's most pieces) keeps this a scalar loop with one masked
+      // pair of LDS writes per step, not a divergent per-lane loop
+      const int first = static_cast<int>(start);
+      for (int j = 0; j < most; ++j)
+        if (j < np && first + j < kDealMax) {
+          s_item_b[first + j] = b;
+          s_item_j[first + j] = j;
+        }
+    } else {
+      for (int j = 0; j < np; ++j) {
+        const int64_t item = start + j;
         const int2 r = piece_range(kv_of(b), np, j);
         for (int h = 0; h < hkv; ++h) {
           const int64_t slot = item * hkv + h;
@@ -1042,6 +1087,14 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     }
     running += chunk;
   }
+  // the deal's buckets: (L - size) >> shift for piece sizes 1..L tiles,
+  // cleared here so the items barrier covers it
+  int* s_count = reinterpret_cast<int*>(s_key[0]);  // groups per bucket
+  int* s_start = reinterpret_cast<int*>(s_key[1]);  // first position of each bucket
+  int shift = 0;
+  while ((lb >> shift) >= kDealMax) ++shift;
+  const int buckets = ((lb - 1) >> shift) + 1;  // <= kDealMax
+  if (deal && tid < buckets) s_count[tid] = 0;
   __syncthreads();  // items complete
 
   // ---- 4. deal: order the groups by size (descending) and place sorted
@@ -1053,12 +1106,6 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   // start + the group's arrival order in it (groups of one size are
   // interchangeable here; the results never depend on the placement).
   if (deal) {
-    int* s_count = reinterpret_cast<int*>(s_key[0]);  // groups per bucket
-    int* s_start = reinterpret_cast<int*>(s_key[1]);  // first position of each bucket
-    int shift = 0;
-    while ((lb >> shift) >= kDealMax) ++shift;
-    s_count[tid] = 0;
-    __syncthreads();
     int bucket = 0, within = 0, b = 0, h = 0, j = 0, np = 0;
     int2 r = make_int2(0, 0);
     if (tid < num_groups) {
@@ -1073,8 +1120,15 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
       within = atomicAdd(&s_count[bucket], 1);
     }
     __syncthreads();
-    {  // exclusive scan of the bucket counts, one bucket per thread
-      const int cnt = s_count[tid];
+    // exclusive scan of the bucket counts, one bucket per thread: in one
+    // wave when the buckets fit it (L <= 64 tiles), else over the block
+    if (buckets <= 64) {
+      if (wave == 0) {
+        const int cnt = lane < buckets ? s_count[lane] : 0;
+        s_start[lane] = wave_scan_sum(cnt) - cnt;
+      }
+    } else {
+      const int cnt = tid < buckets ? s_count[tid] : 0;
       const int incl = wave_scan_sum(cnt);
       if (lane == 63) s_wsum[0][wave] = incl;
       __syncthreads();
@@ -1108,7 +1162,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const int per_item = ids_per_item(fixed ? a.fixed_part_tokens : part_tokens, a.bs_log2);
   const int64_t n_ids = used_groups * per_item;
   const bool listed = used_groups == num_groups && n_ids <= a.ids_cap &&
-                      n_ids <= INT_MAX - kIdsPerPass &&
+                      n_ids <= INT_MAX &&
                       (!fixed || part_tokens <= a.fixed_part_tokens);
   // A plan whose id lists do not fit is unusable: every slot is marked
   // unused, so a launch of it does nothing (no piece runs without its ids).
@@ -1153,6 +1207,7 @@ struct IdsArgs {
   int64_t bt_stride;
   int32_t num_seqs, max_blocks;
   const int32_t* work;
+  int64_t work_cap;
   int32_t* ids;
   int32_t* status;
   int64_t num_blocks;
@@ -1160,57 +1215,47 @@ struct IdsArgs {
 };
 
 // Step 5 of the plan, over many CUs: slot s's list ids[s * n, (s + 1) * n)
-// (n = status[MV_PLAN_IDS_PER_ITEM], a multiple of 4) holds the pool blocks
-// of its piece, -1 past its last block and for an entry outside the pool.
-// One thread writes 4 ids of one slot at a time. The pieces of kv head 0
-// read every block of every valid sequence, and a block belongs to the one
-// piece that holds its first token: counting the bad entries among those
-// reads checks each table entry a sequence needs exactly once.
+// (n = status[MV_PLAN_IDS_PER_ITEM], a multiple of 4, at most kIdCap)
+// holds the pool blocks of its piece, -1 past its last block and for an
+// entry outside the pool. One wave writes one slot's list, 4 ids per lane
+// per pass (n <= 2 passes of 256). The slot follows from blockIdx and the
+// wave alone, so its work entry loads beside the status word: two
+// dependent round trips (entry and status, then the table) before the
+// stores. The pieces of kv head 0 read every block of every valid
+// sequence, and a block belongs to the one piece that holds its first
+// token: counting the bad entries among those reads checks each table
+// entry a sequence needs exactly once.
 template <typename BT>
 __global__ __launch_bounds__(kIdsThreads) void decode_ids_kernel(IdsArgs a) {
-  const int per_item = a.status[MV_PLAN_IDS_PER_ITEM];  // -1: no list this step
-  const int groups = a.status[MV_PLAN_NUM_ITEMS];
-  if (per_item <= 0 || groups <= 0) return;
-  const int quads = groups * (per_item / 4);  // the plan bounds groups * per_item
-  const int quads_per_slot = per_item / 4;
+  constexpr int kSlotsPerGroup = kIdsThreads / 64;
+  const int lane = threadIdx.x & 63;
   const BT* btp = static_cast<const BT*>(a.block_table);
   int bad = 0;
-  for (int base = blockIdx.x * kIdsThreads * kIdsQuads; base < quads;
-       base += gridDim.x * kIdsThreads * kIdsQuads) {
-    int64_t blk[kIdsQuads][4];
-    bool own[kIdsQuads][4];
-#pragma unroll
-    for (int u = 0; u < kIdsQuads; ++u) {
-      const int q = base + u * kIdsThreads + threadIdx.x;
-      const bool live = q < quads;
-      const int slot = live ? q / quads_per_slot : 0;
-      const int k0 = live ? 4 * (q - slot * quads_per_slot) : 0;
-      const int4 w0 = reinterpret_cast<const int4*>(a.work + 8 * static_cast<int64_t>(slot))[0];
-      const int4 w1 = reinterpret_cast<const int4*>(a.work + 8 * static_cast<int64_t>(slot))[1];
-      const int first = w1.x >> a.bs_log2;
-      const int last = (w1.y - 1) >> a.bs_log2;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = first + k0 + e;
-        // the bounds hold for every entry the plan writes
-        const bool read = live && m <= last && m >= 0 && m < a.max_blocks && w0.x >= 0 &&
-                          w0.x < a.num_seqs;
-        own[u][e] = read && w0.y == 0 && (static_cast<int64_t>(m) << a.bs_log2) >= w1.x;
-        blk[u][e] = read ? static_cast<int64_t>(btp[w0.x * a.bt_stride + m]) : -1;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kIdsQuads; ++u) {
-      const int q = base + u * kIdsThreads + threadIdx.x;
+  for (int64_t slot = static_cast<int64_t>(blockIdx.x) * kSlotsPerGroup + (threadIdx.x >> 6);
+       slot < a.work_cap; slot += static_cast<int64_t>(gridDim.x) * kSlotsPerGroup) {
+    const int4 w0 = reinterpret_cast<const int4*>(a.work + 8 * slot)[0];
+    const int4 w1 = reinterpret_cast<const int4*>(a.work + 8 * slot)[1];
+    const int per_item = a.status[MV_PLAN_IDS_PER_ITEM];  // -1: no list this step
+    const int groups = a.status[MV_PLAN_NUM_ITEMS];
+    if (per_item <= 0 || slot >= groups) break;  // uniform per wave; later slots are larger
+    const int first = w1.x >> a.bs_log2;
+    const int last = (w1.y - 1) >> a.bs_log2;
+    // the bounds hold for every entry the plan writes
+    const bool seq_ok = w0.x >= 0 && w0.x < a.num_seqs;
+    const BT* row = btp + (seq_ok ? static_cast<int64_t>(w0.x) * a.bt_stride : 0);
+    int4* out = reinterpret_cast<int4*>(a.ids + slot * per_item);
+    for (int k0 = 4 * lane; k0 < per_item; k0 += 4 * 64) {
       int32_t v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const bool in_pool = blk[u][e] >= 0 && blk[u][e] < a.num_blocks;
-        bad += own[u][e] && !in_pool;
-        v[e] = in_pool ? static_cast<int32_t>(blk[u][e]) : -1;
+        const int m = first + k0 + e;
+        const bool read = seq_ok && m <= last && m >= 0 && m < a.max_blocks;
+        const int64_t blk = read ? static_cast<int64_t>(row[m]) : -1;
+        const bool in_pool = blk >= 0 && blk < a.num_blocks;
+        bad += read && w0.y == 0 && (static_cast<int64_t>(m) << a.bs_log2) >= w1.x && !in_pool;
+        v[e] = in_pool ? static_cast<int32_t>(blk) : -1;
       }
-      if (q < quads)
-        reinterpret_cast<int4*>(a.ids)[q] = make_int4(v[0], v[1], v[2], v[3]);
+      out[k0 >> 2] = make_int4(v[0], v[1], v[2], v[3]);
     }
   }
   if (bad) atomicAdd(&a.status[MV_PLAN_BAD_BLOCK], bad);
@@ -1391,13 +1436,15 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
     d.num_seqs = num_seqs;
     d.max_blocks = max_blocks;
     d.work = work_items;
+    d.work_cap = work_capacity;
     d.ids = block_ids;
     d.status = status;
     d.num_blocks = num_blocks;
     d.bs_log2 = a.bs_log2;
-    // enough work groups for the largest list the capacity admits, in one pass
+    // one wave per slot the work list can hold, in one pass up to 4096 work groups
+    constexpr int64_t kSlotsPerGroup = kIdsThreads / 64;
     const int grid = static_cast<int>(std::min<int64_t>(
-        1024, std::max<int64_t>(1, (block_ids_capacity + kIdsPerPass - 1) / kIdsPerPass)));
+        4096, std::max<int64_t>(1, (work_capacity + kSlotsPerGroup - 1) / kSlotsPerGroup)));
     if (bt_is_i64) decode_ids_kernel<int64_t><<<grid, kIdsThreads, 0, s>>>(d);
     else decode_ids_kernel<int32_t><<<grid, kIdsThreads, 0, s>>>(d);
   }

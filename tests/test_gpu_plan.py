@@ -154,3 +154,28 @@ def test_dealt_plan_fills_slots_round_robin():
     # every piece of the first round is at least as big as every later one
     if second:
         assert min(first_round) >= max(second)
+
+
+def test_bad_entry_in_a_second_id_pass_raises():
+    """Block size 1 and 16 sequences of 5000 tokens: pieces span over 300
+    table entries, so a slot's id list is written in two passes of 256.
+    One entry outside the pool, 300 entries into a piece (the second
+    pass), is counted and raises; the same table without it runs."""
+    n, kv_len, hkv = 16, 5000, 2
+    pool = n * kv_len + 8
+    bt = torch.arange(n * kv_len, dtype=torch.int32, device=DEV).view(n, kv_len)
+    kv = torch.full((n,), kv_len, dtype=torch.int32, device=DEV)
+    plan = plan_decode(bt, kv, 1, pool, DEV, 64, torch.bfloat16, hkv)
+    g = plan.num_groups
+    work = plan.work[: 8 * g].view(g, 8).cpu().tolist()
+    long = [(w[0], w[4], w[5]) for w in work if w[5] - w[4] > 300]
+    say("plan: bad entry in the second id pass,", g, "groups, P", plan.partition_tokens)
+    assert long, "no piece spans over 300 table entries"
+    b, t0, _ = long[0]
+    q = torch.randn(n, 14, 64, device=DEV).to(torch.bfloat16)
+    kc = torch.zeros(pool, hkv, 1, 64, dtype=torch.bfloat16, device=DEV)
+    out = hip_decode_attention(q, kc, kc, bt, kv, 1)
+    assert torch.isfinite(out.float()).all()
+    bt[b, t0 + 300] = pool
+    with pytest.raises(IndexError, match="pool blocks"):
+        hip_decode_attention(q, kc, kc, bt, kv, 1)
