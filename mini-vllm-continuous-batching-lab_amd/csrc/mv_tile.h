@@ -30,13 +30,27 @@ struct TileGeom {
   static constexpr int kElemsPerPiece = 16 / kElemBytes;
 };
 
-// Swizzle of the 16-byte pieces of LDS row r: slot s holds piece s ^ sw(r).
-// With it, a K-operand read (16 rows, one piece each) and a transposed V
-// read (rows 4g+e, two to four neighbouring pieces each) touch 16 distinct
-// 4-bank groups.
+// Swizzle of the 16-byte pieces of LDS row r (r < 16): slot s holds piece
+// s ^ sw(r). sw is the XOR of row bits that makes both reads of a tile
+// free of bank conflicts, whether the LDS serves 32 or 64 banks of 4 bytes
+// a cycle (found by an exhaustive search over such swizzles against a bank
+// model of the two reads):
+//   * the K-operand read, ds_read_b128: lane (g, t) reads row t, piece
+//     g * kLanePieces + c;
+//   * the transposed V read, ds_read_b64_tr_b16: lane (g, t) reads 8 bytes
+//     of row 4g + t/4, piece 2c + (t%4)/2 (v_column_tr below).
+// 8 pieces (head_dim 64, 16-bit): bits (r2, r1, r0^r2^r3); 16 pieces
+// (head_dim 128 16-bit, head_dim 64 fp32): bits (r2, r0, r1, r2^r3). The
+// earlier (r >> 1) & 7 and r & 15 left the V reads 2-way (64 banks) and 4-way
+// (32 banks) conflicted.
 template <int ROW_PIECES>
 __device__ __forceinline__ int piece_swizzle(int r) {
-  return ROW_PIECES == 8 ? (r >> 1) & 7 : r & 15;
+  if constexpr (ROW_PIECES == 8)
+    return ((r >> 2) & 1) | (r & 2) | (((r ^ (r >> 2) ^ (r >> 3)) & 1) << 2);
+  else if constexpr (ROW_PIECES == 16)
+    return ((r >> 2) & 1) | ((r & 1) << 1) | ((r & 2) << 1) | ((((r >> 2) ^ (r >> 3)) & 1) << 3);
+  else
+    return r & 15;
 }
 
 // S^T tile update: acc += K(16 tokens x 32 dims) * Q^T(32 dims x 16 heads)
