@@ -165,7 +165,9 @@ int mv_decode_write_check(const int64_t* slot_mapping, const void* block_table, 
  *               16) always suffices);
  *   block_ids   for slot s, int32 [s * n, (s + 1) * n) with
  *               n = status[MV_PLAN_IDS_PER_ITEM]: the pool blocks of the
- *               table entries its tokens lie in, -1 past the last;
+ *               table entries its tokens lie in (-1 for one outside the
+ *               pool), then -1 to a multiple of 4 entries; the rest of
+ *               the n entries is left unwritten (no launch reads it);
  *               16-byte aligned, block_ids_capacity >=
  *               mv_decode_block_ids_capacity(num_seqs, max_blocks,
  *               num_kv_heads, work_capacity) ints;

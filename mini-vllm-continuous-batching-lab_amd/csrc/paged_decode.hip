@@ -136,7 +136,7 @@ struct Traits : TileGeom<DTYPE, D> {
 // of wide scalar loads fetch them together.
 struct DecodeArgs {
   const int32_t* work;       // per work group: (seq, kv head, piece, pieces, token begin, end, 0, 0)
-  const int32_t* block_ids;  // [work group][ids_per_item]: the piece's pool blocks, -1 padded
+  const int32_t* block_ids;  // [work group][ids_per_item]: the piece's pool blocks first
   const void* q;
   const char* k_cache;
   const char* v_cache;
@@ -1216,9 +1216,12 @@ struct IdsArgs {
 
 // Step 5 of the plan, over many CUs: slot s's list ids[s * n, (s + 1) * n)
 // (n = status[MV_PLAN_IDS_PER_ITEM], a multiple of 4, at most kIdCap)
-// holds the pool blocks of its piece, -1 past its last block and for an
-// entry outside the pool. One wave writes one slot's list, 4 ids per lane
-// per pass (n <= 2 passes of 256). The slot follows from blockIdx and the
+// holds the pool blocks of its piece in entries [0, span) and -1 for an
+// entry outside the pool; -1 fills the rest of the last group of four.
+// Entries past that are not written: the decode kernel uses only [0, span)
+// (with a fixed piece bound n is the widest piece's span, so most of each
+// list is never written). One wave writes one slot's list, 4 ids per lane
+// per pass (at most 2 passes of 256). The slot follows from blockIdx and the
 // wave alone, so its work entry loads beside the status word: two
 // dependent round trips (entry and status, then the table) before the
 // stores. The pieces of kv head 0 read every block of every valid
@@ -1244,7 +1247,9 @@ __global__ __launch_bounds__(kIdsThreads) void decode_ids_kernel(IdsArgs a) {
     const bool seq_ok = w0.x >= 0 && w0.x < a.num_seqs;
     const BT* row = btp + (seq_ok ? static_cast<int64_t>(w0.x) * a.bt_stride : 0);
     int4* out = reinterpret_cast<int4*>(a.ids + slot * per_item);
-    for (int k0 = 4 * lane; k0 < per_item; k0 += 4 * 64) {
+    const int span = seq_ok ? vmax(0, last - first + 1) : 0;
+    const int n_write = vmin(per_item, (span + 3) & ~3);
+    for (int k0 = 4 * lane; k0 < n_write; k0 += 4 * 64) {
       int32_t v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {

@@ -3,7 +3,8 @@
 * Structure, read back from the device: every (sequence, kv head) unit is
   cut into pieces that tile [0, kv_len) exactly once, in order; the launch
   slots form a complete list; each slot's block ids are its table entries
-  (-1 past its last block); pieces respect the reported bounds.
+  (-1 past its last block, to a multiple of 4); pieces respect the
+  reported bounds.
 * Parity on the plan's three paths: groups dealt over the CUs (one
   dispatch round), more groups than can be dealt (natural order), and a
   skewed batch whose one-round split would need oversized pieces (fair
@@ -66,8 +67,11 @@ def _check_plan(case):
             # the stride is at least the span of the widest piece, a multiple of 4
             stride = ((plan.partition_tokens + bs - 1) // bs + 1 + 3) // 4 * 4
             assert stride * g <= ids.numel()
-        row = ids[slot * stride:(slot + 1) * stride].tolist()
-        want = [table[b][first + k] if first + k <= last else -1 for k in range(stride)]
+        # entries [0, span) are the piece's blocks, -1 fills its last group of
+        # four; the decode reads nothing past that, and the plan writes nothing
+        span4 = min(stride, (last - first + 1 + 3) // 4 * 4)
+        row = ids[slot * stride:slot * stride + span4].tolist()
+        want = [table[b][first + k] if first + k <= last else -1 for k in range(span4)]
         assert row == want, (slot, row[:8], want[:8])
     return plan
 
