@@ -34,7 +34,7 @@ def _write_both(k, v, kc, vc, slots, bs):
     assert torch.equal(bits(vd.cpu()), bits(vr)), "value_cache differs"
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c4", "c5"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
 def test_workload_write_bit_exact(name):
     say("write", name)
     c, (_, kref, vref) = cached_case(name)
