@@ -211,6 +211,28 @@ def clear_deferred(capture_id: Optional[int] = None) -> None:
         deferred.pop(capture_id, None)
 
 
+# The eager (not captured) per-step checks and plans that _cache_get keeps.
+_EAGER_CACHES = ("slots", "fused", "plan", "rope_rows", "positions", "prefill")
+
+
+def invalidate_cached_metadata() -> None:
+    """Forget this thread's cached metadata checks and plans (eager calls).
+
+    The wrappers validate a step's metadata (slots, block tables, lengths,
+    positions) once and reuse the result, and the decode plan, while the
+    same tensor objects come back at the same in-place version
+    (``t._version``): the other layers of the step. Writes that torch does
+    not see leave that version unchanged: through ``tensor.numpy()`` or
+    ``torch.from_numpy``, a DLPack alias, or a raw pointer. After such a
+    write, call this before the next call (or pass new tensors, as the
+    reference's input builder does every step). Plans made while capturing
+    a graph belong to that graph and are kept.
+    """
+    for name in _EAGER_CACHES:
+        if hasattr(_state, name):
+            delattr(_state, name)
+
+
 # ============================================================================
 # KV-cache write
 # ============================================================================

@@ -152,3 +152,26 @@ def test_metadata_types_keep_reference_fields():
     assert m.decode_group() is g
     assert m.prefill_slot_mapping.dtype == torch.long and m.prefill_slot_mapping.numel() == 0
     assert AttentionMetadata().decode_group() is None
+
+
+def test_cached_checks_follow_versions_and_can_be_invalidated():
+    """The per-step check cache matches the same tensor objects at the same
+    in-place version. An in-place torch write bumps the version (a new
+    check); a write through a numpy view does not, and
+    invalidate_cached_metadata() drops the entry so the next call checks
+    again."""
+    from mini_vllm.attention import paged_attention_gpu as pg
+
+    pg.invalidate_cached_metadata()
+    bt = torch.zeros(2, 4, dtype=torch.int32)
+    kv = torch.ones(2, dtype=torch.int32)
+    pg._cache_put("plan", (bt, kv), ("x",), "plan-1")
+    assert pg._cache_get("plan", (bt, kv), ("x",)) == "plan-1"
+    assert pg._cache_get("plan", (bt.clone(), kv), ("x",)) is None  # another tensor
+    kv.numpy()[0] = 9  # invisible to torch: same version, the entry still matches
+    assert pg._cache_get("plan", (bt, kv), ("x",)) == "plan-1"
+    pg.invalidate_cached_metadata()
+    assert pg._cache_get("plan", (bt, kv), ("x",)) is None
+    pg._cache_put("plan", (bt, kv), ("x",), "plan-2")
+    kv.add_(0)  # an in-place torch op bumps the version
+    assert pg._cache_get("plan", (bt, kv), ("x",)) is None

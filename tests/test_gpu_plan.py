@@ -183,3 +183,25 @@ def test_bad_entry_in_a_second_id_pass_raises():
     bt[b, t0 + 300] = pool
     with pytest.raises(IndexError, match="pool blocks"):
         hip_decode_attention(q, kc, kc, bt, kv, 1)
+
+
+def test_write_through_dlpack_alias_needs_invalidation():
+    """A length written through a DLPack alias leaves the tensor's in-place
+    version unchanged, so the step's cached plan is reused as it is;
+    invalidate_cached_metadata() makes the next call plan the new length."""
+    from mini_vllm.attention.paged_attention_gpu import invalidate_cached_metadata
+
+    bt = torch.arange(8, dtype=torch.int32, device=DEV).view(2, 4)
+    kv = torch.tensor([40, 20], dtype=torch.int32, device=DEV)
+    p1 = plan_decode(bt, kv, 16, 64, DEV, 64, torch.bfloat16, 2)
+    alias = torch.from_dlpack(kv)
+    alias[0] = 60
+    torch.cuda.synchronize()
+    assert plan_decode(bt, kv, 16, 64, DEV, 64, torch.bfloat16, 2) is p1
+    invalidate_cached_metadata()
+    p2 = plan_decode(bt, kv, 16, 64, DEV, 64, torch.bfloat16, 2)
+    assert p2 is not p1
+    g = p2.num_groups
+    work = p2.work[: 8 * g].view(g, 8).cpu().tolist()
+    ends = {(w[0], w[1]): max(x[5] for x in work if (x[0], x[1]) == (w[0], w[1])) for w in work}
+    assert ends[(0, 0)] == 60 and ends[(1, 0)] == 20, ends
