@@ -87,6 +87,35 @@ def build(verbose: bool = False, defines=(), out: str = LIB_PATH) -> str:
     return out
 
 
+LAUNCHER_SOURCE = os.path.join(CSRC, "py_launch.c")
+LAUNCHER_DIR = os.path.join(HERE, "mini_vllm", "attention")
+
+
+def build_launcher(verbose: bool = False) -> str:
+    """Compile the CPython fast-call wrappers (``csrc/py_launch.c``, host C
+    only) into ``mini_vllm/attention/_mvlaunch<EXT_SUFFIX>``; returns its
+    path. Without it the wrappers call the same entry points through
+    ctypes."""
+    import sysconfig
+
+    out = os.path.join(LAUNCHER_DIR, "_mvlaunch" + sysconfig.get_config_var("EXT_SUFFIX"))
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no C compiler (gcc) for the launcher extension")
+    fd, tmp = tempfile.mkstemp(prefix="_mvlaunch.", suffix=".so.tmp", dir=LAUNCHER_DIR)
+    os.close(fd)
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Wextra", "-Werror",
+           "-I", sysconfig.get_paths()["include"], LAUNCHER_SOURCE, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        os.unlink(tmp)
+        raise RuntimeError(f"launcher build failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     import argparse
 
@@ -98,3 +127,4 @@ if __name__ == "__main__":
     if args.define and os.path.abspath(args.out) == LIB_PATH:
         ap.error("a variant needs --out: lib/libmvattn.so is the default build")
     print(build(verbose=True, defines=args.define, out=args.out))
+    print(build_launcher(verbose=True))

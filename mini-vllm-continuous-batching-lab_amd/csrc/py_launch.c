@@ -1,0 +1,191 @@
+/*
+ * _mvlaunch: CPython fast-call wrappers of the C-ABI entry points that the
+ * Python wrappers call once per layer (mv_paged_decode_write,
+ * mv_paged_decode, mv_kv_cache_write; include/mvattn.h).
+ *
+ * ctypes converts every argument through libffi: about 5 us for the 35
+ * arguments of mv_paged_decode_write on the build host, a third of an eager
+ * layer call's host time. These wrappers take the same arguments, in the
+ * same order, as Python ints / floats / None (None: a null pointer),
+ * convert them with the CPython API (under 1 us) and call the same
+ * functions, through the addresses that ctypes resolved in the one loaded
+ * libmvattn.so (bind()). They return the entry point's status code; the
+ * caller reads mv_last_error() as for the ctypes call.
+ *
+ * Host code only (plain C, no HIP): built by build_lib.build_launcher().
+ */
+#define PY_SSIZE_T_CLEAN
+#include <Python.h>
+#include <stddef.h>
+#include <stdint.h>
+
+typedef int (*decode_write_fn)(const void*, int64_t, int64_t, const void*, int64_t, int64_t,
+                               const void*, int64_t, int64_t, const int64_t*, const void*,
+                               const void*, void*, void*, const int32_t*, const int32_t*,
+                               int64_t, int32_t, int32_t, int32_t, int32_t*, void*, int64_t,
+                               int64_t, float, int32_t, int32_t, int32_t, int32_t, int32_t,
+                               int64_t, int32_t, void*, size_t, void*);
+typedef int (*decode_fn)(const void*, int64_t, int64_t, const void*, const void*, const int32_t*,
+                         const int32_t*, int64_t, int32_t, int32_t, int32_t, int32_t*, void*,
+                         int64_t, int64_t, float, int32_t, int32_t, int32_t, int32_t, int32_t,
+                         int64_t, int32_t, void*, size_t, void*);
+typedef int (*cache_write_fn)(const void*, int64_t, int64_t, const void*, int64_t, int64_t, void*,
+                              void*, const int64_t*, int64_t, int32_t, int32_t, int32_t, int64_t,
+                              int32_t, void*);
+
+static decode_write_fn g_decode_write;
+static decode_fn g_decode;
+static cache_write_fn g_cache_write;
+
+/* A pointer argument: an int address, or None for a null pointer. */
+static void* arg_ptr(PyObject* o) { return o == Py_None ? NULL : PyLong_AsVoidPtr(o); }
+static int64_t arg_i64(PyObject* o) { return (int64_t)PyLong_AsLongLong(o); }
+static int32_t arg_i32(PyObject* o) {
+  const long long v = PyLong_AsLongLong(o);
+  if (!PyErr_Occurred() && (v < INT32_MIN || v > INT32_MAX))
+    PyErr_SetString(PyExc_OverflowError, "argument does not fit int32");
+  return (int32_t)v;
+}
+static size_t arg_size(PyObject* o) { return (size_t)PyLong_AsUnsignedLongLong(o); }
+static float arg_f32(PyObject* o) { return (float)PyFloat_AsDouble(o); }
+
+static int check_nargs(const char* name, Py_ssize_t got, Py_ssize_t want, const void* fn) {
+  if (!fn) {
+    PyErr_Format(PyExc_RuntimeError, "_mvlaunch.%s: bind() was not called", name);
+    return -1;
+  }
+  if (got != want) {
+    PyErr_Format(PyExc_TypeError, "_mvlaunch.%s takes %zd arguments (%zd given)", name, want, got);
+    return -1;
+  }
+  return 0;
+}
+
+/* Arguments of mv_paged_decode_write, in its order. */
+static PyObject* decode_write(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (check_nargs("decode_write", n, 35, (const void*)g_decode_write)) return NULL;
+  const void* query = arg_ptr(a[0]);
+  const int64_t q_st = arg_i64(a[1]), q_sh = arg_i64(a[2]);
+  const void* nk = arg_ptr(a[3]);
+  const int64_t nk_st = arg_i64(a[4]), nk_sh = arg_i64(a[5]);
+  const void* nv = arg_ptr(a[6]);
+  const int64_t nv_st = arg_i64(a[7]), nv_sh = arg_i64(a[8]);
+  const int64_t* slots = (const int64_t*)arg_ptr(a[9]);
+  const void* rope_cos = arg_ptr(a[10]);
+  const void* rope_sin = arg_ptr(a[11]);
+  void* key_cache = arg_ptr(a[12]);
+  void* value_cache = arg_ptr(a[13]);
+  const int32_t* work = (const int32_t*)arg_ptr(a[14]);
+  const int32_t* ids = (const int32_t*)arg_ptr(a[15]);
+  const int64_t ids_cap = arg_i64(a[16]);
+  const int32_t groups = arg_i32(a[17]), part_tokens = arg_i32(a[18]), max_parts = arg_i32(a[19]);
+  int32_t* counters = (int32_t*)arg_ptr(a[20]);
+  void* out = arg_ptr(a[21]);
+  const int64_t o_st = arg_i64(a[22]), o_sh = arg_i64(a[23]);
+  const float scale = arg_f32(a[24]);
+  const int32_t num_seqs = arg_i32(a[25]), hq = arg_i32(a[26]), hkv = arg_i32(a[27]);
+  const int32_t d = arg_i32(a[28]), bs = arg_i32(a[29]);
+  const int64_t num_blocks = arg_i64(a[30]);
+  const int32_t dtype = arg_i32(a[31]);
+  void* ws = arg_ptr(a[32]);
+  const size_t ws_bytes = arg_size(a[33]);
+  void* stream = arg_ptr(a[34]);
+  if (PyErr_Occurred()) return NULL;
+  const int rc = g_decode_write(query, q_st, q_sh, nk, nk_st, nk_sh, nv, nv_st, nv_sh, slots,
+                                rope_cos, rope_sin, key_cache, value_cache, work, ids, ids_cap,
+                                groups, part_tokens, max_parts, counters, out, o_st, o_sh, scale,
+                                num_seqs, hq, hkv, d, bs, num_blocks, dtype, ws, ws_bytes, stream);
+  return PyLong_FromLong(rc);
+}
+
+/* Arguments of mv_paged_decode, in its order. */
+static PyObject* decode(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (check_nargs("decode", n, 26, (const void*)g_decode)) return NULL;
+  const void* query = arg_ptr(a[0]);
+  const int64_t q_st = arg_i64(a[1]), q_sh = arg_i64(a[2]);
+  const void* key_cache = arg_ptr(a[3]);
+  const void* value_cache = arg_ptr(a[4]);
+  const int32_t* work = (const int32_t*)arg_ptr(a[5]);
+  const int32_t* ids = (const int32_t*)arg_ptr(a[6]);
+  const int64_t ids_cap = arg_i64(a[7]);
+  const int32_t groups = arg_i32(a[8]), part_tokens = arg_i32(a[9]), max_parts = arg_i32(a[10]);
+  int32_t* counters = (int32_t*)arg_ptr(a[11]);
+  void* out = arg_ptr(a[12]);
+  const int64_t o_st = arg_i64(a[13]), o_sh = arg_i64(a[14]);
+  const float scale = arg_f32(a[15]);
+  const int32_t num_seqs = arg_i32(a[16]), hq = arg_i32(a[17]), hkv = arg_i32(a[18]);
+  const int32_t d = arg_i32(a[19]), bs = arg_i32(a[20]);
+  const int64_t num_blocks = arg_i64(a[21]);
+  const int32_t dtype = arg_i32(a[22]);
+  void* ws = arg_ptr(a[23]);
+  const size_t ws_bytes = arg_size(a[24]);
+  void* stream = arg_ptr(a[25]);
+  if (PyErr_Occurred()) return NULL;
+  const int rc = g_decode(query, q_st, q_sh, key_cache, value_cache, work, ids, ids_cap, groups,
+                          part_tokens, max_parts, counters, out, o_st, o_sh, scale, num_seqs, hq,
+                          hkv, d, bs, num_blocks, dtype, ws, ws_bytes, stream);
+  return PyLong_FromLong(rc);
+}
+
+/* Arguments of mv_kv_cache_write, in its order. */
+static PyObject* cache_write(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (check_nargs("cache_write", n, 16, (const void*)g_cache_write)) return NULL;
+  const void* key = arg_ptr(a[0]);
+  const int64_t k_st = arg_i64(a[1]), k_sh = arg_i64(a[2]);
+  const void* value = arg_ptr(a[3]);
+  const int64_t v_st = arg_i64(a[4]), v_sh = arg_i64(a[5]);
+  void* key_cache = arg_ptr(a[6]);
+  void* value_cache = arg_ptr(a[7]);
+  const int64_t* slots = (const int64_t*)arg_ptr(a[8]);
+  const int64_t num_tokens = arg_i64(a[9]);
+  const int32_t hkv = arg_i32(a[10]), d = arg_i32(a[11]), bs = arg_i32(a[12]);
+  const int64_t num_blocks = arg_i64(a[13]);
+  const int32_t dtype = arg_i32(a[14]);
+  void* stream = arg_ptr(a[15]);
+  if (PyErr_Occurred()) return NULL;
+  const int rc = g_cache_write(key, k_st, k_sh, value, v_st, v_sh, key_cache, value_cache, slots,
+                               num_tokens, hkv, d, bs, num_blocks, dtype, stream);
+  return PyLong_FromLong(rc);
+}
+
+/* bind(decode_write_address, decode_address, cache_write_address): the
+ * entry points' addresses in the loaded libmvattn.so (ctypes resolves them). */
+static PyObject* bind(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (n != 3) {
+    PyErr_SetString(PyExc_TypeError, "_mvlaunch.bind takes 3 addresses");
+    return NULL;
+  }
+  void* p0 = PyLong_AsVoidPtr(a[0]);
+  void* p1 = PyLong_AsVoidPtr(a[1]);
+  void* p2 = PyLong_AsVoidPtr(a[2]);
+  if (PyErr_Occurred()) return NULL;
+  if (!p0 || !p1 || !p2) {
+    PyErr_SetString(PyExc_ValueError, "_mvlaunch.bind: null address");
+    return NULL;
+  }
+  g_decode_write = (decode_write_fn)p0;
+  g_decode = (decode_fn)p1;
+  g_cache_write = (cache_write_fn)p2;
+  Py_RETURN_NONE;
+}
+
+static PyMethodDef methods[] = {
+    {"bind", (PyCFunction)(void (*)(void))bind, METH_FASTCALL, "bind the entry points"},
+    {"decode_write", (PyCFunction)(void (*)(void))decode_write, METH_FASTCALL,
+     "mv_paged_decode_write with its 35 arguments"},
+    {"decode", (PyCFunction)(void (*)(void))decode, METH_FASTCALL,
+     "mv_paged_decode with its 26 arguments"},
+    {"cache_write", (PyCFunction)(void (*)(void))cache_write, METH_FASTCALL,
+     "mv_kv_cache_write with its 16 arguments"},
+    {NULL, NULL, 0, NULL},
+};
+
+static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, "_mvlaunch",
+                                    "fast-call wrappers of libmvattn entry points", -1, methods,
+                                    NULL, NULL, NULL, NULL};
+
+PyMODINIT_FUNC PyInit__mvlaunch(void) { return PyModule_Create(&module); }

@@ -154,6 +154,35 @@ def library_path() -> str:
     return os.environ.get("MVATTN_LIB", DEFAULT_LIB_PATH)
 
 
+# The per-layer entry points as called by the wrappers: the CPython
+# fast-call wrappers of _mvlaunch (csrc/py_launch.c, built beside this
+# module) when it is present, else the ctypes functions. Same arguments in
+# the same order, same status codes; set when the library is loaded.
+decode_write = None  # mv_paged_decode_write
+decode = None        # mv_paged_decode
+cache_write = None   # mv_kv_cache_write
+
+
+def _bind_calls(lib: ctypes.CDLL) -> None:
+    global decode_write, decode, cache_write
+    try:
+        from . import _mvlaunch
+    except ImportError:
+        _mvlaunch = None
+    if _mvlaunch is None:
+        decode_write, decode, cache_write = (lib.mv_paged_decode_write, lib.mv_paged_decode,
+                                             lib.mv_kv_cache_write)
+        return
+
+    def addr(fn) -> int:
+        return ctypes.cast(fn, ctypes.c_void_p).value
+
+    _mvlaunch.bind(addr(lib.mv_paged_decode_write), addr(lib.mv_paged_decode),
+                   addr(lib.mv_kv_cache_write))
+    decode_write, decode, cache_write = (_mvlaunch.decode_write, _mvlaunch.decode,
+                                         _mvlaunch.cache_write)
+
+
 def load(path: str | None = None) -> ctypes.CDLL:
     """Load (once) and type the kernel library; RuntimeError if it is missing."""
     global _lib
@@ -178,6 +207,7 @@ def load(path: str | None = None) -> ctypes.CDLL:
                 f"{p}: ABI version {lib.mv_abi_version()} != expected {ABI_VERSION}"
             )
         if path is None:
+            _bind_calls(lib)
             _lib = lib
         return lib
 

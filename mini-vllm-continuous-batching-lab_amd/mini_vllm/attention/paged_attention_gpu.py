@@ -27,7 +27,7 @@ import math
 import os
 import threading
 import weakref
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Any, List, Optional, Sequence, Tuple
 
 import torch
@@ -212,7 +212,7 @@ def clear_deferred(capture_id: Optional[int] = None) -> None:
 
 
 # The eager (not captured) per-step checks and plans that _cache_get keeps.
-_EAGER_CACHES = ("slots", "fused", "plan", "rope_rows", "positions", "prefill")
+_EAGER_CACHES = ("slots", "fused", "plan", "fused_step", "rope_rows", "positions", "prefill")
 
 
 def invalidate_cached_metadata() -> None:
@@ -333,9 +333,9 @@ def hip_cache_write(
         key = key.contiguous()
     if value.stride(2) != 1:
         value = value.contiguous()
-    lib = _hip.load()
+    _hip.load()  # binds _hip.cache_write
     _hip.check(
-        lib.mv_kv_cache_write(
+        _hip.cache_write(
             _ptr(key), key.stride(0), key.stride(1),
             _ptr(value), value.stride(0), value.stride(1),
             _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping),
@@ -361,6 +361,8 @@ class DecodePlan:
     num_groups: int
     max_parts: int
     partition_tokens: int
+    # merge workspace bytes per query-head count (asked of the library once)
+    ws_bytes: dict = field(default_factory=dict)
 
 
 # The plan aims for as many work groups as the device holds at once (work
@@ -667,8 +669,18 @@ def hip_decode_attention(
     device = query.device
     num_blocks = kshape[0]
     capture = _capture_id(device)
-    plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
-                       dtype, num_kv_heads, capture=capture)
+    # The other layers of an eager step with the KV write fused: the plan,
+    # the slot check, the fused-write check and the slots' device copy in
+    # one lookup (same tensors at the same in-place versions).
+    step = None
+    step_extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads)
+    if new_key is not None and not capture:
+        step = _cache_get("fused_step", (slot_mapping, block_table, kv_len_after), step_extra)
+    if step is not None:
+        plan = step[0]
+    else:
+        plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
+                           dtype, num_kv_heads, capture=capture)
     output = torch.empty_like(query, memory_format=torch.contiguous_format)
     if total_decode == 0 or plan.num_groups == 0:
         return output
@@ -677,7 +689,10 @@ def hip_decode_attention(
     ) % 16 or query.data_ptr() % 16:
         query = query.contiguous()
     lib = _hip.load()
-    ws_bytes = lib.mv_paged_decode_workspace_bytes(total_decode, num_q_heads, head_dim, plan.max_parts)
+    ws_bytes = plan.ws_bytes.get(num_q_heads)
+    if ws_bytes is None:
+        ws_bytes = plan.ws_bytes[num_q_heads] = lib.mv_paged_decode_workspace_bytes(
+            total_decode, num_q_heads, head_dim, plan.max_parts)
     ws = _workspace(device, ws_bytes) if ws_bytes else None
     if new_key is not None:
         assert new_value is not None and slot_mapping is not None
@@ -688,19 +703,27 @@ def hip_decode_attention(
         assert new_value.shape == nshape
         assert new_key.dtype == dtype and new_value.dtype == dtype
         assert new_key.device == device and new_value.device == device
-        assert slot_mapping.shape == (total_decode,)
-        if slot_mapping.device != device:
-            slot_mapping = slot_mapping.to(device)
-        if slot_mapping.dtype != torch.int64:
-            slot_mapping = slot_mapping.to(torch.int64)
-        slot_mapping = slot_mapping.contiguous()
-        _check_slots(slot_mapping, num_blocks * block_size, capture=capture)
         rope = positions is not None
         if rope:
             assert cos is not None and sin is not None
             assert positions.shape == (total_decode,)
-        if not _fused_write_ok(slot_mapping, block_table, kv_len_after, block_size, device,
-                               capture):
+        if step is not None:
+            slot_mapping = step[1]
+        else:
+            slots_given = slot_mapping
+            assert slot_mapping.shape == (total_decode,)
+            if slot_mapping.device != device:
+                slot_mapping = slot_mapping.to(device)
+            if slot_mapping.dtype != torch.int64:
+                slot_mapping = slot_mapping.to(torch.int64)
+            slot_mapping = slot_mapping.contiguous()
+            _check_slots(slot_mapping, num_blocks * block_size, capture=capture)
+            fused_ok = _fused_write_ok(slot_mapping, block_table, kv_len_after, block_size,
+                                       device, capture)
+            if fused_ok and not capture:
+                _cache_put("fused_step", (slots_given, block_table, kv_len_after), step_extra,
+                           (plan, slot_mapping))
+        if step is None and not fused_ok:
             if rope:  # the unfused sequence: rope + write, then decode of the rotated query
                 query, _ = hip_rope_kv_cache_write(query, new_key, new_value, positions, cos, sin,
                                                    key_cache, value_cache, slot_mapping,
@@ -715,7 +738,7 @@ def hip_decode_attention(
             rope_cos, rope_sin = _rope_rows(positions, cos, sin, head_dim, dtype, device, capture)
         nk, nv = _aligned_rows(new_key), _aligned_rows(new_value)
         _hip.check(
-            lib.mv_paged_decode_write(
+            _hip.decode_write(
                 _ptr(query), query.stride(0), query.stride(1),
                 _ptr(nk), nk.stride(0), nk.stride(1), _ptr(nv), nv.stride(0), nv.stride(1),
                 _ptr(slot_mapping), _ptr(rope_cos), _ptr(rope_sin), _ptr(key_cache),
@@ -731,7 +754,7 @@ def hip_decode_attention(
         )
         return output
     _hip.check(
-        lib.mv_paged_decode(
+        _hip.decode(
             _ptr(query), query.stride(0), query.stride(1),
             _ptr(key_cache), _ptr(value_cache),
             _ptr(plan.work), _ptr(plan.block_ids), plan.block_ids.numel(), plan.num_groups,

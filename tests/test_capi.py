@@ -31,14 +31,18 @@ def _declared_functions():
 
 @pytest.fixture(scope="module")
 def lib():
-    if not os.path.exists(_hip.library_path()):
-        import importlib.util
+    import importlib.util
 
+    launcher = importlib.util.find_spec("mini_vllm.attention._mvlaunch")
+    if not os.path.exists(_hip.library_path()) or launcher is None:
         spec = importlib.util.spec_from_file_location(
             "build_lib", os.path.join(ROOT, "mini-vllm-continuous-batching-lab_amd", "build_lib.py"))
         mod = importlib.util.module_from_spec(spec)
         spec.loader.exec_module(mod)
-        mod.build()
+        if not os.path.exists(_hip.library_path()):
+            mod.build()
+        if launcher is None:
+            mod.build_launcher()
     return _hip.load()
 
 
@@ -231,3 +235,26 @@ def test_check_maps_codes_to_exceptions(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not found"):
         _hip.load(str(tmp_path / "nope.so"))
+
+
+def test_fast_call_wrappers_match_the_header(lib):
+    """The CPython fast-call wrappers (_mvlaunch) are bound to the loaded
+    library, take each entry point's parameter count from the header, and
+    turn a wrong count or an out-of-range int32 into a Python error before
+    any call."""
+    from mini_vllm.attention import _mvlaunch
+
+    declared = _declared_functions()
+    assert _hip.decode_write is _mvlaunch.decode_write
+    assert _hip.decode is _mvlaunch.decode
+    assert _hip.cache_write is _mvlaunch.cache_write
+    for fn, name in ((_mvlaunch.decode_write, "mv_paged_decode_write"),
+                     (_mvlaunch.decode, "mv_paged_decode"),
+                     (_mvlaunch.cache_write, "mv_kv_cache_write")):
+        n = declared[name]
+        with pytest.raises(TypeError, match=f"takes {n} arguments"):
+            fn(*([0] * (n - 1)))
+    # num_kv_heads (argument 10 of mv_kv_cache_write) beyond int32
+    args = [None, 0, 0, None, 0, 0, None, None, None, 0, 1 << 40, 64, 16, 1, 0, None]
+    with pytest.raises(OverflowError):
+        _mvlaunch.cache_write(*args)

@@ -159,3 +159,42 @@ def test_fused_precondition_is_checked_in_a_captured_graph():
         pg.check_deferred(gid)
     del graph
     pg.clear_deferred()
+
+
+def test_step_cache_sees_in_place_slot_edits():
+    """Layers of one step reuse the plan and the slot and fused-write checks
+    (one cached entry for the same slot, table and length tensors). An
+    in-place edit of the slots between layers must be checked again: a
+    slot moved to an earlier attended position of its own sequence runs as
+    the two calls (equal to them bit for bit), and a duplicate slot
+    raises."""
+    say("decode+write: step cache and in-place slot edits")
+    case = make_case("c2", seed=5, nan_fill=False)
+    bs = case.layout.spec.block_size
+    d = to_device(case)
+    slots = d.slot_mapping.clone()
+
+    def fused(kc, vc):
+        return hip_decode_attention(d.query, kc, vc, d.block_table, d.kv_len, bs,
+                                    new_key=d.new_key, new_value=d.new_value, slot_mapping=slots)
+
+    for _ in range(2):  # the second call hits the step's cached entry
+        kc, vc = d.key_cache.clone(), d.value_cache.clone()
+        out = fused(kc, vc)
+    kc1, vc1 = d.key_cache.clone(), d.value_cache.clone()
+    hip_cache_write(d.new_key, d.new_value, kc1, vc1, slots, bs)
+    ref = hip_decode_attention(d.query, kc1, vc1, d.block_table, d.kv_len, bs)
+    _same((ref, kc1, vc1), (out, kc, vc))
+
+    slots[0] = int(case.block_table[0, 5 // bs]) * bs + 5 % bs  # in place: a new version
+    kc, vc = d.key_cache.clone(), d.value_cache.clone()
+    out = fused(kc, vc)
+    kc1, vc1 = d.key_cache.clone(), d.value_cache.clone()
+    hip_cache_write(d.new_key, d.new_value, kc1, vc1, slots, bs)
+    ref = hip_decode_attention(d.query, kc1, vc1, d.block_table, d.kv_len, bs)
+    torch.cuda.synchronize()
+    _same((ref, kc1, vc1), (out, kc, vc))
+
+    slots[1] = slots[2]
+    with pytest.raises(AssertionError, match="Duplicate"):
+        fused(d.key_cache.clone(), d.value_cache.clone())
