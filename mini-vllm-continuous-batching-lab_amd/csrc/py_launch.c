@@ -1,7 +1,8 @@
 /*
  * _mvlaunch: CPython fast-call wrappers of the C-ABI entry points that the
  * Python wrappers call once per layer (mv_paged_decode_write,
- * mv_paged_decode, mv_kv_cache_write; include/mvattn.h).
+ * mv_paged_decode, mv_kv_cache_write, mv_rope_kv_cache_write;
+ * include/mvattn.h).
  *
  * ctypes converts every argument through libffi: about 5 us for the 35
  * arguments of mv_paged_decode_write on the build host, a third of an eager
@@ -33,7 +34,14 @@ typedef int (*cache_write_fn)(const void*, int64_t, int64_t, const void*, int64_
                               void*, const int64_t*, int64_t, int32_t, int32_t, int32_t, int64_t,
                               int32_t, void*);
 
+typedef int (*rope_write_fn)(const void*, int64_t, int64_t, void*, int64_t, int64_t, const void*,
+                             int64_t, int64_t, void*, int64_t, int64_t, const void*, int64_t,
+                             int64_t, void*, void*, const int64_t*, const int64_t*, const void*,
+                             const void*, int64_t, int64_t, int64_t, int32_t, int32_t, int32_t,
+                             int32_t, int64_t, int32_t, void*);
+
 static decode_write_fn g_decode_write;
+static rope_write_fn g_rope_write;
 static decode_fn g_decode;
 static cache_write_fn g_cache_write;
 
@@ -151,25 +159,61 @@ static PyObject* cache_write(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return PyLong_FromLong(rc);
 }
 
-/* bind(decode_write_address, decode_address, cache_write_address): the
- * entry points' addresses in the loaded libmvattn.so (ctypes resolves them). */
+/* Arguments of mv_rope_kv_cache_write, in its order. */
+static PyObject* rope_write(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (check_nargs("rope_write", n, 31, (const void*)g_rope_write)) return NULL;
+  const void* query = arg_ptr(a[0]);
+  const int64_t q_st = arg_i64(a[1]), q_sh = arg_i64(a[2]);
+  void* query_out = arg_ptr(a[3]);
+  const int64_t qo_st = arg_i64(a[4]), qo_sh = arg_i64(a[5]);
+  const void* key = arg_ptr(a[6]);
+  const int64_t k_st = arg_i64(a[7]), k_sh = arg_i64(a[8]);
+  void* key_out = arg_ptr(a[9]);
+  const int64_t ko_st = arg_i64(a[10]), ko_sh = arg_i64(a[11]);
+  const void* value = arg_ptr(a[12]);
+  const int64_t v_st = arg_i64(a[13]), v_sh = arg_i64(a[14]);
+  void* key_cache = arg_ptr(a[15]);
+  void* value_cache = arg_ptr(a[16]);
+  const int64_t* slots = (const int64_t*)arg_ptr(a[17]);
+  const int64_t* positions = (const int64_t*)arg_ptr(a[18]);
+  const void* cos_table = arg_ptr(a[19]);
+  const void* sin_table = arg_ptr(a[20]);
+  const int64_t table_stride = arg_i64(a[21]), max_positions = arg_i64(a[22]);
+  const int64_t num_tokens = arg_i64(a[23]);
+  const int32_t hq = arg_i32(a[24]), hkv = arg_i32(a[25]), d = arg_i32(a[26]), bs = arg_i32(a[27]);
+  const int64_t num_blocks = arg_i64(a[28]);
+  const int32_t dtype = arg_i32(a[29]);
+  void* stream = arg_ptr(a[30]);
+  if (PyErr_Occurred()) return NULL;
+  const int rc = g_rope_write(query, q_st, q_sh, query_out, qo_st, qo_sh, key, k_st, k_sh, key_out,
+                              ko_st, ko_sh, value, v_st, v_sh, key_cache, value_cache, slots,
+                              positions, cos_table, sin_table, table_stride, max_positions,
+                              num_tokens, hq, hkv, d, bs, num_blocks, dtype, stream);
+  return PyLong_FromLong(rc);
+}
+
+/* bind(decode_write, decode, cache_write, rope_write): the entry points'
+ * addresses in the loaded libmvattn.so (ctypes resolves them). */
 static PyObject* bind(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
-  if (n != 3) {
-    PyErr_SetString(PyExc_TypeError, "_mvlaunch.bind takes 3 addresses");
+  if (n != 4) {
+    PyErr_SetString(PyExc_TypeError, "_mvlaunch.bind takes 4 addresses");
     return NULL;
   }
-  void* p0 = PyLong_AsVoidPtr(a[0]);
-  void* p1 = PyLong_AsVoidPtr(a[1]);
-  void* p2 = PyLong_AsVoidPtr(a[2]);
-  if (PyErr_Occurred()) return NULL;
-  if (!p0 || !p1 || !p2) {
-    PyErr_SetString(PyExc_ValueError, "_mvlaunch.bind: null address");
-    return NULL;
+  void* p[4];
+  for (int i = 0; i < 4; ++i) {
+    p[i] = PyLong_AsVoidPtr(a[i]);
+    if (PyErr_Occurred()) return NULL;
+    if (!p[i]) {
+      PyErr_SetString(PyExc_ValueError, "_mvlaunch.bind: null address");
+      return NULL;
+    }
   }
-  g_decode_write = (decode_write_fn)p0;
-  g_decode = (decode_fn)p1;
-  g_cache_write = (cache_write_fn)p2;
+  g_decode_write = (decode_write_fn)p[0];
+  g_decode = (decode_fn)p[1];
+  g_cache_write = (cache_write_fn)p[2];
+  g_rope_write = (rope_write_fn)p[3];
   Py_RETURN_NONE;
 }
 
@@ -181,6 +225,8 @@ static PyMethodDef methods[] = {
      "mv_paged_decode with its 26 arguments"},
     {"cache_write", (PyCFunction)(void (*)(void))cache_write, METH_FASTCALL,
      "mv_kv_cache_write with its 16 arguments"},
+    {"rope_write", (PyCFunction)(void (*)(void))rope_write, METH_FASTCALL,
+     "mv_rope_kv_cache_write with its 31 arguments"},
     {NULL, NULL, 0, NULL},
 };
 

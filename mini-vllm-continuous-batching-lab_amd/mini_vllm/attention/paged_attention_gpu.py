@@ -212,7 +212,8 @@ def clear_deferred(capture_id: Optional[int] = None) -> None:
 
 
 # The eager (not captured) per-step checks and plans that _cache_get keeps.
-_EAGER_CACHES = ("slots", "fused", "plan", "fused_step", "rope_rows", "positions", "prefill")
+_EAGER_CACHES = ("slots", "fused", "plan", "fused_step", "rope_step", "rope_rows", "positions",
+                 "prefill")
 
 
 def invalidate_cached_metadata() -> None:
@@ -882,19 +883,31 @@ def hip_rope_kv_cache_write(
         assert _is_pow2(block_size), f"block_size {block_size} must be a power of 2"
         assert key_cache.shape[1] == num_kv_heads and key_cache.shape[3] == head_dim
         assert key_cache.is_contiguous() and value_cache.is_contiguous(), "cache must be contiguous"
-        if slot_mapping.device != device:
-            slot_mapping = slot_mapping.to(device)
-        if slot_mapping.dtype != torch.int64:
-            slot_mapping = slot_mapping.to(torch.int64)
-        slot_mapping = slot_mapping.contiguous()
         num_blocks = key_cache.shape[0]
-        _check_slots(slot_mapping, num_blocks * block_size)
-    if positions.device != device:
-        positions = positions.to(device)
-    if positions.dtype != torch.int64:
-        positions = positions.to(torch.int64)
-    positions = positions.contiguous()
-    _check_positions(positions, cos.shape[0])
+    # The other layers of an eager step: the slot and position checks and
+    # their device copies in one lookup (same tensors, same versions).
+    capture = _capture_id(device)
+    given = (slot_mapping, positions) if write else (positions,)
+    step_extra = (num_blocks * block_size, cos.shape[0], device)
+    step = None if capture else _cache_get("rope_step", given, step_extra)
+    if step is not None:
+        slot_mapping, positions = step
+    else:
+        if write:
+            if slot_mapping.device != device:
+                slot_mapping = slot_mapping.to(device)
+            if slot_mapping.dtype != torch.int64:
+                slot_mapping = slot_mapping.to(torch.int64)
+            slot_mapping = slot_mapping.contiguous()
+            _check_slots(slot_mapping, num_blocks * block_size, capture=capture)
+        if positions.device != device:
+            positions = positions.to(device)
+        if positions.dtype != torch.int64:
+            positions = positions.to(torch.int64)
+        positions = positions.contiguous()
+        _check_positions(positions, cos.shape[0])
+        if not capture:
+            _cache_put("rope_step", given, step_extra, (slot_mapping, positions))
 
     q_out = None
     if query is not None:
@@ -908,9 +921,9 @@ def hip_rope_kv_cache_write(
         value = _rope_operand(value)
     if cos.stride(1) != 1 or sin.stride(1) != 1 or cos.stride(0) != sin.stride(0):
         cos, sin = cos.contiguous(), sin.contiguous()
-    lib = _hip.load()
+    _hip.load()  # binds _hip.rope_write
     _hip.check(
-        lib.mv_rope_kv_cache_write(
+        _hip.rope_write(
             _ptr(query), query.stride(0) if query is not None else 0,
             query.stride(1) if query is not None else 0,
             _ptr(q_out), q_out.stride(0) if q_out is not None else 0,

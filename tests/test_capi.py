@@ -248,9 +248,11 @@ def test_fast_call_wrappers_match_the_header(lib):
     assert _hip.decode_write is _mvlaunch.decode_write
     assert _hip.decode is _mvlaunch.decode
     assert _hip.cache_write is _mvlaunch.cache_write
+    assert _hip.rope_write is _mvlaunch.rope_write
     for fn, name in ((_mvlaunch.decode_write, "mv_paged_decode_write"),
                      (_mvlaunch.decode, "mv_paged_decode"),
-                     (_mvlaunch.cache_write, "mv_kv_cache_write")):
+                     (_mvlaunch.cache_write, "mv_kv_cache_write"),
+                     (_mvlaunch.rope_write, "mv_rope_kv_cache_write")):
         n = declared[name]
         with pytest.raises(TypeError, match=f"takes {n} arguments"):
             fn(*([0] * (n - 1)))
