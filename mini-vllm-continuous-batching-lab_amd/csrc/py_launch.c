@@ -1,8 +1,8 @@
 /*
  * _mvlaunch: CPython fast-call wrappers of the C-ABI entry points that the
- * Python wrappers call once per layer (mv_paged_decode_write,
- * mv_paged_decode, mv_kv_cache_write, mv_rope_kv_cache_write;
- * include/mvattn.h).
+ * Python wrappers call once per layer or step (mv_paged_decode_write,
+ * mv_paged_decode, mv_kv_cache_write, mv_rope_kv_cache_write,
+ * mv_decode_plan; include/mvattn.h).
  *
  * ctypes converts every argument through libffi: about 5 us for the 35
  * arguments of mv_paged_decode_write on the build host, a third of an eager
@@ -40,8 +40,13 @@ typedef int (*rope_write_fn)(const void*, int64_t, int64_t, void*, int64_t, int6
                              const void*, int64_t, int64_t, int64_t, int32_t, int32_t, int32_t,
                              int32_t, int64_t, int32_t, void*);
 
+typedef int (*plan_fn)(const void*, int32_t, const void*, int32_t, int64_t, int32_t, int32_t,
+                       int32_t, int64_t, int32_t, int32_t, int32_t, int32_t, int32_t*, int64_t,
+                       int32_t*, int64_t, int32_t*, int32_t*, void*);
+
 static decode_write_fn g_decode_write;
 static rope_write_fn g_rope_write;
+static plan_fn g_plan;
 static decode_fn g_decode;
 static cache_write_fn g_cache_write;
 
@@ -193,16 +198,43 @@ static PyObject* rope_write(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return PyLong_FromLong(rc);
 }
 
-/* bind(decode_write, decode, cache_write, rope_write): the entry points'
- * addresses in the loaded libmvattn.so (ctypes resolves them). */
+/* Arguments of mv_decode_plan, in its order. */
+static PyObject* plan(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (check_nargs("plan", n, 20, (const void*)g_plan)) return NULL;
+  const void* kv_len = arg_ptr(a[0]);
+  const int32_t kv_i64 = arg_i32(a[1]);
+  const void* block_table = arg_ptr(a[2]);
+  const int32_t bt_i64 = arg_i32(a[3]);
+  const int64_t bt_stride = arg_i64(a[4]);
+  const int32_t num_seqs = arg_i32(a[5]), max_blocks = arg_i32(a[6]), bs = arg_i32(a[7]);
+  const int64_t num_blocks = arg_i64(a[8]);
+  const int32_t hkv = arg_i32(a[9]), per_cu = arg_i32(a[10]), cus = arg_i32(a[11]);
+  const int32_t fixed = arg_i32(a[12]);
+  int32_t* work = (int32_t*)arg_ptr(a[13]);
+  const int64_t work_cap = arg_i64(a[14]);
+  int32_t* ids = (int32_t*)arg_ptr(a[15]);
+  const int64_t ids_cap = arg_i64(a[16]);
+  int32_t* counters = (int32_t*)arg_ptr(a[17]);
+  int32_t* status = (int32_t*)arg_ptr(a[18]);
+  void* stream = arg_ptr(a[19]);
+  if (PyErr_Occurred()) return NULL;
+  const int rc = g_plan(kv_len, kv_i64, block_table, bt_i64, bt_stride, num_seqs, max_blocks, bs,
+                        num_blocks, hkv, per_cu, cus, fixed, work, work_cap, ids, ids_cap,
+                        counters, status, stream);
+  return PyLong_FromLong(rc);
+}
+
+/* bind(decode_write, decode, cache_write, rope_write, plan): the entry
+ * points' addresses in the loaded libmvattn.so (ctypes resolves them). */
 static PyObject* bind(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
-  if (n != 4) {
-    PyErr_SetString(PyExc_TypeError, "_mvlaunch.bind takes 4 addresses");
+  if (n != 5) {
+    PyErr_SetString(PyExc_TypeError, "_mvlaunch.bind takes 5 addresses");
     return NULL;
   }
-  void* p[4];
-  for (int i = 0; i < 4; ++i) {
+  void* p[5];
+  for (int i = 0; i < 5; ++i) {
     p[i] = PyLong_AsVoidPtr(a[i]);
     if (PyErr_Occurred()) return NULL;
     if (!p[i]) {
@@ -214,6 +246,7 @@ static PyObject* bind(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   g_decode = (decode_fn)p[1];
   g_cache_write = (cache_write_fn)p[2];
   g_rope_write = (rope_write_fn)p[3];
+  g_plan = (plan_fn)p[4];
   Py_RETURN_NONE;
 }
 
@@ -227,6 +260,8 @@ static PyMethodDef methods[] = {
      "mv_kv_cache_write with its 16 arguments"},
     {"rope_write", (PyCFunction)(void (*)(void))rope_write, METH_FASTCALL,
      "mv_rope_kv_cache_write with its 31 arguments"},
+    {"plan", (PyCFunction)(void (*)(void))plan, METH_FASTCALL,
+     "mv_decode_plan with its 20 arguments"},
     {NULL, NULL, 0, NULL},
 };
 

@@ -162,22 +162,24 @@ decode_write = None  # mv_paged_decode_write
 decode = None        # mv_paged_decode
 cache_write = None   # mv_kv_cache_write
 rope_write = None    # mv_rope_kv_cache_write
+plan = None          # mv_decode_plan
 
 
 def _bind_calls(lib: ctypes.CDLL) -> None:
-    global decode_write, decode, cache_write, rope_write
+    global decode_write, decode, cache_write, rope_write, plan
     ctypes_calls = (lib.mv_paged_decode_write, lib.mv_paged_decode, lib.mv_kv_cache_write,
-                    lib.mv_rope_kv_cache_write)
+                    lib.mv_rope_kv_cache_write, lib.mv_decode_plan)
     try:
         from . import _mvlaunch
     except ImportError:
         _mvlaunch = None
     if _mvlaunch is None:
-        decode_write, decode, cache_write, rope_write = ctypes_calls
+        decode_write, decode, cache_write, rope_write, plan = ctypes_calls
         return
     _mvlaunch.bind(*(ctypes.cast(fn, ctypes.c_void_p).value for fn in ctypes_calls))
-    decode_write, decode, cache_write, rope_write = (_mvlaunch.decode_write, _mvlaunch.decode,
-                                                     _mvlaunch.cache_write, _mvlaunch.rope_write)
+    decode_write, decode, cache_write, rope_write, plan = (
+        _mvlaunch.decode_write, _mvlaunch.decode, _mvlaunch.cache_write, _mvlaunch.rope_write,
+        _mvlaunch.plan)
 
 
 def load(path: str | None = None) -> ctypes.CDLL:

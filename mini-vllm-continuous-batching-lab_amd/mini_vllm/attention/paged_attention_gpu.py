@@ -386,6 +386,22 @@ def _groups_per_cu(device: torch.device, head_dim: int, dtype: torch.dtype) -> T
     return split
 
 
+_IDS_CAPACITY: dict = {}
+
+
+def _ids_capacity(num_seqs: int, max_blocks: int, num_kv_heads: int, cap: int) -> int:
+    """``mv_decode_block_ids_capacity``, asked of the library once per shape
+    (steps of one batch shape share it)."""
+    key = (num_seqs, max_blocks, num_kv_heads, cap)
+    n = _IDS_CAPACITY.get(key)
+    if n is None:
+        if len(_IDS_CAPACITY) > 4096:
+            _IDS_CAPACITY.clear()
+        n = _IDS_CAPACITY[key] = _hip.load().mv_decode_block_ids_capacity(
+            num_seqs, max_blocks, num_kv_heads, cap)
+    return n
+
+
 def _decode_metadata(block_table: torch.Tensor, kv_len_after: torch.Tensor,
                      device: torch.device) -> Tuple[torch.Tensor, torch.Tensor]:
     """Block table ``[B, max_blocks]`` and kv lengths ``[B]`` on ``device``
@@ -503,26 +519,29 @@ def plan_decode(
                       cap * per_item)
     else:
         cap = num_seqs * num_kv_heads * max(1, math.ceil(max_blocks * block_size / 16))
-        ids_cap = lib.mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, cap)
+        ids_cap = _ids_capacity(num_seqs, max_blocks, num_kv_heads, cap)
     # one allocation, cut into the work list, block ids, counters and
-    # status words (each part 16-byte aligned)
+    # status words (each part 16-byte aligned); the launch takes the parts'
+    # addresses, and their views are made while the plan runs
     n_work, n_ids = 8 * max(cap, 1), -(-max(ids_cap, 4) // 4) * 4
-    n_cnt = -(-max(num_seqs * num_kv_heads, 1) // 4) * 4
+    n_units = max(num_seqs * num_kv_heads, 1)
+    n_cnt = -(-n_units // 4) * 4
     buf = torch.empty(n_work + n_ids + n_cnt + _hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
-    work = buf[:n_work]
-    block_ids = buf[n_work:n_work + n_ids]
-    counters = buf[n_work + n_ids:n_work + n_ids + max(num_seqs * num_kv_heads, 1)]
-    status = buf[n_work + n_ids + n_cnt:]
+    base = buf.data_ptr()
     _hip.check(
-        lib.mv_decode_plan(
-            _ptr(kv), int(kv.dtype == torch.int64), _ptr(bt), int(bt.dtype == torch.int64),
-            bt.stride(0) if bt.dim() == 2 else 0, num_seqs, max_blocks, block_size,
-            num_blocks, num_kv_heads, *split, fixed,
-            _ptr(work), cap, _ptr(block_ids), n_ids,
-            _ptr(counters), _ptr(status), _stream(device),
+        _hip.plan(
+            kv.data_ptr(), int(kv.dtype == torch.int64), bt.data_ptr(),
+            int(bt.dtype == torch.int64), bt.stride(0) if bt.dim() == 2 else 0, num_seqs,
+            max_blocks, block_size, num_blocks, num_kv_heads, split[0], split[1], fixed,
+            base, cap, base + 4 * n_work, n_ids, base + 4 * (n_work + n_ids),
+            base + 4 * (n_work + n_ids + n_cnt), _stream(device),
         ),
         "mv_decode_plan",
     )
+    work = buf[:n_work]
+    block_ids = buf[n_work:n_work + n_ids]
+    counters = buf[n_work + n_ids:n_work + n_ids + n_units]
+    status = buf[n_work + n_ids + n_cnt:]
 
     def raise_plan(st) -> None:
         if st[_hip.MV_PLAN_BAD_KV_LEN]:

@@ -249,10 +249,12 @@ def test_fast_call_wrappers_match_the_header(lib):
     assert _hip.decode is _mvlaunch.decode
     assert _hip.cache_write is _mvlaunch.cache_write
     assert _hip.rope_write is _mvlaunch.rope_write
+    assert _hip.plan is _mvlaunch.plan
     for fn, name in ((_mvlaunch.decode_write, "mv_paged_decode_write"),
                      (_mvlaunch.decode, "mv_paged_decode"),
                      (_mvlaunch.cache_write, "mv_kv_cache_write"),
-                     (_mvlaunch.rope_write, "mv_rope_kv_cache_write")):
+                     (_mvlaunch.rope_write, "mv_rope_kv_cache_write"),
+                     (_mvlaunch.plan, "mv_decode_plan")):
         n = declared[name]
         with pytest.raises(TypeError, match=f"takes {n} arguments"):
             fn(*([0] * (n - 1)))
