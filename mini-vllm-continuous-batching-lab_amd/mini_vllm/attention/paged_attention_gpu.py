@@ -212,8 +212,8 @@ def clear_deferred(capture_id: Optional[int] = None) -> None:
 
 
 # The eager (not captured) per-step checks and plans that _cache_get keeps.
-_EAGER_CACHES = ("slots", "fused", "plan", "fused_step", "rope_step", "rope_rows", "positions",
-                 "prefill")
+_EAGER_CACHES = ("slots", "fused", "plan", "fused_step", "rope_step", "write_step", "rope_rows",
+                 "positions", "prefill")
 
 
 def invalidate_cached_metadata() -> None:
@@ -321,13 +321,25 @@ def hip_cache_write(
     assert key.dtype in SUPPORTED_DTYPES, f"dtype {key.dtype} not supported"
     assert key_cache.is_contiguous() and value_cache.is_contiguous(), "cache must be contiguous"
 
-    if slot_mapping.device != key.device:
-        slot_mapping = slot_mapping.to(key.device)
-    if slot_mapping.dtype != torch.int64:
-        slot_mapping = slot_mapping.to(torch.int64)
-    slot_mapping = slot_mapping.contiguous()
     num_blocks = key_cache.shape[0]
-    _check_slots(slot_mapping, num_blocks * block_size)
+    # The other layers of an eager step: the checked slots' device copy
+    # from one lookup (same tensor, same version).
+    device = key.device
+    capture = _capture_id(device)
+    step_extra = (num_blocks * block_size, device)
+    step = None if capture else _cache_get("write_step", (slot_mapping,), step_extra)
+    if step is not None:
+        slot_mapping = step
+    else:
+        slots_given = slot_mapping
+        if slot_mapping.device != device:
+            slot_mapping = slot_mapping.to(device)
+        if slot_mapping.dtype != torch.int64:
+            slot_mapping = slot_mapping.to(torch.int64)
+        slot_mapping = slot_mapping.contiguous()
+        _check_slots(slot_mapping, num_blocks * block_size, capture=capture)
+        if not capture:
+            _cache_put("write_step", (slots_given,), step_extra, slot_mapping)
     if num_tokens == 0:
         return
     if key.stride(2) != 1:
