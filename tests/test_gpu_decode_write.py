@@ -198,3 +198,34 @@ def test_step_cache_sees_in_place_slot_edits():
     slots[1] = slots[2]
     with pytest.raises(AssertionError, match="Duplicate"):
         fused(d.key_cache.clone(), d.value_cache.clone())
+
+
+def test_ctypes_route_matches_the_fast_calls(monkeypatch):
+    """Without the fast-call extension the wrappers call the same entry
+    points through ctypes: the fused layer call, the decode and the write
+    give the same bits either way."""
+    from mini_vllm.attention import _hip
+
+    say("decode+write: ctypes route against the fast calls")
+    case = make_case("c2", seed=6, nan_fill=False)
+    bs = case.layout.spec.block_size
+    d = to_device(case)
+
+    def run():
+        kc, vc = d.key_cache.clone(), d.value_cache.clone()
+        fused = hip_decode_attention(d.query, kc, vc, d.block_table, d.kv_len, bs,
+                                     new_key=d.new_key, new_value=d.new_value,
+                                     slot_mapping=d.slot_mapping)
+        kc2, vc2 = d.key_cache.clone(), d.value_cache.clone()
+        hip_cache_write(d.new_key, d.new_value, kc2, vc2, d.slot_mapping, bs)
+        dec = hip_decode_attention(d.query, kc2, vc2, d.block_table, d.kv_len, bs)
+        torch.cuda.synchronize()
+        return fused, kc, vc, dec, kc2, vc2
+
+    fast = run()
+    lib = _hip.load()
+    monkeypatch.setattr(_hip, "decode_write", lib.mv_paged_decode_write)
+    monkeypatch.setattr(_hip, "decode", lib.mv_paged_decode)
+    monkeypatch.setattr(_hip, "cache_write", lib.mv_kv_cache_write)
+    slow = run()
+    _same(fast, slow)
