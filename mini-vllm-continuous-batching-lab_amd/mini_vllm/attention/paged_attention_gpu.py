@@ -706,7 +706,7 @@ def hip_decode_attention(
     # one lookup (same tensors at the same in-place versions).
     step = None
     step_extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads)
-    if new_key is not None and not capture:
+    if new_key is not None and slot_mapping is not None and not capture:
         step = _cache_get("fused_step", (slot_mapping, block_table, kv_len_after), step_extra)
     if step is not None:
         plan = step[0]
