@@ -176,6 +176,12 @@ __device__ __forceinline__ void store_coherent_u64(uint64_t* p, uint64_t v) {
 __device__ __forceinline__ uint64_t load_coherent_u64(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_coherent_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // Two fp32 values in one 8-byte word (lo = first in memory).
 __device__ __forceinline__ uint64_t pack_f32x2(float lo, float hi) {
   return static_cast<uint64_t>(__float_as_uint(lo)) | (static_cast<uint64_t>(__float_as_uint(hi)) << 32);
@@ -183,12 +189,22 @@ __device__ __forceinline__ uint64_t pack_f32x2(float lo, float hi) {
 __device__ __forceinline__ float unpack_lo(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
 __device__ __forceinline__ float unpack_hi(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); }
 
+// Split-K partial O rows of 16-bit data in the data's own type: a partial
+// row is a convex combination of V rows, so the type holds it, and the
+// final output is rounded to that type anyway. Half the bytes of fp32
+// partials on the merge's critical tail (stores, then the merger's loads);
+// the (max, sum) pairs stay fp32.
+#ifndef MV_DECODE_PARTIALS16
+#define MV_DECODE_PARTIALS16 1
+#endif
+
 // ----------------------------------------------------------- the kernel ---
 
 template <int DTYPE, int D, bool FUSED, bool ROPE>
 __global__ __launch_bounds__(kWaves * 64)
 __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged_decode_kernel(DecodeArgs a) {
   static_assert(FUSED || !ROPE, "the fused RoPE comes with the fused write");
+  constexpr bool kPartials16 = DTYPE != MV_DTYPE_F32 && MV_DECODE_PARTIALS16;
   using Tr = Traits<DTYPE, D>;
   using raw_t = typename Elem<DTYPE>::raw;
   constexpr int L = Tr::kLoads;
@@ -631,15 +647,33 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       }
     } else {
       const int64_t slot = slot_base + static_cast<int64_t>(r) * a.max_parts + part;
-      uint64_t* dst = reinterpret_cast<uint64_t*>(a.ws_o + slot * D + 2 * q);
+      if constexpr (kPartials16) {  // dims 2q + 32j, +1 as two 16-bit values
+        uint32_t* dst = reinterpret_cast<uint32_t*>(a.ws_o) + slot * (D / 2) + q;
 #pragma unroll
-      for (int j = 0; j < NPAIR; ++j) store_coherent_u64(dst + 16 * j, pack_f32x2(v[j].x * inv, v[j].y * inv));
+        for (int j = 0; j < NPAIR; ++j)
+          store_coherent_u32(dst + 16 * j,
+                             static_cast<uint32_t>(from_f32<DTYPE>(v[j].x * inv)) |
+                                 (static_cast<uint32_t>(from_f32<DTYPE>(v[j].y * inv)) << 16));
+      } else {
+        uint64_t* dst = reinterpret_cast<uint64_t*>(a.ws_o + slot * D + 2 * q);
+#pragma unroll
+        for (int j = 0; j < NPAIR; ++j) store_coherent_u64(dst + 16 * j, pack_f32x2(v[j].x * inv, v[j].y * inv));
+      }
       if (q == 0) store_coherent_u64(reinterpret_cast<uint64_t*>(a.ws_ml) + slot, pack_f32x2(mx, sum));
     }
   }
   if (n_parts == 1) return;
 
   // ---- cross-partition merge by the last work group --------------------
+  // (the partial O words: two fp32, or two values of the 16-bit data type)
+  auto ov_lo = [](uint64_t x) -> float {
+    if constexpr (kPartials16) return to_f32<DTYPE>(static_cast<uint16_t>(x));
+    else return unpack_lo(x);
+  };
+  auto ov_hi = [](uint64_t x) -> float {
+    if constexpr (kPartials16) return to_f32<DTYPE>(static_cast<uint16_t>(x >> 16));
+    else return unpack_hi(x);
+  };
   // The partials above are device-coherent stores; once every wave has
   // seen them acknowledged (vmcnt(0)), the counter increment publishes
   // them. The work group that completes the count reads all partials
@@ -675,9 +709,15 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       for (int pp = 0; pp < RR; ++pp) {
         const int64_t slot = slot0 + p0 + min(pp, np - 1);
         ml[pp] = load_coherent_u64(reinterpret_cast<const uint64_t*>(a.ws_ml) + slot);
-        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.ws_o + slot * D + 2 * q);
+        if constexpr (kPartials16) {
+          const uint32_t* src = reinterpret_cast<const uint32_t*>(a.ws_o) + slot * (D / 2) + q;
 #pragma unroll
-        for (int j = 0; j < NPAIR; ++j) ov[pp][j] = load_coherent_u64(src + 16 * j);
+          for (int j = 0; j < NPAIR; ++j) ov[pp][j] = load_coherent_u32(src + 16 * j);
+        } else {
+          const uint64_t* src = reinterpret_cast<const uint64_t*>(a.ws_o + slot * D + 2 * q);
+#pragma unroll
+          for (int j = 0; j < NPAIR; ++j) ov[pp][j] = load_coherent_u64(src + 16 * j);
+        }
       }
       float m_round = m_all;
 #pragma unroll
@@ -696,8 +736,8 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
         l_all += w;
 #pragma unroll
         for (int j = 0; j < NPAIR; ++j) {
-          acc[j].x += w * unpack_lo(ov[pp][j]);
-          acc[j].y += w * unpack_hi(ov[pp][j]);
+          acc[j].x += w * ov_lo(ov[pp][j]);
+          acc[j].y += w * ov_hi(ov[pp][j]);
         }
       }
       m_all = m_round;
