@@ -30,8 +30,9 @@ and on c2's shape.
 rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under profiles/ for the
 workload (``traffic_source`` names it). It is reported only when that
 summary was taken on the current decode kernel source (its
-``source_sha256`` line matches); otherwise it is null and
-``traffic_note`` says why.
+``source_sha256`` line matches the hash of the kernel's source files with
+comments and layout removed); otherwise it is null and ``traffic_note``
+says why.
 """
 
 from __future__ import annotations
@@ -417,13 +418,43 @@ KERNEL_SOURCES = ("csrc/paged_decode.hip", "csrc/mv_tile.h", "csrc/mv_common.h")
 COPY_BYTES = 256 << 20
 
 
+def code_without_comments(text):
+    """C/C++ source text with its comments removed and every run of blank
+    space collapsed to one space: what the compiler sees, so an edit of a
+    comment or of the layout leaves it unchanged. String and character
+    literals are kept as written."""
+    out, i, n = [], 0, len(text)
+    while i < n:
+        c = text[i]
+        if c == "/" and text.startswith("//", i):
+            j = text.find("\n", i)
+            i = n if j < 0 else j
+            out.append(" ")
+        elif c == "/" and text.startswith("/*", i):
+            j = text.find("*/", i + 2)
+            i = n if j < 0 else j + 2
+            out.append(" ")
+        elif c in "\"'":
+            j = i + 1
+            while j < n and text[j] != c:
+                j += 2 if text[j] == "\\" else 1
+            out.append(text[i:j + 1])
+            i = j + 1
+        else:
+            out.append(c)
+            i += 1
+    return " ".join("".join(out).split())
+
+
 def kernel_source_sha256():
     """Hash of the decode kernel's sources (the files a PMC profile of it
-    depends on), as written into the traffic summaries."""
+    depends on) without comments or layout, as written into the traffic
+    summaries."""
     h = hashlib.sha256()
     for rel in KERNEL_SOURCES:
-        with open(os.path.join(PKG, rel), "rb") as f:
-            h.update(f.read())
+        with open(os.path.join(PKG, rel), encoding="utf-8") as f:
+            h.update(code_without_comments(f.read()).encode())
+        h.update(b"\0")
     return h.hexdigest()
 
 

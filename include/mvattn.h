@@ -231,8 +231,9 @@ size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, in
  * status[MV_PLAN_PARTITION_TOKENS], max_partitions =
  * status[MV_PLAN_MAX_PARTS]; the block table itself is not read.
  * Sequences split into several partitions are merged inside the same
- * launch (log-sum-exp over fp32 partials in `workspace`,
- * mv_paged_decode_workspace_bytes); calls sharing one plan's counters or
+ * launch (log-sum-exp over partials in `workspace`: normalised O rows in
+ * the data type for F16 / BF16, fp32 for F32, and fp32 (max, sum) pairs;
+ * mv_paged_decode_workspace_bytes sizes the rows as fp32 for every dtype); calls sharing one plan's counters or
  * one workspace must be ordered on one stream. Output rows of sequences the
  * plan rejected are left untouched. Supported: head_dim 64 or 128,
  * block_size a power of two, num_q_heads / num_kv_heads in [1, 16], dtype

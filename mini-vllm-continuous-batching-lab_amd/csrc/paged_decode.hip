@@ -150,7 +150,7 @@ struct DecodeArgs {
   int32_t* counters;  // [num_seqs * num_kv_heads], zero at rest
   void* out;
   int64_t out_stride_tok, out_stride_head;  // elements
-  float* ws_o;                              // [num_seqs, Hq, max_parts, D]
+  float* ws_o;                              // [num_seqs, Hq, max_parts, D], 16-bit rows for F16/BF16
   float* ws_ml;                             // [num_seqs, Hq, max_parts, 2]: (max, sum)
   // Fused KV write of the step's new tokens (FUSED kernels only): row b of
   // new_k / new_v goes to pool slot slots[b].
@@ -1308,6 +1308,8 @@ __global__ __launch_bounds__(kIdsThreads) void decode_ids_kernel(IdsArgs a) {
 
 // ------------------------------------------------------------- dispatch ---
 
+// Partial O rows sized as fp32 for every dtype (the workspace size takes no
+// dtype); 16-bit rows use the first half.
 size_t ws_o_bytes(int64_t num_seqs, int64_t hq, int64_t d, int64_t parts) {
   return static_cast<size_t>(num_seqs * hq * parts * d * 4);
 }
@@ -1644,7 +1646,7 @@ extern "C" int mv_paged_decode(const void* query, int64_t q_stride_tok, int64_t 
 
 // ---------------------------------------------------- no-allocation decode ---
 // mv_paged_decode for callers that cannot allocate (graph capture, serving
-// loops that forbid it): the fp32 partials of the split-K merge live in this
+// loops that forbid it): the partials of the split-K merge live in this
 // file-scope array instead of a caller's workspace. Every GPU the library
 // runs on holds one copy (MV_DECODE_SCRATCH_BYTES) until the process ends;
 // all calls on that GPU share it, so calls that overlap on one GPU race.

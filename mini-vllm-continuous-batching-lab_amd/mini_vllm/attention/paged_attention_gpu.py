@@ -125,7 +125,7 @@ _WORKSPACE_LOCK = threading.Lock()
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Grow-only, never-freed per-device fp32 partial buffer of the decode
+    """Grow-only, never-freed per-device partial buffer of the decode
     merge."""
     ws = _WORKSPACES.get(device)
     if ws is not None and ws.numel() >= nbytes:
