@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define MVATTN_ABI_VERSION 4
+#define MVATTN_ABI_VERSION 5
 
 /* Element types of query / key / value / cache / output. */
 #define MV_DTYPE_F32 0
@@ -412,6 +412,50 @@ int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_h
                      int64_t out_stride_tok, int64_t out_stride_head, float scale,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream);
+
+/*
+ * Bytes of the workspace mv_paged_prefill_parts needs for num_units units
+ * cut into at most max_parts parts (0 when max_parts <= 1 or the head
+ * shape is unsupported). Its first 64 KiB are the units' counters and must
+ * be zero before the first call; every call leaves them zero again.
+ */
+size_t mv_paged_prefill_workspace_bytes(int32_t num_units, int32_t max_parts,
+                                        int32_t num_q_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, int32_t dtype);
+
+/*
+ * mv_paged_prefill with the keys of a unit (one (sequence, kv head, token
+ * block) of mv_paged_prefill's work list) cut into parts, one work group
+ * each, for launches with fewer units than the device has CUs (one long
+ * sequence's chunk: 64 units at 512 tokens). No counterpart in the
+ * reference, whose prefill runs one SDPA per sequence; the result is that
+ * of mv_paged_prefill on the same units within fp32 rounding of the
+ * log-sum-exp merge, and it does not depend on which part finishes last.
+ *   work_items  int32[8] per work group: the 4 of mv_paged_prefill, then
+ *               (first key, end key, unit, part | parts << 8 |
+ *               max_parts << 16): the part's keys [first key, min(end key,
+ *               cached + first token + tokens)), first key a multiple of
+ *               256 and the parts of a unit contiguous from key 0, units
+ *               numbered 0 .. num_units-1 (at most 16384), parts 0 ..
+ *               parts-1 (parts <= max_parts <= 8); every part of a unit
+ *               in the same launch;
+ *   workspace   mv_paged_prefill_workspace_bytes(num_units, max_parts, ..)
+ *               bytes, 256-byte aligned, counters zero (see there); calls
+ *               sharing one workspace must be ordered on one stream.
+ * The part that completes a unit's count folds the parts in part order and
+ * writes the unit's rows of out.
+ */
+int mv_paged_prefill_parts(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                           const void* key, int64_t k_stride_tok, int64_t k_stride_head,
+                           const void* value, int64_t v_stride_tok, int64_t v_stride_head,
+                           const void* key_cache, const void* value_cache, const void* block_table,
+                           int32_t bt_is_i64, int64_t bt_stride, const int64_t* seqs,
+                           int32_t num_seqs, const int32_t* work_items, int32_t num_work_groups,
+                           int32_t num_units, int32_t max_parts, void* out,
+                           int64_t out_stride_tok, int64_t out_stride_head, float scale,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t block_size, int64_t num_blocks, int32_t dtype, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /*
  * Device-side plan of mv_paged_prefill for a launch of fixed size, e.g.

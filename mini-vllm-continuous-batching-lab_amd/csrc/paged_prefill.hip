@@ -32,9 +32,19 @@
 // end; the other instantiations one set (R = 1, T = 1). Waves skip
 // sub-tiles that lie wholly past their rows' causal limit; the online
 // softmax is updated once per stage.
+//
+// Key split (mv_paged_prefill_parts): when a launch has fewer (sequence, kv
+// head, token block) units than the device has CUs, the host cuts a unit's
+// keys into parts at stage boundaries, one work group each. A part leaves
+// its rows' normalised O and (max, sum) in a workspace with device-coherent
+// stores and counts itself on the unit's counter; the work group that
+// completes the count folds the parts in part order (log-sum-exp) and
+// writes the rows, so the result does not depend on which part finishes
+// last.
 #include <algorithm>
 #include <climits>
 
+#include "mv_coherent.h"
 #include "mv_common.h"
 #include "mv_tile.h"
 
@@ -42,6 +52,11 @@ namespace mv {
 namespace {
 
 constexpr int kPfIdCap = 2048;  // prefix block ids staged in LDS per window
+// Key split: at most kPfMaxParts parts per unit, kPfMaxUnits units per launch
+// (the workspace's counters come first, kPfCountersBytes of them).
+constexpr int kPfMaxParts = 8;
+constexpr int kPfMaxUnits = 16384;
+constexpr int kPfCountersBytes = kPfMaxUnits * 4;
 // Waves per work group: 8 (twice the query rows per pass over the keys,
 // and more waves to hide latency -- 39.8 us against 46.7 us with 4, two
 // such groups then sharing a CU, on a 4 x (1536 + 512) bf16 step) when two
@@ -133,6 +148,14 @@ struct PrefillArgs {
   int32_t num_kv_heads, n_rep, tpw, bs_log2;
   uint32_t num_blocks_u32;
   int32_t lane_offsets_32;  // 16 chunk rows of K and of V span < 2 GiB: 32-bit lane offsets
+  // Key split: work items of 8 ints whose second half is (first key, end
+  // key, unit, part | parts << 8 | max parts << 16); 4 ints: whole key
+  // ranges, no split.
+  int32_t item_ints;
+  // The split's workspace: kPfMaxUnits int32 counters (parts done per
+  // unit, zero at rest), then per unit max parts blocks of kRowWaves * tpw
+  // * n_rep records (D normalised fp32 values, the fp32 (max, sum) pair).
+  char* ws;
 };
 
 template <int DTYPE, int D, typename BT>
@@ -159,13 +182,23 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   const int rwave = Tr::kSets == 1 ? wave : wave % Tr::kRowWaves;  // rows
   const int set = Tr::kSets == 1 ? 0 : wave / Tr::kRowWaves;       // sub-tiles set * U .. of every stage
 
-  const int4 w = reinterpret_cast<const int4*>(a.work)[blockIdx.x];
+  const int4 w = reinterpret_cast<const int4*>(a.work)[blockIdx.x * (a.item_ints >> 2)];
   if (w.x < 0) return;  // an unused slot of a launch of fixed size
   const int seq = w.x, h = w.y, tok0 = w.z, ntok = w.w;
+  // the key range of a split unit (its part number and count are read
+  // again after the key loop, where they are used: registers are full)
+  int kb0 = 0, kb1 = INT_MAX;
+  if (a.item_ints == 8) {
+    const int4 w2 = reinterpret_cast<const int4*>(a.work)[blockIdx.x * 2 + 1];
+    kb0 = w2.x;
+    kb1 = w2.y;
+  }
   const int64_t row = a.seqs[4 * seq];
   const int cached = static_cast<int>(a.seqs[4 * seq + 1]);
   const int64_t qbase = a.seqs[4 * seq + 2] + tok0;  // chunk row of token tok0
-  const int key_end = cached + tok0 + ntok;           // keys of the work group: [0, key_end)
+  // keys of this work group: [kb0, key_end); the rows see keys below
+  // cached + tok0 + ntok, and a part ends at a stage boundary below that
+  const int key_end = min(cached + tok0 + ntok, kb1);
   const int bs_mask = (1 << a.bs_log2) - 1;
 
   // ---- rows of this wave: limits and Q (registers, straight from HBM)
@@ -492,7 +525,9 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   };
 
   // ---- windows of kPfIdCap prefix blocks (one window below 2048 blocks)
-  for (int win0 = 0; win0 < key_end; win0 += win_tokens) {
+  // (first: the first key of the window's stages, a stage boundary)
+  for (int first = kb0; first < key_end;) {
+    const int win0 = first / win_tokens * win_tokens;
     win_blk0 = win0 >> a.bs_log2;
     if (win0 < cached) {
       const int pref_end = min(cached, win0 + win_tokens);
@@ -501,8 +536,8 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         s_ids[i] = static_cast<int32_t>(btp[row * a.bt_stride + win_blk0 + i]);
     }
     __syncthreads();  // block ids of the window visible; previous window's stages released
-    const int k0 = win0 / kPfStageTokens;
-    const int n = (min(key_end, win0 + win_tokens) - win0 + kPfStageTokens - 1) / kPfStageTokens;
+    const int k0 = first / kPfStageTokens;
+    const int n = (min(key_end, win0 + win_tokens) - first + kPfStageTokens - 1) / kPfStageTokens;
     unsigned valid[S];
     valid[0] = issue(k0, IntC<0>{});
     if constexpr (S > 2) {
@@ -532,6 +567,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
       }
     }
     __syncthreads();  // every wave is done with this window's stages and ids
+    first = win0 + win_tokens;
   }
 
   // Lane coordinates recomputed for the epilogue rather than kept live
@@ -560,7 +596,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
       }
     }
     __syncthreads();
-    if (set == 1) return;
+    if (set == 0) {
 #pragma unroll
     for (int rt = 0; rt < R; ++rt) {
       const float m1 = xm[rt * 16 + te];
@@ -570,6 +606,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
       const float a0 = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
       const float a1 = __builtin_amdgcn_exp2f(m1 - m_ref);
       l_run[rt] = l_run[rt] * a0 + l1 * a1;
+      m_run[rt] = m;  // (max, sum) of both sets: a key-split part stores them
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float a0r = __shfl(a0, 4 * ge + e);
@@ -579,26 +616,123 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
           o[rt][c][e] = o[rt][c][e] * a0r + xo[((rt * (D / 16) + c) * 4 + e) * 64] * a1r;
       }
     }
-  }
-
-  // ---- normalise and store this wave's rows
-#pragma unroll
-  for (int rt = 0; rt < R; ++rt) {
-    const float inv = l_run[rt] > 0.f ? 1.f / l_run[rt] : 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int rr = 4 * ge + e;  // row of o[rt][.][e]
-      const float ir = __shfl(inv, rr);
-      const int r = rt * 16 + rr;
-      const int rtok = wtok0 + r / a.n_rep;
-      if (r < a.tpw * a.n_rep && rtok < ntok) {
-        raw_t* op = static_cast<raw_t*>(a.out) + (qbase + rtok) * a.o_st +
-                    (h * a.n_rep + r % a.n_rep) * a.o_sh;
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) op[16 * c + te] = from_f32<DTYPE>(o[rt][c][e] * ir);
-      }
     }
   }
+  const bool rows_owner = Tr::kSets == 1 || set == 0;  // holds its rows' merged state
+
+  // n_rep again, opaque to the compiler: its division constants are
+  // recomputed here rather than held in a register through the key loop
+  int n_rep_e = a.n_rep;
+  asm volatile("" : "+s"(n_rep_e));
+  // ---- normalise and store this wave's rows: to the output, or as this
+  // part's partial rows (row index within the unit: token * n_rep + head)
+  int unit = 0, part = 0, nparts = 1, max_parts = 1;
+  if (a.item_ints == 8) {
+    const int4 w2 = reinterpret_cast<const int4*>(a.work)[blockIdx.x * 2 + 1];
+    unit = w2.z;
+    part = w2.w & 0xff;
+    nparts = (w2.w >> 8) & 0xff;
+    max_parts = w2.w >> 16;
+  }
+  constexpr int kRec = D + 2;  // floats per record: the row, then (max, sum)
+  const int rows_cap = Tr::kRowWaves * a.tpw * n_rep_e;
+  float* recs = reinterpret_cast<float*>(a.ws + kPfCountersBytes) +
+                static_cast<int64_t>(unit) * max_parts * rows_cap * kRec;
+  int32_t* counter = reinterpret_cast<int32_t*>(a.ws) + unit;
+  if (rows_owner) {
+    const int64_t pbase = static_cast<int64_t>(part) * rows_cap + static_cast<int64_t>(rwave) * a.tpw * n_rep_e;
+#pragma unroll
+    for (int rt = 0; rt < R; ++rt) {
+      const float inv = l_run[rt] > 0.f ? 1.f / l_run[rt] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rr = 4 * ge + e;  // row of o[rt][.][e]
+        const float ir = __shfl(inv, rr);
+        const int r = rt * 16 + rr;
+        const int rtok = wtok0 + r / n_rep_e;
+        if (r < a.tpw * n_rep_e && rtok < ntok) {
+          if (nparts == 1) {
+            raw_t* op = static_cast<raw_t*>(a.out) + (qbase + rtok) * a.o_st +
+                        (h * n_rep_e + r % n_rep_e) * a.o_sh;
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) op[16 * c + te] = from_f32<DTYPE>(o[rt][c][e] * ir);
+          } else {
+            uint32_t* pp = reinterpret_cast<uint32_t*>(recs + (pbase + r) * kRec);
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) store_coherent_u32(pp + 16 * c + te, __float_as_uint(o[rt][c][e] * ir));
+          }
+        }
+      }
+      const int r = rt * 16 + te;  // the (max, sum) of row te, from the lanes ge == 0
+      if (nparts > 1 && ge == 0 && r < a.tpw * n_rep_e && wtok0 + r / n_rep_e < ntok)
+        store_coherent_u64(reinterpret_cast<uint64_t*>(recs + (pbase + r) * kRec + D), pack_f32x2(m_run[rt], l_run[rt]));
+    }
+  }
+  if (nparts == 1) return;
+
+  // ---- the part that completes the unit's count folds all parts: the
+  // partial rows above are device-coherent stores; once every wave has seen
+  // them acknowledged, the counter increment publishes them
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == nparts - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  constexpr int kRowThreads = D / 16;  // 16 dims (8 fp32 pairs) per thread
+  const int nrows = ntok * n_rep_e;
+  const int d0 = (threadIdx.x % kRowThreads) * 16;
+  for (int gr = threadIdx.x / kRowThreads; gr < nrows; gr += kPfWaves * 64 / kRowThreads) {
+    const float* rec0 = recs + static_cast<int64_t>(gr) * kRec;
+    float m_all = kNegInf, l_all = 0.f;
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    // rounds of 4 parts, every load of a round in flight before the first use
+    for (int p0 = 0; p0 < nparts; p0 += 4) {
+      uint64_t ml[4], ov[4][8];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const float* rec = rec0 + static_cast<int64_t>(min(p0 + pp, nparts - 1)) * rows_cap * kRec;
+        ml[pp] = load_coherent_u64(reinterpret_cast<const uint64_t*>(rec + D));
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(rec + d0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ov[pp][j] = load_coherent_u64(src + j);
+      }
+      float m_round = m_all;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp)
+        if (p0 + pp < nparts) m_round = fmaxf(m_round, unpack_lo(ml[pp]));
+      // every row sees key 0, which part 0 holds: m_round is finite
+      const float rescale = m_all == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m_all - m_round);
+      l_all *= rescale;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] *= rescale;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const float mp = unpack_lo(ml[pp]);
+        const float wgt = p0 + pp < nparts && mp != kNegInf
+                              ? unpack_hi(ml[pp]) * __builtin_amdgcn_exp2f(mp - m_round) : 0.f;
+        l_all += wgt;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          acc[2 * j] += wgt * unpack_lo(ov[pp][j]);
+          acc[2 * j + 1] += wgt * unpack_hi(ov[pp][j]);
+        }
+      }
+      m_all = m_round;
+    }
+    const float inv = 1.f / l_all;
+    raw_t* op = static_cast<raw_t*>(a.out) + (qbase + gr / n_rep_e) * a.o_st +
+                (h * n_rep_e + gr % n_rep_e) * a.o_sh + d0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) op[i] = from_f32<DTYPE>(acc[i] * inv);
+  }
+  if (threadIdx.x == 0)  // ready for the next call
+    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int DTYPE, int D>
@@ -753,17 +887,36 @@ extern "C" int mv_prefill_tokens_per_group(int32_t num_q_heads, int32_t num_kv_h
   return mv::by_type<mv::TokensPerGroup>(head_dim, dtype, num_q_heads / num_kv_heads);
 }
 
-extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
-                                const void* key, int64_t k_stride_tok, int64_t k_stride_head,
-                                const void* value, int64_t v_stride_tok, int64_t v_stride_head,
-                                const void* key_cache, const void* value_cache,
-                                const void* block_table, int32_t bt_is_i64, int64_t bt_stride,
-                                const int64_t* seqs, int32_t num_seqs, const int32_t* work_items,
-                                int32_t num_work_groups, void* out, int64_t out_stride_tok,
-                                int64_t out_stride_head, float scale, int32_t num_q_heads,
-                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                int64_t num_blocks, int32_t dtype, void* stream) {
-  using namespace mv;
+extern "C" size_t mv_paged_prefill_workspace_bytes(int32_t num_units, int32_t max_parts,
+                                                   int32_t num_q_heads, int32_t num_kv_heads,
+                                                   int32_t head_dim, int32_t dtype) {
+  const int tpg = mv_prefill_tokens_per_group(num_q_heads, num_kv_heads, head_dim, dtype);
+  if (tpg == 0 || num_units <= 0 || max_parts <= 1) return 0;
+  const size_t rows = static_cast<size_t>(num_units) * max_parts * tpg * (num_q_heads / num_kv_heads);
+  return mv::kPfCountersBytes + rows * (head_dim + 2) * 4;
+}
+
+namespace mv {
+namespace {
+
+// Key split of mv_paged_prefill_parts (null for mv_paged_prefill).
+struct PrefillParts {
+  int32_t num_units;
+  int32_t max_parts;
+  void* workspace;
+  size_t workspace_bytes;
+};
+
+int paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                  const void* key, int64_t k_stride_tok, int64_t k_stride_head,
+                  const void* value, int64_t v_stride_tok, int64_t v_stride_head,
+                  const void* key_cache, const void* value_cache, const void* block_table,
+                  int32_t bt_is_i64, int64_t bt_stride, const int64_t* seqs, int32_t num_seqs,
+                  const int32_t* work_items, int32_t num_work_groups, void* out,
+                  int64_t out_stride_tok, int64_t out_stride_head, float scale,
+                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                  int32_t block_size, int64_t num_blocks, int32_t dtype,
+                  const PrefillParts* parts, void* stream) {
   const int eb = dtype_bytes(dtype);
   if (eb == 0) return fail(MV_ERR_UNSUPPORTED, "mv_paged_prefill: unknown dtype %d", dtype);
   if (head_dim != 64 && head_dim != 128)
@@ -816,6 +969,26 @@ extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t
     const int64_t span = 16 * std::max(std::abs(a.k_st), std::abs(a.v_st)) + 16 * head_dim * eb;
     a.lane_offsets_32 = a.k_st >= 0 && a.v_st >= 0 && span < (int64_t(1) << 31);
   }
+  a.item_ints = 4;
+  a.ws = nullptr;
+  if (parts) {
+    a.item_ints = 8;
+    if (parts->num_units < 0 || parts->num_units > kPfMaxUnits || parts->max_parts < 1 ||
+        parts->max_parts > kPfMaxParts)
+      return fail(MV_ERR_INVALID_ARGUMENT,
+                  "mv_paged_prefill_parts: %d units of %d parts (at most %d units, %d parts)",
+                  parts->num_units, parts->max_parts, kPfMaxUnits, kPfMaxParts);
+    if (parts->max_parts > 1) {
+      const size_t need = mv_paged_prefill_workspace_bytes(parts->num_units, parts->max_parts,
+                                                           num_q_heads, num_kv_heads, head_dim, dtype);
+      if (!parts->workspace || parts->workspace_bytes < need)
+        return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_prefill_parts: workspace %zu bytes, need %zu",
+                    parts->workspace_bytes, need);
+      if (reinterpret_cast<uintptr_t>(parts->workspace) % 256)
+        return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_prefill_parts: workspace not 256-byte aligned");
+      a.ws = static_cast<char*>(parts->workspace);
+    }
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool i64 = bt_is_i64 != 0;
   const int n_rep = num_q_heads / num_kv_heads;
@@ -824,4 +997,44 @@ extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t
     case MV_DTYPE_F16: return launch_prefill_d<MV_DTYPE_F16>(a, head_dim, n_rep, num_work_groups, i64, s);
     default: return launch_prefill_d<MV_DTYPE_BF16>(a, head_dim, n_rep, num_work_groups, i64, s);
   }
+}
+
+}  // namespace
+}  // namespace mv
+
+extern "C" int mv_paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                                const void* key, int64_t k_stride_tok, int64_t k_stride_head,
+                                const void* value, int64_t v_stride_tok, int64_t v_stride_head,
+                                const void* key_cache, const void* value_cache,
+                                const void* block_table, int32_t bt_is_i64, int64_t bt_stride,
+                                const int64_t* seqs, int32_t num_seqs, const int32_t* work_items,
+                                int32_t num_work_groups, void* out, int64_t out_stride_tok,
+                                int64_t out_stride_head, float scale, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                int64_t num_blocks, int32_t dtype, void* stream) {
+  return mv::paged_prefill(query, q_stride_tok, q_stride_head, key, k_stride_tok, k_stride_head,
+                           value, v_stride_tok, v_stride_head, key_cache, value_cache, block_table,
+                           bt_is_i64, bt_stride, seqs, num_seqs, work_items, num_work_groups, out,
+                           out_stride_tok, out_stride_head, scale, num_q_heads, num_kv_heads,
+                           head_dim, block_size, num_blocks, dtype, nullptr, stream);
+}
+
+extern "C" int mv_paged_prefill_parts(const void* query, int64_t q_stride_tok, int64_t q_stride_head,
+                                      const void* key, int64_t k_stride_tok, int64_t k_stride_head,
+                                      const void* value, int64_t v_stride_tok, int64_t v_stride_head,
+                                      const void* key_cache, const void* value_cache,
+                                      const void* block_table, int32_t bt_is_i64, int64_t bt_stride,
+                                      const int64_t* seqs, int32_t num_seqs,
+                                      const int32_t* work_items, int32_t num_work_groups,
+                                      int32_t num_units, int32_t max_parts, void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                                      float scale, int32_t num_q_heads, int32_t num_kv_heads,
+                                      int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                      int32_t dtype, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  const mv::PrefillParts parts{num_units, max_parts, workspace, workspace_bytes};
+  return mv::paged_prefill(query, q_stride_tok, q_stride_head, key, k_stride_tok, k_stride_head,
+                           value, v_stride_tok, v_stride_head, key_cache, value_cache, block_table,
+                           bt_is_i64, bt_stride, seqs, num_seqs, work_items, num_work_groups, out,
+                           out_stride_tok, out_stride_head, scale, num_q_heads, num_kv_heads,
+                           head_dim, block_size, num_blocks, dtype, &parts, stream);
 }

@@ -14,7 +14,7 @@ import threading
 
 import torch  # noqa: F401  (must be loaded before the kernel library)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MV_OK = 0
 MV_ERR_INVALID_ARGUMENT = -1
@@ -143,6 +143,20 @@ SIGNATURES = {
         _P, _I64, _I64,            # out, strides
         _F, _I32, _I32, _I32,      # scale, num_q_heads, num_kv_heads, head_dim
         _I32, _I64, _I32, _P,      # block_size, num_blocks, dtype, stream
+    ]),
+    "mv_paged_prefill_workspace_bytes": (ctypes.c_size_t, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "mv_paged_prefill_parts": (ctypes.c_int, [
+        _P, _I64, _I64,            # query, strides
+        _P, _I64, _I64,            # key, strides
+        _P, _I64, _I64,            # value, strides
+        _P, _P,                    # key_cache, value_cache
+        _P, _I32, _I64,            # block_table, bt_is_i64, bt_stride
+        _P, _I32, _P, _I32,        # seqs, num_seqs, work_items (8 ints each), num_work_groups
+        _I32, _I32,                # num_units, max_parts
+        _P, _I64, _I64,            # out, strides
+        _F, _I32, _I32, _I32,      # scale, num_q_heads, num_kv_heads, head_dim
+        _I32, _I64, _I32,          # block_size, num_blocks, dtype
+        _P, ctypes.c_size_t, _P,   # workspace, workspace_bytes, stream
     ]),
 }
 

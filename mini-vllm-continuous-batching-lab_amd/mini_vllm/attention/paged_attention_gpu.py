@@ -1065,6 +1065,33 @@ def _check_prefix_tables(bt_host: torch.Tensor, rows: Sequence[int], lens: Seque
             )
 
 
+PREFILL_MAX_PARTS = 8     # key parts per prefill unit (mv_paged_prefill_parts)
+PREFILL_PART_KEYS = 256   # parts start at multiples of this many keys
+
+
+def prefill_key_parts(key_ends: Sequence[int], cu_count: int,
+                      max_parts: int = PREFILL_MAX_PARTS) -> List[List[Tuple[int, int]]]:
+    """Key ranges of the parts of each prefill unit (one (sequence, kv head,
+    token block) work group, whose rows see keys ``[0, key_end)``).
+
+    A launch of fewer units than ``cu_count`` leaves CUs idle, so each unit
+    is cut at multiples of ``PREFILL_PART_KEYS`` into up to
+    ``min(max_parts, cu_count // units)`` parts of at least two such blocks,
+    one work group each (``mv_paged_prefill_parts``). Returns
+    ``[(first key, end key), ...]`` per unit; ``[(0, key_end)]`` for a unit
+    that is not cut.
+    """
+    n = len(key_ends)
+    split = max(1, min(max_parts, cu_count // n)) if 0 < n < cu_count else 1
+    out = []
+    for ke in key_ends:
+        blocks = -(-ke // PREFILL_PART_KEYS)
+        parts = max(1, min(split, blocks // 2))
+        bounds = [(p * blocks // parts) * PREFILL_PART_KEYS for p in range(parts)] + [ke]
+        out.append([(bounds[p], bounds[p + 1]) for p in range(parts)])
+    return out
+
+
 def _prefill_plan(block_table, rows, cached, qlens, block_size, num_blocks, num_q_heads,
                   num_kv_heads, head_dim, dtype, device):
     """Validated table and device work list of one step's prefill, built once:
@@ -1074,6 +1101,11 @@ def _prefill_plan(block_table, rows, cached, qlens, block_size, num_blocks, num_
 
     Work groups are (sequence, kv head, first token, tokens), the most keys
     first; per sequence (table row, cached, first chunk row, chunk tokens).
+    When the units are fewer than the CUs their keys are cut into parts
+    (``prefill_key_parts``): the work groups then carry (first key, end key,
+    unit, part | parts << 8 | max parts << 16) as well, and the plan its own
+    workspace for the merge (counters zero). ``MVATTN_PREFILL_PARTS`` caps
+    the parts per unit (1: no cut).
     """
     lib = _hip.load()
     extra = (tuple(rows), tuple(cached), tuple(qlens), block_size, num_blocks, num_q_heads,
@@ -1108,10 +1140,27 @@ def _prefill_plan(block_table, rows, cached, qlens, block_size, num_blocks, num_
                 items.append((i, h, t0, nt))
                 keys.append(c + t0 + nt)
         start += ql
-    order = sorted(range(len(items)), key=lambda k: -keys[k])
-    work = torch.tensor([items[k] for k in order] or [(0, 0, 0, 0)], dtype=torch.int32)
+    cap = int(os.environ.get("MVATTN_PREFILL_PARTS", PREFILL_MAX_PARTS))
+    parts = prefill_key_parts(keys, _groups_per_cu(device, head_dim, dtype)[1], cap)
+    max_parts = max((len(p) for p in parts), default=1)
+    split = None
+    if max_parts > 1:
+        groups = [(*items[u], k0, k1, u, p | len(pr) << 8 | max_parts << 16)
+                  for u, pr in enumerate(parts) for p, (k0, k1) in enumerate(pr)]
+        groups.sort(key=lambda g: g[4] - g[5])  # the most keys first
+        work = torch.tensor(groups, dtype=torch.int32)
+        ws_bytes = lib.mv_paged_prefill_workspace_bytes(len(items), max_parts, num_q_heads,
+                                                        num_kv_heads, head_dim,
+                                                        _hip.MV_DTYPE[dtype])
+        # the plan's own merge workspace: its counters start at zero and every
+        # launch leaves them so; the layers of a step share it on one stream
+        split = (len(items), max_parts, torch.zeros(ws_bytes, dtype=torch.uint8, device=device))
+    else:
+        order = sorted(range(len(items)), key=lambda k: -keys[k])
+        work = torch.tensor([items[k] for k in order] or [(0, 0, 0, 0)], dtype=torch.int32)
     meta = torch.tensor(seqs or [(0, 0, 0, 0)], dtype=torch.int64)
-    plan = (bt, meta.to(device, non_blocking=True), work.to(device, non_blocking=True), len(items))
+    plan = (bt, meta.to(device, non_blocking=True), work.to(device, non_blocking=True),
+            work.shape[0] if items else 0, split)
     _cache_put("prefill", (block_table,), extra, plan)
     return plan
 
@@ -1271,6 +1320,7 @@ def hip_prefill_attention(
         bt, meta, work, n_work = _prefill_device_plan(
             block_table, rows, cached_len_before, query_len, total_q, block_size, num_blocks,
             num_q_heads, num_kv_heads, head_dim, query.dtype, device, capture)
+        split = None
     else:
         def host_ints(x):
             return x.tolist() if isinstance(x, torch.Tensor) else x
@@ -1285,25 +1335,25 @@ def hip_prefill_attention(
         out = torch.empty(total, num_q_heads, head_dim, dtype=query.dtype, device=device)
         if total == 0:
             return out
-        bt, meta, work, n_work = _prefill_plan(block_table, rows, cached, qlens, block_size,
-                                               num_blocks, num_q_heads, num_kv_heads, head_dim,
-                                               query.dtype, device)
+        bt, meta, work, n_work, split = _prefill_plan(block_table, rows, cached, qlens,
+                                                      block_size, num_blocks, num_q_heads,
+                                                      num_kv_heads, head_dim, query.dtype, device)
 
     q = _aligned_rows(query)
     k = _aligned_rows(key)
     v = _aligned_rows(value)
-    _hip.check(
-        lib.mv_paged_prefill(
-            _ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), k.stride(1),
+    head = (_ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), k.stride(1),
             _ptr(v), v.stride(0), v.stride(1), _ptr(key_cache), _ptr(value_cache),
             _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
-            bt.stride(0) if bt.numel() else 0, _ptr(meta), len(rows), _ptr(work), n_work,
-            _ptr(out), out.stride(0), out.stride(1), float(head_dim ** -0.5), num_q_heads,
-            num_kv_heads, head_dim, block_size, num_blocks, _hip.MV_DTYPE[query.dtype],
-            _stream(device),
-        ),
-        "mv_paged_prefill",
-    )
+            bt.stride(0) if bt.numel() else 0, _ptr(meta), len(rows), _ptr(work), n_work)
+    tail = (_ptr(out), out.stride(0), out.stride(1), float(head_dim ** -0.5), num_q_heads,
+            num_kv_heads, head_dim, block_size, num_blocks, _hip.MV_DTYPE[query.dtype])
+    if split is None:
+        _hip.check(lib.mv_paged_prefill(*head, *tail, _stream(device)), "mv_paged_prefill")
+    else:
+        units, max_parts, ws = split
+        _hip.check(lib.mv_paged_prefill_parts(*head, units, max_parts, *tail, _ptr(ws), ws.numel(),
+                                              _stream(device)), "mv_paged_prefill_parts")
     return out
 
 

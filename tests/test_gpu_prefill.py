@@ -11,7 +11,8 @@ import pytest
 import torch
 
 from gpu_util import DEV, TOL, say
-from mini_vllm.attention import AttentionBackend
+from mini_vllm.attention import AttentionBackend, _hip
+from mini_vllm.attention import paged_attention_gpu as pag
 from mini_vllm.attention.paged_attention_gpu import hip_prefill_attention
 from mini_vllm.model_runner.base import AttentionGroup, AttentionMetadata, ModelConfig
 from oracle import paged_ref
@@ -162,3 +163,65 @@ def test_backend_prefill_groups():
     torch.cuda.synchronize()
     err = (out.float().cpu() - _ref(c)).abs().max().item()
     assert err <= TOL[torch.bfloat16], err
+
+
+# ---- key split (mv_paged_prefill_parts): launches with fewer units than CUs
+
+def _max_parts(c):
+    """The most parts the plan cuts a unit of this case into."""
+    lib = _hip.load()
+    tpg = lib.mv_prefill_tokens_per_group(c["hq"], c["hkv"], c["d"], _hip.MV_DTYPE[c["dtype"]])
+    keys = [cc + t0 + min(tpg, q - t0) for cc, q in zip(c["cached"], c["qlen"])
+            for t0 in range(0, q, tpg) for _ in range(c["hkv"])]
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    return max(len(p) for p in pag.prefill_key_parts(keys, cus))
+
+
+SPLIT_SHAPES = [  # (hq, hkv, d, bs, dtype): units of one 512-token chunk, parts
+    (14, 2, 64, 16, torch.bfloat16),   # 64 units, 4 parts
+    (14, 2, 64, 16, torch.float32),    # 64 units, 4 parts
+    (28, 4, 128, 16, torch.bfloat16),  # 128 units, 2 parts
+    (8, 8, 64, 32, torch.float16),     # n_rep 1: 32 units, 8 parts
+    (16, 1, 128, 16, torch.bfloat16),  # n_rep 16: 64 units, 4 parts
+]
+
+
+@pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=lambda s: f"{s[0]}-{s[1]}-{s[2]}-bs{s[3]}-{s[4]}")
+def test_key_split_long_prefix(shape):
+    """One sequence's 512-token chunk over a 3584-token prefix: too few
+    units for the CUs, so each unit's keys are cut into parts and merged by
+    the last part to finish."""
+    hq, hkv, d, bs, dt = shape
+    say("prefill key split", shape)
+    c = _case(hq, hkv, d, bs, dt, [3584], [512], seed=7)
+    assert _max_parts(c) > 1
+    out = _run(c)
+    assert not torch.isnan(out).any()
+    err = (out - _ref(c)).abs().max().item()
+    assert err <= TOL[dt], err
+
+
+def test_key_split_mixed_units():
+    """Cut and whole units in one launch: a long prefix, and a chunk-only
+    sequence whose parts read their keys from the key / value rows."""
+    say("prefill key split, mixed")
+    # n_rep 1: 128 tokens per work group, 8 kv heads: 112 units, 2 parts at most
+    c = _case(8, 8, 64, 32, torch.float16, [2000, 0, 7], [100, 1500, 30], seed=8)
+    assert _max_parts(c) == 2
+    err = (_run(c) - _ref(c)).abs().max().item()
+    assert err <= TOL[torch.float16], err
+
+
+def test_key_split_is_deterministic_and_matches_whole_units(monkeypatch):
+    """The parts are folded in part order: repeated calls give the same
+    bits; and the result is that of the uncut launch within fp32 rounding."""
+    say("prefill key split, repeats")
+    c = _case(14, 2, 64, 16, torch.float32, [3000], [256], seed=9)
+    assert _max_parts(c) > 1
+    first = _run(c)
+    for _ in range(3):
+        assert torch.equal(_run(c), first)
+    monkeypatch.setenv("MVATTN_PREFILL_PARTS", "1")
+    whole = _run(c)  # a new table tensor: a new plan, uncut
+    assert (first - whole).abs().max().item() <= 1e-5
+    assert (whole - _ref(c)).abs().max().item() <= TOL[torch.float32]
