@@ -57,6 +57,10 @@ constexpr int kPfIdCap = 2048;  // prefix block ids staged in LDS per window
 constexpr int kPfMaxParts = 8;
 constexpr int kPfMaxUnits = 16384;
 constexpr int kPfCountersBytes = kPfMaxUnits * 4;
+// 16-bit types: a stage keeps p = exp2(s - m) with the row's reference m
+// unchanged when every row's stage sum lies in [kPfFastMin, kPfFastMax].
+constexpr float kPfFastMax = 4096.f;
+constexpr float kPfFastMin = 1.f / 4096.f;
 // Waves per work group: 8 (twice the query rows per pass over the keys,
 // and more waves to hide latency -- 39.8 us against 46.7 us with 4, two
 // such groups then sharing a CU, on a 4 x (1536 + 512) bf16 step) when two
@@ -145,6 +149,7 @@ struct PrefillArgs {
   int64_t o_st, o_sh;     // elements
   int64_t bt_stride;      // elements
   float scale_log2;
+  float inv_scale_log2;
   int32_t num_kv_heads, n_rep, tpw, bs_log2;
   uint32_t num_blocks_u32;
   int32_t lane_offsets_32;  // 16 chunk rows of K and of V span < 2 GiB: 32-bit lane offsets
@@ -219,7 +224,11 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     const char* qrow = reinterpret_cast<const char*>(static_cast<const raw_t*>(a.q) +
                                                      (qbase + tq) * a.q_st + head * a.q_sh);
 #pragma unroll
-    for (int c = 0; c < QP; ++c) qr[rt][c] = *reinterpret_cast<const uint4*>(qrow + (g * QP + c) * 16);
+    for (int c = 0; c < QP; ++c) {
+      qr[rt][c] = *reinterpret_cast<const uint4*>(qrow + (g * QP + c) * 16);
+      // a padding row's Q is zero: finite scores, never written
+      if (!ok) qr[rt][c] = uint4{0, 0, 0, 0};
+    }
   }
   // Q must have landed before the tile copies are counted by vmcnt.
 #pragma unroll
@@ -240,7 +249,8 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   f32x4 o[R][D / 16];
 #pragma unroll
   for (int rt = 0; rt < R; ++rt) {
-    m_run[rt] = kNegInf;
+    // 16-bit types: the row's reference (finite, see compute_stage)
+    m_run[rt] = DTYPE == MV_DTYPE_F32 ? kNegInf : 0.f;
     l_run[rt] = 0.f;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) o[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -360,12 +370,24 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
 
   // One stage for this wave's rows, over the U sub-tiles of 16 keys of its
   // set (all kPfWaves sub-tiles with one set): S^T for every sub-tile some
-  // row may see, one online-softmax update per row tile
-  // over the whole stage (one max / sum exchange and one rescale of O),
-  // then O += P V per sub-tile. The 16-bit types mask only the stages that
-  // cross the causal diagonal, fold the scale into the exponent's FMA
-  // (exp2(s * scale - m); the max is taken on unscaled scores, as scale > 0)
-  // and round P once, packed, for both the PV MFMA and the row sum.
+  // row may see, one online-softmax update per row tile over the whole
+  // stage, then O += P V per sub-tile.
+  //
+  // 16-bit types keep a per-row reference m (not necessarily the running
+  // maximum; s and m in the exponent's units, s = scale * log2(e) * q.k)
+  // with O and l relative to it. The QK^T MFMAs start from -m / (scale *
+  // log2(e)) instead of 0, so one multiply turns their result into s - m.
+  // A stage that no row's causal limit cuts ("whole") first tries
+  // p = exp2(s - m) as it comes: no row maximum and no rescale of O (Q
+  // itself is not scaled: rounding Q * scale * log2(e) to the data type
+  // measured 0.077 max abs error against 0.016 on sharp bf16 scores, at
+  // the same speed). It keeps that result when every
+  // row's stage sum lies in [2^-12, 2^12] (so every p <= 2^12, within the
+  // 16-bit types' range, and l stays well above underflow); otherwise, and
+  // in the stages that cross the causal diagonal, the stage is computed
+  // exactly: the row maximum d of s - m moves the reference by max(d, 0)
+  // (by d while the row has seen no key), P and O are rescaled by it, and
+  // P is rounded once, packed, for both the PV MFMA and the row sum.
   auto compute_stage = [&](int k, int st) __attribute__((always_inline)) {
     const int k_first = k * kPfStageTokens + set * U * kTile;  // the set's first key
     if (k_first > wave_limit) return;  // causal: no row of the wave sees these keys
@@ -375,17 +397,37 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     const char* stage = s_lds + st * Tr::kStageBytes + set * U * Tr::kSubBytes;
     const int ksw = piece_swizzle<RP>(t);
     f32x4 acc[U][R];
+    // S^T - m (16-bit types; fp32: S^T) of the sub-tiles u < nu (u >= nu:
+    // -m, never used unmasked). A whole stage has nu == U and branches on
+    // no sub-tile.
+    {
+      f32x4 c0[R];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int rt = 0; rt < R; ++rt) acc[u][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (u < nu) {
+      for (int rt = 0; rt < R; ++rt) {
+        const float c = DTYPE == MV_DTYPE_F32 ? 0.f : -m_run[rt] * a.inv_scale_log2;
+        c0[rt] = f32x4{c, c, c, c};
+      }
+      auto qk_tile = [&](int u) __attribute__((always_inline)) {
         const char* k_tile = stage + u * Tr::kSubBytes;
 #pragma unroll
         for (int c = 0; c < QP; ++c) {
           const uint4 kp = *reinterpret_cast<const uint4*>(k_tile + (t * RP + ((g * QP + c) ^ ksw)) * 16);
 #pragma unroll
-          for (int rt = 0; rt < R; ++rt) acc[u][rt] = mfma_qk<DTYPE>(kp, qr[rt][c], acc[u][rt]);
+          for (int rt = 0; rt < R; ++rt) acc[u][rt] = mfma_qk<DTYPE>(kp, qr[rt][c], c == 0 ? c0[rt] : acc[u][rt]);
+        }
+      };
+      if (whole) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) qk_tile(u);
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (u < nu) {
+            qk_tile(u);
+          } else {
+#pragma unroll
+            for (int rt = 0; rt < R; ++rt) acc[u][rt] = c0[rt];
+          }
         }
       }
     }
@@ -431,68 +473,17 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
       for (int u = 0; u < U; ++u)
         if (u < nu) mfma_pv_rows<DTYPE, D, R>(pr[u], stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, o);
     } else {
-      // Two instantiations, chosen once per stage (a uniform branch): the
-      // compiler would otherwise compute the mask and select per element.
-      auto softmax_pv = [&](auto whole_c) __attribute__((always_inline)) {
-        constexpr bool kWhole = decltype(whole_c)::value;
-        s16x4 pk[U][R];
-#pragma unroll
-        for (int rt = 0; rt < R; ++rt) {
-          float mc = kNegInf;
-          int lim = 0;
-          if constexpr (!kWhole) {
-            // the row's causal limit, recomputed in the few masked stages
-            // (opaque to hoisting: a live copy per row tile costs registers)
-            int r = rt * 16 + t;
-            asm volatile("" : "+v"(r));
-            const int rtok = wtok0 + r / a.n_rep;
-            lim = r < a.tpw * a.n_rep && rtok < ntok ? cached + tok0 + rtok : -1;
-          }
-#pragma unroll
-          for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              if constexpr (!kWhole) {
-                const int key = k_first + u * kTile + 4 * g + e;
-                acc[u][rt][e] = u < nu && key <= lim ? acc[u][rt][e] : kNegInf;
-              }
-              mc = fmaxf(mc, acc[u][rt][e]);
-            }
-          mc = fmaxf(mc, __shfl_xor(mc, 16));
-          mc = fmaxf(mc, __shfl_xor(mc, 32));
-          const float m_new = fmaxf(m_run[rt], mc * a.scale_log2);
-          const float m_ref = m_new == kNegInf ? 0.f : m_new;
-          const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_ref);
-          float lc = 0.f;
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            float pe[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              pe[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u][rt][e], a.scale_log2, -m_ref));
-            pk[u][rt] = pack_p<DTYPE>(pe[0], pe[1], pe[2], pe[3], lc);
-          }
-          lc += __shfl_xor(lc, 16);
-          lc += __shfl_xor(lc, 32);
-          l_run[rt] = l_run[rt] * alpha + lc;
-          m_run[rt] = m_new;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float ar = __shfl(alpha, 4 * g + e);
-#pragma unroll
-            for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
-          }
-        }
-        // O += P V, sub-tile by sub-tile. At head_dim 64 the next sub-tile's
-        // V operands are read while this one's MFMAs run (two operand sets
-        // in flight: 41.9 against 42.5 us); at 128 a second set would not
-        // fit the registers.
+      // O += P V, sub-tile by sub-tile (past nu, P is 0 and every V slot
+      // holds a pool row or zeros). At head_dim 64 the next sub-tile's V
+      // operands are read while this one's MFMAs run (two operand sets in
+      // flight: 41.9 against 42.5 us); at 128 a second set would not fit
+      // the registers.
+      auto pv = [&](s16x4 (&pk)[U][R], bool all) __attribute__((always_inline)) {
         if constexpr (D == 64 && MV_PREFILL_PV32) {
           // Two sub-tiles per 16x16x32 MFMA (half the MFMAs of 16x16x16).
-          // Past nu, P is 0 and every V slot holds a pool row or zeros.
 #pragma unroll
           for (int u = 0; u < U; u += 2) {
-            if (kWhole || u < nu) {
+            if (all || u < nu) {
               s16x4 va[D / 16], vb[D / 16];
               read_v_operands<DTYPE, D>(stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, va);
               read_v_operands<DTYPE, D>(stage + (u + 1) * Tr::kSubBytes + Tr::kTileBytes, g, t, vb);
@@ -504,8 +495,8 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
           read_v_operands<DTYPE, D>(stage + Tr::kTileBytes, g, t, vb[0]);
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            if (kWhole || u < nu) {
-              if (u + 1 < U && (kWhole || u + 1 < nu))
+            if (all || u < nu) {
+              if (u + 1 < U && (all || u + 1 < nu))
                 read_v_operands<DTYPE, D>(stage + (u + 1) * Tr::kSubBytes + Tr::kTileBytes, g, t,
                                           vb[(u + 1) & 1]);
               __builtin_amdgcn_sched_barrier(0);
@@ -515,12 +506,81 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         } else {
 #pragma unroll
           for (int u = 0; u < U; ++u)
-            if (kWhole || u < nu)
+            if (all || u < nu)
               mfma_pv_packed<DTYPE, D, R>(pk[u], stage + u * Tr::kSubBytes + Tr::kTileBytes, g, t, o);
         }
       };
-      if (whole) softmax_pv(IntC<1>{});
-      else softmax_pv(IntC<0>{});
+      // s - m in the exponent's units (+ b) from an MFMA result
+      auto sc = [&](float x, float b = 0.f) __attribute__((always_inline)) {
+        return __builtin_fmaf(x, a.scale_log2, b);
+      };
+      s16x4 pk[U][R];
+      if (whole) {
+        // p = exp2(s - m) as it comes; kept if every row's sum is in range
+        float lc[R];
+        bool out_of_range = false;
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt) {
+          lc[rt] = 0.f;
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            pk[u][rt] = pack_p<DTYPE>(__builtin_amdgcn_exp2f(sc(acc[u][rt][0])), __builtin_amdgcn_exp2f(sc(acc[u][rt][1])),
+                                      __builtin_amdgcn_exp2f(sc(acc[u][rt][2])), __builtin_amdgcn_exp2f(sc(acc[u][rt][3])),
+                                      lc[rt]);
+          lc[rt] += __shfl_xor(lc[rt], 16);
+          lc[rt] += __shfl_xor(lc[rt], 32);
+          // (a NaN sum fails both comparisons: it takes the exact path)
+          out_of_range |= !(lc[rt] <= kPfFastMax && l_run[rt] + lc[rt] >= kPfFastMin);
+        }
+        if (__builtin_amdgcn_ballot_w64(out_of_range) == 0) {
+#pragma unroll
+          for (int rt = 0; rt < R; ++rt) l_run[rt] += lc[rt];
+          pv(pk, true);
+          return;
+        }
+        // (acc still holds s - m: the exact path below starts from it)
+      }
+      // exact: masked (the causal limit per row, recomputed here rather
+      // than kept in registers), row maximum, reference moved, O rescaled
+#pragma unroll
+      for (int rt = 0; rt < R; ++rt) {
+        int r = rt * 16 + t;
+        asm volatile("" : "+v"(r));  // opaque to hoisting: a live copy per row tile costs registers
+        const int rtok = wtok0 + r / a.n_rep;
+        const int lim = r < a.tpw * a.n_rep && rtok < ntok ? cached + tok0 + rtok : -1;
+        float mc = kNegInf;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = k_first + u * kTile + 4 * g + e;
+            acc[u][rt][e] = u < nu && key <= lim ? acc[u][rt][e] : kNegInf;
+            mc = fmaxf(mc, acc[u][rt][e]);
+          }
+        mc = fmaxf(mc, __shfl_xor(mc, 16));
+        mc = sc(fmaxf(mc, __shfl_xor(mc, 32)));
+        const bool seen = l_run[rt] > 0.f;
+        const float shift = mc == kNegInf ? 0.f : seen ? fmaxf(mc, 0.f) : mc;
+        const float alpha = seen ? __builtin_amdgcn_exp2f(-shift) : 0.f;  // O, l are 0 when unseen
+        float lc = 0.f;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          pk[u][rt] = pack_p<DTYPE>(__builtin_amdgcn_exp2f(sc(acc[u][rt][0], -shift)),
+                                    __builtin_amdgcn_exp2f(sc(acc[u][rt][1], -shift)),
+                                    __builtin_amdgcn_exp2f(sc(acc[u][rt][2], -shift)),
+                                    __builtin_amdgcn_exp2f(sc(acc[u][rt][3], -shift)), lc);
+        lc += __shfl_xor(lc, 16);
+        lc += __shfl_xor(lc, 32);
+        l_run[rt] = l_run[rt] * alpha + lc;
+        m_run[rt] += shift;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float ar = __shfl(alpha, 4 * g + e);
+#pragma unroll
+          for (int c = 0; c < D / 16; ++c) o[rt][c][e] *= ar;
+        }
+      }
+      pv(pk, false);
     }
   };
 
@@ -568,6 +628,13 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     }
     __syncthreads();  // every wave is done with this window's stages and ids
     first = win0 + win_tokens;
+  }
+
+  if constexpr (DTYPE != MV_DTYPE_F32) {
+    // a row that saw no key has no reference: the merges give it no weight
+#pragma unroll
+    for (int rt = 0; rt < R; ++rt)
+      if (!(l_run[rt] > 0.f)) m_run[rt] = kNegInf;
   }
 
   // Lane coordinates recomputed for the epilogue rather than kept live
@@ -960,6 +1027,7 @@ int paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head
   a.o_sh = out_stride_head;
   a.bt_stride = bt_stride;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.inv_scale_log2 = 1.f / a.scale_log2;
   a.num_kv_heads = num_kv_heads;
   a.n_rep = num_q_heads / num_kv_heads;
   a.tpw = 0;  // set per instantiation at launch

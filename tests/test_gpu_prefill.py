@@ -225,3 +225,73 @@ def test_key_split_is_deterministic_and_matches_whole_units(monkeypatch):
     whole = _run(c)  # a new table tensor: a new plan, uncut
     assert (first - whole).abs().max().item() <= 1e-5
     assert (whole - _ref(c)).abs().max().item() <= TOL[torch.float32]
+
+
+# ---- the softmax reference: stages kept as computed, or redone exactly
+
+def _scaled(c, q_mul=1.0, k_mul=1.0, k_keys=None):
+    """The case with Q (and K: all keys, or prefix positions k_keys of every
+    sequence) multiplied, rounded again to the case's type."""
+    dt = c["dtype"]
+    out = dict(c)
+    out["q"] = (c["q"] * q_mul).to(dt).float()
+    k, kc = c["k"], c["kc"].clone()
+    if k_keys is None:
+        k = (k * k_mul).to(dt).float()
+        kc = (kc * k_mul).to(dt).float()
+    else:
+        bs = c["bs"]
+        for row, cached in zip(c["rows"], c["cached"]):
+            for p in k_keys:
+                if p < cached:
+                    b = int(c["bt"][row, p // bs])
+                    kc[b, :, p % bs] = (kc[b, :, p % bs] * k_mul).to(dt).float()
+    out["k"], out["kc"] = k, kc
+    return out
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=str)
+def test_sharp_scores(dt):
+    """Q x 4: scores of a few tens in the exponent's units, so stage sums
+    leave [2^-12, 2^12] and those stages are computed exactly (reference
+    moved, O rescaled)."""
+    say("prefill sharp scores", dt)
+    c = _scaled(_case(14, 2, 64, 16, dt, [1536, 300, 0], [512, 40, 100], seed=11), q_mul=4.0)
+    out = _run(c)
+    assert not torch.isnan(out).any()
+    err = (out - _ref(c)).abs().max().item()
+    say("max abs err", err)
+    assert err <= TOL[dt], err
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=str)
+def test_late_key_with_a_far_higher_score(dt):
+    """16 prefix keys (positions 1200-1215) with K x 12: their stage's sums
+    overflow the range, the reference moves up by tens of units, and the
+    stages after it are kept as computed again (sums far below 1, l above)."""
+    say("prefill late high key", dt)
+    c = _scaled(_case(14, 2, 64, 16, dt, [1536, 1300], [512, 64], seed=12), k_mul=12.0,
+                k_keys=range(1200, 1216))
+    out = _run(c)
+    assert not torch.isnan(out).any()
+    err = (out - _ref(c)).abs().max().item()
+    say("max abs err", err)
+    assert err <= TOL[dt], err
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=str)
+def test_scores_far_below_zero(dt):
+    """Every score near -60 in the exponent's units: the first stage's sums
+    fall below 2^-12 and are computed exactly, which moves the reference
+    down to the row maximum."""
+    say("prefill negative scores", dt)
+    c = _case(14, 2, 64, 16, dt, [700, 0], [300, 33], seed=13)
+    c["q"] = (c["q"].abs() * 2 + 1).to(dt).float()
+    c["k"] = (-(c["k"].abs() * 2 + 1)).to(dt).float()
+    kc = c["kc"]
+    c["kc"] = torch.where(torch.isnan(kc), kc, -(kc.abs() * 2 + 1)).to(dt).float()
+    out = _run(c)
+    assert not torch.isnan(out).any()
+    err = (out - _ref(c)).abs().max().item()
+    say("max abs err", err)
+    assert err <= TOL[dt], err
