@@ -388,9 +388,14 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
   // exactly: the row maximum d of s - m moves the reference by max(d, 0)
   // (by d while the row has seen no key), P and O are rescaled by it, and
   // P is rounded once, packed, for both the PV MFMA and the row sum.
-  auto compute_stage = [&](int k, int st) __attribute__((always_inline)) {
+  // (after_qk(): run once the stage's Q K^T MFMAs are issued, or at once
+  // when the wave's rows see none of the stage's keys)
+  auto compute_stage = [&](int k, int st, auto&& after_qk) __attribute__((always_inline)) {
     const int k_first = k * kPfStageTokens + set * U * kTile;  // the set's first key
-    if (k_first > wave_limit) return;  // causal: no row of the wave sees these keys
+    if (k_first > wave_limit) {  // causal: no row of the wave sees these keys
+      after_qk();
+      return;
+    }
     // sub-tiles u < nu hold keys some row of the wave sees
     const int nu = min(U, (wave_limit - k_first) / kTile + 1);
     const bool whole = k_first + U * kTile - 1 <= wave_first_limit;  // then nu == U
@@ -431,6 +436,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
         }
       }
     }
+    after_qk();
     if constexpr (DTYPE == MV_DTYPE_F32) {
       float pr[U][R][4];
 #pragma unroll
@@ -606,6 +612,11 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     // Stage i: wait for this wave's copies of it, clear its invalid V slots,
     // one barrier (every wave's part landed; stage i-1 consumed by all),
     // then refill stage i-1's buffer with stage i+S-1 and compute stage i.
+    // With two sets, set 1 issues its copies after its Q K^T: the waves'
+    // copy instructions then reach the CU's memory pipe in two rounds
+    // instead of one, and set 1 starts its MFMAs at once (31.0 against
+    // 31.7 us on a 4 x (1536 + 512) bf16 step; set 1 copying before P V
+    // instead: 32.6 us).
     auto step = [&](int i, auto st_c) __attribute__((always_inline)) {
       constexpr int ST = decltype(st_c)::value;
       constexpr int NX = (ST + S - 1) % S;
@@ -613,9 +624,14 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
       asm volatile("" ::: "memory");
       zero_invalid_v(ST, valid[ST]);
       __syncthreads();
-      if (i + S - 1 < n) valid[NX] = issue(k0 + i + S - 1, IntC<NX>{});
+      const bool more = i + S - 1 < n;
+      const bool late = Tr::kSets > 1 && set == 1;
+      if (more && !late) valid[NX] = issue(k0 + i + S - 1, IntC<NX>{});
       asm volatile("" ::: "memory");
-      compute_stage(k0 + i, ST);
+      compute_stage(k0 + i, ST, [&] {
+        if (more && late) valid[NX] = issue(k0 + i + S - 1, IntC<NX>{});
+        asm volatile("" ::: "memory");
+      });
     };
     for (int i = 0; i < n; i += S) {
       step(i, IntC<0>{});
