@@ -146,7 +146,7 @@ struct DecodeArgs {
   float scale_log2;                     // scale * log2(e)
   int32_t num_q_heads, max_parts;
   uint32_t num_blocks_u32;  // pool blocks (at most 2^31): ids at or above are not read
-  uint32_t unused;
+  float inv_scale_log2;  // 1 / scale_log2
   int32_t* counters;  // [num_seqs * num_kv_heads], zero at rest
   void* out;
   int64_t out_stride_tok, out_stride_head;  // elements
@@ -197,6 +197,11 @@ __device__ __forceinline__ float unpack_hi(uint64_t v) { return __uint_as_float(
 #ifndef MV_DECODE_PARTIALS16
 #define MV_DECODE_PARTIALS16 1
 #endif
+
+// A tile keeps p = exp2(s - m) with the head's reference m unchanged when
+// every head's tile sum lies in [kLazyMin, kLazyMax].
+constexpr float kLazyMax = 4096.f;
+constexpr float kLazyMin = 1.f / 4096.f;
 
 // ----------------------------------------------------------- the kernel ---
 
@@ -392,8 +397,10 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   };
 
   uint4 qr[QP];  // Q^T operand: head t of the group, dims of quarter g (from LDS)
-  float m_run = kNegInf;  // running max of head t (log2 domain)
-  float l_run = 0.f;      // running sum of head t
+  // head t's reference m (log2 domain; not necessarily its running max)
+  // and running sum, with O and l relative to m
+  float m_run = 0.f;
+  float l_run = 0.f;
   f32x4 o[D / 16];        // O[head 4g+e][dim 16c+t]
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -402,7 +409,9 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   auto compute_tile = [&](int k, int st) __attribute__((always_inline)) {
     const char* k_tile = wave_tiles + st * Tr::kStageBytes;
     const char* v_tile = k_tile + Tr::kTileBytes;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // the MFMAs start from -m / (scale log2 e): acc * scale log2 e = s - m
+    const float c0 = -m_run * a.inv_scale_log2;
+    f32x4 acc = {c0, c0, c0, c0};
 #if defined(MV_DECODE_QK_VALU)
     if constexpr (!ROPE) {
       // Build-time alternative for measurement (MFMA against VALU): S^T by
@@ -437,35 +446,57 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       }
     }
     const int tile_tok = tok_begin + k * Tr::kChunk + wave * kTile;
-    float s[4];
-    float mc = kNegInf;
+    float s[4];  // s - m of the lane's 4 tokens (-inf past the piece)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      s[e] = tile_tok + 4 * g + e < tok_end ? acc[e] * a.scale_log2 : kNegInf;
-      mc = fmaxf(mc, s[e]);
-    }
-    mc = rows_max(mc);  // head t's max over the tile: lanes t, t+16, t+32, t+48
-    const float m_new = fmaxf(m_run, mc);
-    const float m_ref = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
-    // P = exp2(S - m), rounded to the MFMA input type; the sum uses the
+    for (int e = 0; e < 4; ++e) s[e] = tile_tok + 4 * g + e < tok_end ? acc[e] * a.scale_log2 : kNegInf;
+    // P = exp2(s - m), rounded to the MFMA input type; the sum uses the
     // rounded values so O / l is an exact convex combination of V rows.
+    // A tile whose 16 tokens all count first keeps p = exp2(s - m) with m
+    // unchanged when every head's tile sum lies in [2^-12, 2^12] (then no
+    // p exceeds 2^12 and l stays far from underflow): no maximum, no
+    // exchange of it and no rescale of O. Otherwise the tile is exact: the
+    // head's maximum d of s - m moves m by max(d, 0) (by d while the head
+    // has seen no token) and O, l are rescaled.
     float p[4];
     float lc = 0.f;
+    bool kept = false;
+    if (tile_tok + kTile <= tok_end) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      p[e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e] - m_ref)));
-      lc += p[e];
+      for (int e = 0; e < 4; ++e) {
+        p[e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e])));
+        lc += p[e];
+      }
+      lc = rows_sum(lc);
+      const bool out_of_range = !(lc <= kLazyMax && l_run + lc >= kLazyMin);  // NaN: out
+      if (__builtin_amdgcn_ballot_w64(out_of_range) == 0) {
+        l_run += lc;
+        kept = true;
+      }
     }
-    lc = rows_sum(lc);
-    l_run = l_run * alpha + lc;
-    m_run = m_new;
-    // rescale O rows (head 4g+e takes the alpha of lane 4g+e)
+    if (!kept) {
+      float mc = kNegInf;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float ar = __shfl(alpha, 4 * g + e);
+      for (int e = 0; e < 4; ++e) mc = fmaxf(mc, s[e]);
+      mc = rows_max(mc);  // head t's max over the tile: lanes t, t+16, t+32, t+48
+      const bool seen = l_run > 0.f;
+      const float shift = mc == kNegInf ? 0.f : seen ? fmaxf(mc, 0.f) : mc;
+      const float alpha = seen ? __builtin_amdgcn_exp2f(-shift) : 0.f;  // O, l are 0 when unseen
+      lc = 0.f;
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) o[c][e] *= ar;
+      for (int e = 0; e < 4; ++e) {
+        p[e] = to_f32<DTYPE>(from_f32<DTYPE>(__builtin_amdgcn_exp2f(s[e] - shift)));
+        lc += p[e];
+      }
+      lc = rows_sum(lc);
+      l_run = l_run * alpha + lc;
+      m_run += shift;
+      // rescale O rows (head 4g+e takes the alpha of lane 4g+e)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float ar = __shfl(alpha, 4 * g + e);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) o[c][e] *= ar;
+      }
     }
     mfma_pv<DTYPE, D>(p, v_tile, g, t, o);
   };
@@ -598,7 +629,8 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   {
     float* my_o = wave_o(wave);
     if (g == 0) {
-      wave_ms(wave)[t] = m_run;
+      // a head that saw no token has no reference: weight 0 in the merge
+      wave_ms(wave)[t] = l_run > 0.f ? m_run : kNegInf;
       wave_ms(wave)[kMaxGroup + t] = l_run;
     }
     // all 16 accumulator rows (= query heads of the group; rows >= n_rep
@@ -637,7 +669,9 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
         v[j].y += x.y * f;
       }
     }
-    const float inv = 1.f / sum;  // >= 1: the partition's largest logit contributes exp2(0)
+    // > 0: the wave whose reference is mx has l > 2^-12 (every kept tile
+    // leaves l at least that, an exact one at least 1)
+    const float inv = 1.f / sum;
     if (n_parts == 1) {
       raw_t* op = out_row(r) + 2 * q;
 #pragma unroll
@@ -1568,13 +1602,13 @@ int decode_launch(const void* query, int64_t q_stride_tok, int64_t q_stride_head
   a.out_stride_tok = out_stride_tok;
   a.out_stride_head = out_stride_head;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.inv_scale_log2 = 1.f / a.scale_log2;
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
   a.n_rep = n_rep;
   a.bs_log2 = bs_log2;
   a.max_parts = max_partitions;
   a.num_blocks_u32 = static_cast<uint32_t>(std::min<int64_t>(num_blocks, int64_t(1) << 31));
-  a.unused = 0;
   a.ws_o = nullptr;
   a.ws_ml = nullptr;
   if (max_partitions > 1) {

@@ -439,3 +439,57 @@ def test_backend_prefill_matches_oracle_prefill():
     out = be.prefill_attention(0, q.to(DEV), k.to(DEV), v.to(DEV), meta, pool)
     ref = paged_ref.prefill_attention(q, kc, vc, torch.tensor(rows), [0, 1, 2], cached, qlens, 4)
     assert (out.cpu() - ref).abs().max().item() < 1e-5
+
+
+# ---- the softmax reference: tiles kept as computed, or redone exactly
+
+SHARP_LENS = [1, 17, 300, 1000, 2048]
+
+
+def _sharp_case(dtype, seed):
+    return _random_case(14, 2, 64, 16, SHARP_LENS, dtype, seed=seed)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=str)
+def test_sharp_scores(dtype):
+    """Q x 4: tile sums leave [2^-12, 2^12], so those tiles are computed
+    exactly (reference moved, O rescaled)."""
+    say("decode sharp scores", dtype)
+    c = _sharp_case(dtype, seed=21)
+    c.query = (c.query.float() * 4).to(c.query.dtype)
+    ref, _, _ = oracle_step(c)
+    out, _ = _step_on_gpu(c)
+    say("  max abs err", _check(out, ref, dtype, f"sharp {dtype}"))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_late_key_with_a_far_higher_score(dtype):
+    """Keys of each sequence's sixth block (tokens 80-95) x 12: their tile
+    overflows the range, the reference moves up by tens of units, and later
+    tiles are kept as computed again (sums far below 1, l above)."""
+    say("decode late high key", dtype)
+    c = _sharp_case(dtype, seed=22)
+    kc = c.key_cache.float()
+    for b, n in enumerate(c.kv_len.tolist()):
+        if n > 96:
+            blk = int(c.block_table[b, 5])
+            kc[blk] = kc[blk] * 12
+    c.key_cache = kc.to(c.key_cache.dtype)
+    ref, _, _ = oracle_step(c)
+    out, _ = _step_on_gpu(c)
+    say("  max abs err", _check(out, ref, dtype, f"late key {dtype}"))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_scores_far_below_zero(dtype):
+    """Every score near -60 in the exponent's units: the first tile's sums
+    fall below 2^-12 and are computed exactly, which moves the reference
+    down to the head's maximum."""
+    say("decode negative scores", dtype)
+    c = _sharp_case(dtype, seed=23)
+    c.query = (c.query.float().abs() * 2 + 1).to(c.query.dtype)
+    c.key_cache = (-(c.key_cache.float().abs() * 2 + 1)).to(c.key_cache.dtype)
+    c.new_key = (-(c.new_key.float().abs() * 2 + 1)).to(c.new_key.dtype)
+    ref, _, _ = oracle_step(c)
+    out, _ = _step_on_gpu(c)
+    say("  max abs err", _check(out, ref, dtype, f"negative {dtype}"))
