@@ -451,11 +451,12 @@ def _sharp_case(dtype, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=str)
-def test_sharp_scores(dtype):
+@pytest.mark.parametrize("d", [64, 128])
+def test_sharp_scores(dtype, d):
     """Q x 4: tile sums leave [2^-12, 2^12], so those tiles are computed
     exactly (reference moved, O rescaled)."""
-    say("decode sharp scores", dtype)
-    c = _sharp_case(dtype, seed=21)
+    say("decode sharp scores", dtype, d)
+    c = _random_case(14, 2, d, 16, SHARP_LENS, dtype, seed=21)
     c.query = (c.query.float() * 4).to(c.query.dtype)
     ref, _, _ = oracle_step(c)
     out, _ = _step_on_gpu(c)

@@ -89,6 +89,7 @@ SHAPES = [  # (hq, hkv, d, bs, dtype)
     (16, 1, 64, 64, torch.bfloat16),   # n_rep 16, block 64
     (10, 2, 64, 16, torch.bfloat16),   # n_rep 5: 6 tokens per row wave, 2 padding rows
     (12, 2, 64, 16, torch.float16),    # n_rep 6: 5 tokens per row wave (20 per work group)
+    (8, 2, 128, 16, torch.float16),    # head_dim 128 in fp16
 ]
 
 
@@ -251,12 +252,13 @@ def _scaled(c, q_mul=1.0, k_mul=1.0, k_keys=None):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=str)
-def test_sharp_scores(dt):
+@pytest.mark.parametrize("d", [64, 128])
+def test_sharp_scores(dt, d):
     """Q x 4: scores of a few tens in the exponent's units, so stage sums
     leave [2^-12, 2^12] and those stages are computed exactly (reference
-    moved, O rescaled)."""
-    say("prefill sharp scores", dt)
-    c = _scaled(_case(14, 2, 64, 16, dt, [1536, 300, 0], [512, 40, 100], seed=11), q_mul=4.0)
+    moved, O rescaled); head_dim 64 (two wave sets) and 128 (one)."""
+    say("prefill sharp scores", dt, d)
+    c = _scaled(_case(14, 2, d, 16, dt, [1536, 300, 0], [512, 40, 100], seed=11), q_mul=4.0)
     out = _run(c)
     assert not torch.isnan(out).any()
     err = (out - _ref(c)).abs().max().item()
