@@ -262,6 +262,43 @@ def plan_step_us(bt, kv, bs, num_blocks, dev, spec, plan_decode, reps=20):
     return statistics.median(times)
 
 
+def checks_measure(dev, stream, bt, kv, slots, num_blocks, bs, steps):
+    """GPU time (events) of the per-step metadata checks, called through the
+    C ABI so that no per-step cache skips them: the slot check at the
+    step's token count and at a 32k-token prefill step (the grid path over
+    a workspace hash table), and the fused-write check (both launches)."""
+    import ctypes
+
+    from mini_vllm.attention import _hip
+
+    lib = _hip.load()
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    s = ctypes.c_void_p(stream.cuda_stream)
+    status = torch.empty(2, dtype=torch.int32, device=dev)
+    out = {}
+    big = torch.randperm(max(2 * 32768, num_blocks * bs), device=dev)[:32768].to(torch.int64)
+    for name, sl in (("slots_check_us", slots), ("slots_check_32k_us", big)):
+        n = sl.numel()
+        nbytes = lib.mv_kv_slots_check_workspace_bytes(n)
+        ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)
+        total = max(num_blocks * bs, 2 * 32768)
+        call = lambda i: lib.mv_kv_slots_check(ptr(sl), n, total, ptr(status), ptr(ws),  # noqa: E731
+                                               nbytes, s)
+        for i in range(5):
+            call(i)
+        out[name] = round(time_loop(call, steps, stream), 3)
+    n = kv.shape[0]
+    nbytes = lib.mv_decode_write_check_workspace_bytes(n)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    call = lambda i: lib.mv_decode_write_check(  # noqa: E731
+        ptr(slots), ptr(bt), 1, bt.stride(0), ptr(kv), 1, n, bt.shape[1], bs, ptr(status),
+        ptr(ws), nbytes, s)
+    for i in range(5):
+        call(i)
+    out["fused_write_check_us"] = round(time_loop(call, steps, stream), 3)
+    return out
+
+
 def measure_workload(name, steps, warmup, dev, stream, seed):
     """The fused layer call (KV write + decode, one launch) and decode alone
     on another configuration, timed as the headline: >= 1 GiB of per-layer
@@ -545,6 +582,8 @@ def main(argv=None) -> int:
     plan = plan_decode(bt, kv, bs, layout.num_blocks, dev, spec.head_dim, spec.dtype,
                        spec.num_kv_heads)
     plan_us = plan_step_us(bt, kv, bs, layout.num_blocks, dev, spec, plan_decode)
+    checks = checks_measure(dev, stream, bt, kv, slots, layout.num_blocks, bs, 50)
+    log(f"[bench] checks (GPU us): {checks}")
 
     def layer_call(i):  # one launch: the step's KV write fused into the decode
         L = rot.take()
@@ -710,6 +749,7 @@ def main(argv=None) -> int:
         "two_call_host_inclusive_us": round(us_two_wall, 3),
         "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "plan_us_per_step": round(plan_us, 1),
+        "checks": checks,
         "sublayer": {
             "what": "decode attention sub-layer (qwen_runner.py:164-190, decode rows): RoPE of q "
                     "and new k + KV write + decode",

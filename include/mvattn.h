@@ -24,8 +24,12 @@
  *   - Return value: MV_OK (0) or a negative MV_ERR_* code; the message of
  *     the last error on the calling thread is returned by mv_last_error().
  *     No entry point aborts the process.
- *   - The library allocates no device memory and keeps no state other
- *     than the thread-local error string.
+ *   - No entry point allocates device memory: buffers beyond the inputs
+ *     and outputs (workspaces, status words) are the caller's. The library
+ *     keeps the thread-local error string, a per-device cache of one
+ *     device address (looked up once, never changed), and one static
+ *     device array of MV_DECODE_SCRATCH_BYTES per GPU that only
+ *     mv_paged_decode_noalloc uses (see there).
  */
 #ifndef MVATTN_H
 #define MVATTN_H
@@ -37,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MVATTN_ABI_VERSION 5
+#define MVATTN_ABI_VERSION 6
 
 /* Element types of query / key / value / cache / output. */
 #define MV_DTYPE_F32 0
@@ -53,6 +57,11 @@ extern "C" {
 /* Status words written by mv_kv_slots_check (int32[2], device memory). */
 #define MV_SLOTS_OUT_OF_RANGE 0 /* # slots < -1 or >= num_blocks*block_size */
 #define MV_SLOTS_DUPLICATES 1   /* # (i < j) pairs with slot[i] == slot[j] >= 0 */
+
+/* Status words written by mv_decode_write_check (int32[2], device memory). */
+#define MV_WRITE_CHECK_OWN_SLOT 0 /* # slots not at their own sequence's kv_len - 1 */
+#define MV_WRITE_CHECK_SHARED 1   /* # table entries of the batch reading a slot written */
+#define MV_WRITE_CHECK_MAX_SEQS 4096
 
 /* Status words written by mv_decode_plan (int32[8], device memory). */
 #define MV_PLAN_NUM_ITEMS 0     /* number of work groups (launch grid) */
@@ -113,31 +122,53 @@ int mv_kv_cache_write(const void* key, int64_t key_stride_tok, int64_t key_strid
 /*
  * Slot validation for mv_kv_cache_write.
  * Replaces the host-side duplicate check of `triton_cache_write`
- * (paged_attention_gpu.py:126-135, `slot_mapping.unique()`) and the range
- * check of `write_to_paged_cache` (cache_write.py:61-66). Writes
- * status[MV_SLOTS_OUT_OF_RANGE] and status[MV_SLOTS_DUPLICATES] (int32[2],
- * device) without sorting. The caller reads the two words back.
+ * (paged_attention_gpu.py:126-135, `slot_mapping.unique()`, O(T log T)
+ * with a host sync) and the range check of `write_to_paged_cache`
+ * (cache_write.py:61-66). Writes status[MV_SLOTS_OUT_OF_RANGE] and
+ * status[MV_SLOTS_DUPLICATES] (int32[2], device; the pair count saturates
+ * at INT32_MAX) in O(T) expected work: every slot is counted into a hash
+ * table. Up to 4096 tokens one work group does it in LDS and `workspace`
+ * may be null; above, `workspace` (device, 8-byte aligned) must hold
+ * mv_kv_slots_check_workspace_bytes(num_tokens) bytes, which the call
+ * clears itself (two launches). num_tokens < 2^20 and total_slots < 2^44,
+ * else MV_ERR_UNSUPPORTED. The caller reads the two words back.
  */
+size_t mv_kv_slots_check_workspace_bytes(int64_t num_tokens);
 int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens, int64_t total_slots,
-                      int32_t* status, void* stream);
+                      int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Precondition check of mv_paged_decode_write (the fused decode + KV write;
- * no counterpart in the reference, whose runner makes the two calls):
- * status[0] (int32, device) = number of sequences b whose slot_mapping[b]
- * is neither -1 nor the table position of b's token kv_len[b] - 1, i.e.
- * block_table[b, (kv_len[b]-1) / block_size] * block_size +
- * (kv_len[b]-1) % block_size (a sequence whose kv_len or table entry
- * cannot address that position counts too). When it is 0 -- and no other
- * sequence of the batch attends those slots, which the block manager
- * guarantees (a sequence's last block is its own) -- the fused call is
- * bit-identical to mv_kv_cache_write followed by mv_paged_decode. The
- * block table and kv_len may each be int32 or int64.
+ * no counterpart in the reference, whose runner makes the two calls
+ * write_kv_cache then decode_attention, qwen_runner.py:168-190). Writes two
+ * int32 status words (device):
+ *   status[MV_WRITE_CHECK_OWN_SLOT] = number of sequences b whose
+ *     slot_mapping[b] is neither -1 nor the table position of b's token
+ *     kv_len[b] - 1, i.e. block_table[b, (kv_len[b]-1) / block_size] *
+ *     block_size + (kv_len[b]-1) % block_size (a sequence whose kv_len or
+ *     table entry cannot address that position counts too);
+ *   status[MV_WRITE_CHECK_SHARED] = number of table entries (c, j) that a
+ *     sequence c attends (j < ceil(kv_len[c] / block_size)) and that name a
+ *     block holding a slot written by this call at an offset c reads
+ *     through that entry (below kv_len[c] - j * block_size), other than c's
+ *     own slot at its own position kv_len[c] - 1. Counted only among the
+ *     writers that pass the first check. Such a batch arises when blocks
+ *     are shared without copy-on-write (the reference's prefix cache shares
+ *     a prompt's partial last block: mini_vllm/cache/manager.py:140-172).
+ * When both are 0 the fused call is bit-identical to mv_kv_cache_write
+ * followed by mv_paged_decode; otherwise a work group could read a pool row
+ * another one rewrites. The block table and kv_len may each be int32 or
+ * int64. `workspace` (device, 8-byte aligned) holds
+ * mv_decode_write_check_workspace_bytes(num_seqs) bytes (a hash table of
+ * the writers, rebuilt by every call). num_seqs <= MV_WRITE_CHECK_MAX_SEQS
+ * and block_size <= 2^20, else MV_ERR_UNSUPPORTED (make the two calls).
+ * Two launches: one work group, then a (sequence, 256 table entries) grid.
  */
+size_t mv_decode_write_check_workspace_bytes(int32_t num_seqs);
 int mv_decode_write_check(const int64_t* slot_mapping, const void* block_table, int32_t bt_is_i64,
                           int64_t bt_stride, const void* kv_len, int32_t kv_len_is_i64,
                           int32_t num_seqs, int32_t max_blocks, int32_t block_size,
-                          int32_t* status, void* stream);
+                          int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Per-step decode metadata: validation, work split, work list.
@@ -349,10 +380,10 @@ int mv_positions_check(const int64_t* positions, int64_t num_tokens, int64_t max
  * the new rows when its slot is that token's table position, which is
  * what the block manager produces; otherwise it is read from the pool.
  * Precondition (the block manager's layout): every slot is -1 or its
- * sequence's position kv_len - 1 (mv_decode_write_check counts the
- * others), and no other sequence of the batch attends it. The output and
- * the pool are then bit-identical to mv_kv_cache_write followed by
- * mv_paged_decode.
+ * sequence's position kv_len - 1, and no other table entry of the batch
+ * reads it (mv_decode_write_check counts both; the caller makes the two
+ * calls when either count is nonzero). The output and the pool are then
+ * bit-identical to mv_kv_cache_write followed by mv_paged_decode.
  *
  * With rope_cos_rows / rope_sin_rows ([num_seqs][head_dim] rows of the
  * rotary cos / sin tables at each sequence's position, query dtype,

@@ -105,7 +105,7 @@ def build_launcher(verbose: bool = False) -> str:
     fd, tmp = tempfile.mkstemp(prefix="_mvlaunch.", suffix=".so.tmp", dir=LAUNCHER_DIR)
     os.close(fd)
     cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Wextra", "-Werror",
-           "-I", sysconfig.get_paths()["include"], LAUNCHER_SOURCE, "-o", tmp]
+           "-I", sysconfig.get_paths()["include"], "-I", INCLUDE, LAUNCHER_SOURCE, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -85,77 +85,274 @@ __global__ __launch_bounds__(256) void kv_cache_write_kernel(WriteArgs a) {
   }
 }
 
-// One work group compares a 256-slot tile `i` against tile `j >= i`.
-// status[0] counts slots outside [-1, total_slots), status[1] counts pairs
-// (x < y) of equal in-range slots. Counters start at zero (zero_status).
-constexpr int kCheckTile = 256;
+// ---------------------------------------------------------------------------
+// Slot check: out-of-range slots and duplicate pairs in O(T) expected work.
+//
+// Every in-range slot is inserted into an open-addressing hash table of
+// 64-bit words (count << 44) | (slot + 1), 0 marking an empty entry. An
+// insert that finds its slot already present adds one to the count and
+// learns how many equal slots were inserted before it; summed over all
+// inserts that is sum_v k_v (k_v - 1) / 2 = the number of pairs (x < y)
+// with slots[x] == slots[y], whatever the insertion order. The table has at
+// least twice as many entries as slots, so every probe sequence ends.
+// Up to kSlotsLdsMax slots one work group does it in LDS; beyond, a grid
+// does it in a workspace table cleared by a fill kernel first.
+constexpr int kSlotCountShift = 44;
+constexpr uint64_t kSlotKeyMask = (uint64_t(1) << kSlotCountShift) - 1;
+constexpr int kSlotsLdsMax = 4096;
+constexpr int kSlotsLdsEntries = 2 * kSlotsLdsMax;  // 64 KiB of LDS
+constexpr int kSlotsCheckThreads = 1024;
+constexpr int kSlotsGridThreads = 256;
+constexpr int64_t kSlotsMax = (int64_t(1) << (64 - kSlotCountShift)) - 1;  // count field
 
-__global__ __launch_bounds__(kCheckTile) void slots_check_kernel(const int64_t* slots, int64_t n,
-                                                                 int64_t total_slots,
-                                                                 int32_t* status) {
-  const int64_t ti = blockIdx.x, tj = blockIdx.y;
-  if (tj < ti) return;
-  __shared__ int64_t s_other[kCheckTile];
-  __shared__ int s_dups, s_bad;
-  if (threadIdx.x == 0) { s_dups = 0; s_bad = 0; }
-  const int64_t y0 = tj * kCheckTile;
-  const int64_t yi = y0 + threadIdx.x;
-  s_other[threadIdx.x] = yi < n ? slots[yi] : -1;
-  __syncthreads();
-  const int64_t x = ti * kCheckTile + threadIdx.x;
-  int dups = 0;
-  if (x < n) {
-    const int64_t s = slots[x];
-    const bool in_range = s >= 0 && s < total_slots;
-    if (ti == tj && !in_range && s != -1) atomicAdd(&s_bad, 1);
-    if (in_range) {
-      const int64_t lim = min<int64_t>(kCheckTile, n - y0);
-      for (int k = 0; k < lim; ++k) {
-        dups += (y0 + k > x) && (s_other[k] == s);
-      }
+__device__ __forceinline__ uint32_t hash64(uint64_t k) {
+  return static_cast<uint32_t>((k * 0x9E3779B97F4A7C15ull) >> 29);
+}
+
+// Inserts `key` (slot + 1); returns the number of equal keys inserted
+// before it. `table` is LDS or global memory; the atomics are the
+// address space's own.
+template <typename Word>
+__device__ __forceinline__ uint64_t count_insert(Word* table, uint32_t hmask, uint64_t key) {
+  uint32_t h = hash64(key) & hmask;
+  const unsigned long long first = (1ull << kSlotCountShift) | key;
+  while (true) {
+    const unsigned long long old = atomicCAS(reinterpret_cast<unsigned long long*>(&table[h]), 0ull, first);
+    if (old == 0) return 0;
+    if ((old & kSlotKeyMask) == key) {
+      const unsigned long long prev =
+          atomicAdd(reinterpret_cast<unsigned long long*>(&table[h]), 1ull << kSlotCountShift);
+      return prev >> kSlotCountShift;
     }
-  }
-  if (dups) atomicAdd(&s_dups, dups);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    if (s_bad) atomicAdd(&status[MV_SLOTS_OUT_OF_RANGE], s_bad);
-    if (s_dups) atomicAdd(&status[MV_SLOTS_DUPLICATES], s_dups);
+    h = (h + 1) & hmask;
   }
 }
 
-// The fused decode + KV write (mv_paged_decode_write) is exact when every
-// slot is -1 or the table position of its own sequence's last attended
-// token kv_len - 1 (the block manager's layout). One work group counts the
-// sequences for which that does not hold (including those with a kv_len or
-// table entry that cannot address such a position) into status[0].
-constexpr int kWriteCheckThreads = 256;
+__device__ __forceinline__ int32_t saturate_i32(uint64_t v) {
+  return v > static_cast<uint64_t>(INT_MAX) ? INT_MAX : static_cast<int32_t>(v);
+}
+
+__global__ __launch_bounds__(kSlotsCheckThreads) void slots_check_lds_kernel(
+    const int64_t* slots, int32_t n, int64_t total_slots, uint32_t hmask, int32_t* status) {
+  __shared__ uint64_t table[kSlotsLdsEntries];
+  __shared__ int s_bad;
+  __shared__ unsigned long long s_pairs;
+  for (uint32_t i = threadIdx.x; i <= hmask; i += kSlotsCheckThreads) table[i] = 0;
+  if (threadIdx.x == 0) { s_bad = 0; s_pairs = 0; }
+  __syncthreads();
+  int bad = 0;
+  uint64_t pairs = 0;
+  for (int x = threadIdx.x; x < n; x += kSlotsCheckThreads) {
+    const int64_t s = slots[x];
+    if (s == -1) continue;
+    if (s < 0 || s >= total_slots) { ++bad; continue; }
+    pairs += count_insert(table, hmask, static_cast<uint64_t>(s) + 1);
+  }
+  if (bad) atomicAdd(&s_bad, bad);
+  if (pairs) atomicAdd(&s_pairs, static_cast<unsigned long long>(pairs));
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    status[MV_SLOTS_OUT_OF_RANGE] = s_bad;
+    status[MV_SLOTS_DUPLICATES] = saturate_i32(s_pairs);
+  }
+}
+
+__global__ __launch_bounds__(kSlotsGridThreads) void slots_clear_kernel(uint64_t* table,
+                                                                        int64_t entries,
+                                                                        int32_t* status) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSlotsGridThreads;
+  for (int64_t i = blockIdx.x * int64_t(kSlotsGridThreads) + threadIdx.x; i < entries; i += stride)
+    table[i] = 0;
+  if (blockIdx.x == 0 && threadIdx.x < 2) status[threadIdx.x] = 0;
+}
+
+__global__ __launch_bounds__(kSlotsGridThreads) void slots_check_grid_kernel(
+    const int64_t* slots, int64_t n, int64_t total_slots, uint64_t* table, uint32_t hmask,
+    int32_t* status) {
+  __shared__ int s_bad;
+  __shared__ unsigned long long s_pairs;
+  if (threadIdx.x == 0) { s_bad = 0; s_pairs = 0; }
+  __syncthreads();
+  const int64_t x = blockIdx.x * int64_t(kSlotsGridThreads) + threadIdx.x;
+  if (x < n) {
+    const int64_t s = slots[x];
+    if (s != -1) {
+      if (s < 0 || s >= total_slots) {
+        atomicAdd(&s_bad, 1);
+      } else {
+        const uint64_t prev = count_insert(table, hmask, static_cast<uint64_t>(s) + 1);
+        if (prev) atomicAdd(&s_pairs, static_cast<unsigned long long>(prev));
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (s_bad) atomicAdd(&status[MV_SLOTS_OUT_OF_RANGE], s_bad);
+    if (s_pairs) {  // saturating add
+      int32_t* p = &status[MV_SLOTS_DUPLICATES];
+      int32_t old = *p;
+      while (true) {
+        const int32_t want = saturate_i32(static_cast<uint64_t>(old) + s_pairs);
+        const int32_t seen = atomicCAS(p, old, want);
+        if (seen == old) break;
+        old = seen;
+      }
+    }
+  }
+}
+
+inline uint32_t pow2_at_least(int64_t v) {
+  uint32_t h = 1;
+  while (h < v) h <<= 1;
+  return h;
+}
+
+// ---------------------------------------------------------------------------
+// Fused decode + KV write precondition (mv_paged_decode_write).
+//
+// Phase 1 (one work group): counts the sequences whose slot is neither -1
+// nor the table position of their own token kv_len - 1 (status[0]), and
+// puts every other writer b -- slot s_b in block k_b at offset o_b -- into
+// a hash table keyed by k_b + 1 whose value is the minimum of
+// (o_b << 12) | b over the writers of that block, as 64-bit words
+// ((k_b + 1) << 32) | value (0: empty). Built in LDS, then stored to the
+// workspace.
+// Phase 2 (a grid of (sequence c, 256 table entries)): an entry j that c
+// attends (j < ceil(kv_c / bs)) whose block is in the table is counted
+// (status[1]) when the block's smallest written offset lies below c's
+// limit in that block, min(bs, kv_c - j bs), unless that writer is c itself
+// at its own last position. That is exact: a write at offset o is read
+// through entry (c, j) iff o < the limit, and if the smallest-offset writer
+// is c's own last position, every other writer of the block is either not
+// attended by c or writes c's very slot (a duplicate slot). Phase 2 does
+// not count c's own entry in that last case; phase 1 does, once per block
+// whose smallest written offset has two or more writers, so that status[1]
+// is exactly the number of attended entries (c, j) through which c reads a
+// slot that some writer other than c-at-its-last-entry writes.
+constexpr int kWriteCheckThreads = 1024;
+constexpr int kWriteCheckEntries = 2 * MV_WRITE_CHECK_MAX_SEQS;  // 64 KiB of LDS
+constexpr int kWriterSeqBits = 12;  // MV_WRITE_CHECK_MAX_SEQS = 1 << 12
+constexpr int kWriterMaxBlockLog2 = 20;  // offsets < 2^20 fit the value's upper bits
+static_assert(kWriterMaxBlockLog2 + kWriterSeqBits <= 32, "writer value bits");
+constexpr int kSharedCheckThreads = 256;
+static_assert(MV_WRITE_CHECK_MAX_SEQS == (1 << kWriterSeqBits), "writer index bits");
+
+__device__ __forceinline__ uint32_t hash32(uint32_t k) { return (k * 0x9E3779B1u) >> 7; }
+
 template <typename KV, typename BT>
 __global__ __launch_bounds__(kWriteCheckThreads) void decode_write_check_kernel(
     const int64_t* slots, const BT* bt, int64_t bt_stride, const KV* kv_len, int32_t num_seqs,
-    int32_t max_blocks, int32_t bs_log2, int32_t* status) {
-  __shared__ int s_bad;
-  if (threadIdx.x == 0) s_bad = 0;
+    int32_t max_blocks, int32_t bs_log2, uint64_t* writers, uint32_t hmask, int32_t* status) {
+  constexpr int kMine = MV_WRITE_CHECK_MAX_SEQS / kWriteCheckThreads;
+  __shared__ uint64_t table[kWriteCheckEntries];
+  __shared__ uint32_t dup_blocks[kWriteCheckEntries / 32];
+  __shared__ int s_bad, s_dups;
+  for (uint32_t i = threadIdx.x; i <= hmask; i += kWriteCheckThreads) table[i] = 0;
+  for (uint32_t i = threadIdx.x; i < kWriteCheckEntries / 32; i += kWriteCheckThreads) dup_blocks[i] = 0;
+  if (threadIdx.x == 0) { s_bad = 0; s_dups = 0; }
   __syncthreads();
   int bad = 0;
-  for (int b = threadIdx.x; b < num_seqs; b += kWriteCheckThreads) {
+  uint64_t mine[kMine];  // this thread's writers' words (0: none)
+#pragma unroll
+  for (int i = 0; i < kMine; ++i) mine[i] = 0;
+#pragma unroll
+  for (int i = 0; i < kMine; ++i) {
+    const int b = static_cast<int>(threadIdx.x) + i * kWriteCheckThreads;
+    if (b >= num_seqs) continue;
     const int64_t s = slots[b];
     if (s == -1) continue;
     const int64_t kv = static_cast<int64_t>(kv_len[b]);
     const int64_t e = (kv - 1) >> bs_log2;
+    const int64_t off = (kv - 1) & ((int64_t(1) << bs_log2) - 1);
     bool ok = kv >= 1 && e < max_blocks;
+    int64_t blk = -1;
     if (ok) {
-      const int64_t blk = static_cast<int64_t>(bt[b * bt_stride + e]);
-      ok = blk >= 0 && s == (blk << bs_log2) + ((kv - 1) & ((int64_t(1) << bs_log2) - 1));
+      blk = static_cast<int64_t>(bt[b * bt_stride + e]);
+      // ids that cannot be keyed lie far outside any pool
+      ok = blk >= 0 && blk < int64_t(0xFFFFFFFF) && s == (blk << bs_log2) + off;
     }
-    bad += !ok;
+    if (!ok) { ++bad; continue; }
+    const uint64_t key = static_cast<uint64_t>(blk + 1) << 32;
+    const uint64_t word = key | (static_cast<uint64_t>(off) << kWriterSeqBits) | static_cast<uint64_t>(b);
+    mine[i] = word;
+    uint32_t h = hash32(static_cast<uint32_t>(blk + 1)) & hmask;
+    while (true) {
+      const unsigned long long old = atomicCAS(reinterpret_cast<unsigned long long*>(&table[h]), 0ull,
+                                               static_cast<unsigned long long>(key | 0xFFFFFFFFull));
+      if (old == 0 || (old & 0xFFFFFFFF00000000ull) == key) {
+        // the same key in the high bits: the word's minimum is the value's
+        atomicMin(reinterpret_cast<unsigned long long*>(&table[h]), static_cast<unsigned long long>(word));
+        break;
+      }
+      h = (h + 1) & hmask;
+    }
   }
   if (bad) atomicAdd(&s_bad, bad);
   __syncthreads();
-  if (threadIdx.x == 0) status[0] = s_bad;
+  // A writer at its block's smallest written offset that is not the
+  // block's minimum word writes the minimum writer's slot too.
+  constexpr uint64_t kSeqMask = (1u << kWriterSeqBits) - 1;
+#pragma unroll
+  for (int i = 0; i < kMine; ++i) {
+    const uint64_t word = mine[i];
+    if (!word) continue;
+    uint32_t h = hash32(static_cast<uint32_t>(word >> 32)) & hmask;
+    while ((table[h] ^ word) >> 32) h = (h + 1) & hmask;  // present: inserted above
+    const uint64_t least = table[h];
+    if (((least ^ word) & 0xFFFFFFFFull) >> kWriterSeqBits == 0 && (least & kSeqMask) != (word & kSeqMask))
+      atomicOr(&dup_blocks[h >> 5], 1u << (h & 31));
+  }
+  __syncthreads();
+  int dups = 0;
+  for (uint32_t i = threadIdx.x; i < kWriteCheckEntries / 32; i += kWriteCheckThreads)
+    dups += __popc(dup_blocks[i]);
+  if (dups) atomicAdd(&s_dups, dups);
+  for (uint32_t i = threadIdx.x; i <= hmask; i += kWriteCheckThreads) writers[i] = table[i];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    status[MV_WRITE_CHECK_OWN_SLOT] = s_bad;
+    status[MV_WRITE_CHECK_SHARED] = s_dups;
+  }
 }
 
-__global__ void zero_status(int32_t* status, int n) {
-  if (threadIdx.x < n) status[threadIdx.x] = 0;
+template <typename KV, typename BT>
+__global__ __launch_bounds__(kSharedCheckThreads) void decode_shared_slot_kernel(
+    const BT* bt, int64_t bt_stride, const KV* kv_len, int32_t max_blocks, int32_t bs_log2,
+    const uint64_t* writers, uint32_t hmask, int32_t* status) {
+  const int c = blockIdx.x;
+  const int64_t j = static_cast<int64_t>(blockIdx.y) * kSharedCheckThreads + threadIdx.x;
+  // the table entry is loaded beside the length (j < max_blocks: in the row)
+  const int64_t blk = j < max_blocks ? static_cast<int64_t>(bt[c * bt_stride + j]) : -1;
+  const int64_t kv = static_cast<int64_t>(kv_len[c]);
+  if (kv < 1) return;  // reported by the decode plan
+  const int64_t bs = int64_t(1) << bs_log2;
+  const int64_t n = min<int64_t>((kv + bs - 1) >> bs_log2, max_blocks);
+  if (static_cast<int64_t>(blockIdx.y) * kSharedCheckThreads >= n) return;
+  int hit = 0;
+  if (j < n) {
+    if (blk >= 0 && blk < int64_t(0xFFFFFFFF)) {
+      const uint64_t key = static_cast<uint64_t>(blk + 1) << 32;
+      uint32_t h = hash32(static_cast<uint32_t>(blk + 1)) & hmask;
+      while (true) {
+        const uint64_t w = writers[h];
+        if (w == 0) break;
+        if ((w & 0xFFFFFFFF00000000ull) == key) {
+          const int b = static_cast<int>(w & ((1u << kWriterSeqBits) - 1));
+          const int64_t off = static_cast<int64_t>((w & 0xFFFFFFFFull) >> kWriterSeqBits);
+          const int64_t lim = min<int64_t>(bs, kv - (j << bs_log2));
+          hit = off < lim && !(b == c && j == ((kv - 1) >> bs_log2));
+          break;
+        }
+        h = (h + 1) & hmask;
+      }
+    }
+  }
+  __shared__ int s_hits;
+  if (threadIdx.x == 0) s_hits = 0;
+  __syncthreads();
+  if (hit) atomicAdd(&s_hits, 1);
+  __syncthreads();
+  if (threadIdx.x == 0 && s_hits) atomicAdd(&status[MV_WRITE_CHECK_SHARED], s_hits);
 }
 
 inline int pick_vec(int64_t row_bytes, std::initializer_list<int64_t> values) {
@@ -229,60 +426,111 @@ extern "C" int mv_kv_cache_write(const void* key, int64_t key_stride_tok, int64_
   return check_launch("mv_kv_cache_write");
 }
 
+extern "C" size_t mv_kv_slots_check_workspace_bytes(int64_t num_tokens) {
+  using namespace mv;
+  if (num_tokens <= kSlotsLdsMax) return 0;
+  return static_cast<size_t>(pow2_at_least(2 * num_tokens)) * sizeof(uint64_t);
+}
+
 extern "C" int mv_kv_slots_check(const int64_t* slot_mapping, int64_t num_tokens,
-                                 int64_t total_slots, int32_t* status, void* stream) {
+                                 int64_t total_slots, int32_t* status, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   using namespace mv;
   if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "mv_kv_slots_check: null status");
   if (num_tokens < 0 || total_slots < 0)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_kv_slots_check: negative size");
+  if (num_tokens > kSlotsMax)
+    return fail(MV_ERR_UNSUPPORTED, "mv_kv_slots_check: %lld tokens (at most %lld)",
+                (long long)num_tokens, (long long)kSlotsMax);
+  if (total_slots >= static_cast<int64_t>(kSlotKeyMask))
+    return fail(MV_ERR_UNSUPPORTED, "mv_kv_slots_check: %lld slots in the pool (fewer than 2^44)",
+                (long long)total_slots);
+  if (num_tokens > 0 && !slot_mapping)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_kv_slots_check: null slots");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  zero_status<<<1, 64, 0, s>>>(status, 2);
-  if (num_tokens > 0) {
-    if (!slot_mapping) return fail(MV_ERR_INVALID_ARGUMENT, "mv_kv_slots_check: null slots");
-    const int64_t tiles = (num_tokens + kCheckTile - 1) / kCheckTile;
-    if (tiles > 65535)
-      return fail(MV_ERR_INVALID_ARGUMENT, "mv_kv_slots_check: %lld tokens is too many",
-                  (long long)num_tokens);
-    dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(tiles));
-    slots_check_kernel<<<grid, kCheckTile, 0, s>>>(slot_mapping, num_tokens, total_slots, status);
+  if (num_tokens <= kSlotsLdsMax) {
+    const uint32_t entries = pow2_at_least(std::max<int64_t>(64, 2 * num_tokens));
+    slots_check_lds_kernel<<<1, kSlotsCheckThreads, 0, s>>>(
+        slot_mapping, static_cast<int32_t>(num_tokens), total_slots, entries - 1, status);
+    return check_launch("mv_kv_slots_check");
   }
+  const size_t need = mv_kv_slots_check_workspace_bytes(num_tokens);
+  if (!workspace || workspace_bytes < need)
+    return fail(MV_ERR_INVALID_ARGUMENT,
+                "mv_kv_slots_check: %lld tokens need a %zu-byte workspace (got %zu)",
+                (long long)num_tokens, need, workspace ? workspace_bytes : size_t(0));
+  if (reinterpret_cast<uintptr_t>(workspace) % 8)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_kv_slots_check: workspace not 8-byte aligned");
+  uint64_t* table = static_cast<uint64_t*>(workspace);
+  const int64_t entries = static_cast<int64_t>(need / sizeof(uint64_t));
+  const int64_t clear_groups = std::min<int64_t>((entries + kSlotsGridThreads - 1) / kSlotsGridThreads, 1024);
+  slots_clear_kernel<<<static_cast<unsigned>(clear_groups), kSlotsGridThreads, 0, s>>>(table, entries,
+                                                                                     status);
+  const int64_t groups = (num_tokens + kSlotsGridThreads - 1) / kSlotsGridThreads;
+  slots_check_grid_kernel<<<static_cast<unsigned>(groups), kSlotsGridThreads, 0, s>>>(
+      slot_mapping, num_tokens, total_slots, table, static_cast<uint32_t>(entries - 1), status);
   return check_launch("mv_kv_slots_check");
+}
+
+extern "C" size_t mv_decode_write_check_workspace_bytes(int32_t num_seqs) {
+  using namespace mv;
+  if (num_seqs < 0 || num_seqs > MV_WRITE_CHECK_MAX_SEQS) return 0;
+  return static_cast<size_t>(pow2_at_least(std::max<int64_t>(64, 2 * int64_t(num_seqs)))) *
+         sizeof(uint64_t);
 }
 
 extern "C" int mv_decode_write_check(const int64_t* slot_mapping, const void* block_table,
                                      int32_t bt_is_i64, int64_t bt_stride, const void* kv_len,
                                      int32_t kv_len_is_i64, int32_t num_seqs, int32_t max_blocks,
-                                     int32_t block_size, int32_t* status, void* stream) {
+                                     int32_t block_size, int32_t* status, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
   using namespace mv;
   if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_write_check: null status");
   if (num_seqs < 0 || max_blocks < 0)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_write_check: negative size");
-  if (!is_pow2(block_size))
-    return fail(MV_ERR_UNSUPPORTED, "mv_decode_write_check: block_size %d is not a power of 2",
-                block_size);
+  if (num_seqs > MV_WRITE_CHECK_MAX_SEQS)
+    return fail(MV_ERR_UNSUPPORTED, "mv_decode_write_check: %d sequences (at most %d)", num_seqs,
+                MV_WRITE_CHECK_MAX_SEQS);
+  if (!is_pow2(block_size) || ilog2_exact(block_size) > kWriterMaxBlockLog2)
+    return fail(MV_ERR_UNSUPPORTED,
+                "mv_decode_write_check: block_size %d is not a power of 2 up to 2^%d", block_size,
+                kWriterMaxBlockLog2);
   if (num_seqs > 0 && (!slot_mapping || !kv_len || (max_blocks > 0 && !block_table)))
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_write_check: null pointer");
+  const size_t need = mv_decode_write_check_workspace_bytes(num_seqs);
+  if (!workspace || workspace_bytes < need)
+    return fail(MV_ERR_INVALID_ARGUMENT,
+                "mv_decode_write_check: %d sequences need a %zu-byte workspace (got %zu)",
+                num_seqs, need, workspace ? workspace_bytes : size_t(0));
+  if (reinterpret_cast<uintptr_t>(workspace) % 8)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_write_check: workspace not 8-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int bl = ilog2_exact(block_size);
   const int mb = block_table ? max_blocks : 0;
+  uint64_t* writers = static_cast<uint64_t*>(workspace);
+  const uint32_t hmask = static_cast<uint32_t>(need / sizeof(uint64_t)) - 1;
+  const unsigned chunks = static_cast<unsigned>((mb + kSharedCheckThreads - 1) / kSharedCheckThreads);
+  if (chunks > 65535)
+    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_write_check: %d table columns is too many", mb);
+  const dim3 grid(static_cast<unsigned>(num_seqs), chunks);
+  const bool scan = num_seqs > 0 && chunks > 0;
+#define MV_WRITE_CHECK(KV, BT)                                                                   \
+  do {                                                                                           \
+    decode_write_check_kernel<KV, BT><<<1, kWriteCheckThreads, 0, s>>>(                          \
+        slot_mapping, static_cast<const BT*>(block_table), bt_stride,                            \
+        static_cast<const KV*>(kv_len), num_seqs, mb, bl, writers, hmask, status);               \
+    if (scan)                                                                                    \
+      decode_shared_slot_kernel<KV, BT><<<grid, kSharedCheckThreads, 0, s>>>(                    \
+          static_cast<const BT*>(block_table), bt_stride, static_cast<const KV*>(kv_len), mb, bl, \
+          writers, hmask, status);                                                               \
+  } while (0)
   if (kv_len_is_i64) {
-    if (bt_is_i64)
-      decode_write_check_kernel<int64_t, int64_t><<<1, kWriteCheckThreads, 0, s>>>(
-          slot_mapping, static_cast<const int64_t*>(block_table), bt_stride,
-          static_cast<const int64_t*>(kv_len), num_seqs, mb, bl, status);
-    else
-      decode_write_check_kernel<int64_t, int32_t><<<1, kWriteCheckThreads, 0, s>>>(
-          slot_mapping, static_cast<const int32_t*>(block_table), bt_stride,
-          static_cast<const int64_t*>(kv_len), num_seqs, mb, bl, status);
+    if (bt_is_i64) MV_WRITE_CHECK(int64_t, int64_t);
+    else MV_WRITE_CHECK(int64_t, int32_t);
   } else {
-    if (bt_is_i64)
-      decode_write_check_kernel<int32_t, int64_t><<<1, kWriteCheckThreads, 0, s>>>(
-          slot_mapping, static_cast<const int64_t*>(block_table), bt_stride,
-          static_cast<const int32_t*>(kv_len), num_seqs, mb, bl, status);
-    else
-      decode_write_check_kernel<int32_t, int32_t><<<1, kWriteCheckThreads, 0, s>>>(
-          slot_mapping, static_cast<const int32_t*>(block_table), bt_stride,
-          static_cast<const int32_t*>(kv_len), num_seqs, mb, bl, status);
+    if (bt_is_i64) MV_WRITE_CHECK(int32_t, int64_t);
+    else MV_WRITE_CHECK(int32_t, int32_t);
   }
+#undef MV_WRITE_CHECK
   return check_launch("mv_decode_write_check");
 }

@@ -20,29 +20,16 @@
 #include <stddef.h>
 #include <stdint.h>
 
-typedef int (*decode_write_fn)(const void*, int64_t, int64_t, const void*, int64_t, int64_t,
-                               const void*, int64_t, int64_t, const int64_t*, const void*,
-                               const void*, void*, void*, const int32_t*, const int32_t*,
-                               int64_t, int32_t, int32_t, int32_t, int32_t*, void*, int64_t,
-                               int64_t, float, int32_t, int32_t, int32_t, int32_t, int32_t,
-                               int64_t, int32_t, void*, size_t, void*);
-typedef int (*decode_fn)(const void*, int64_t, int64_t, const void*, const void*, const int32_t*,
-                         const int32_t*, int64_t, int32_t, int32_t, int32_t, int32_t*, void*,
-                         int64_t, int64_t, float, int32_t, int32_t, int32_t, int32_t, int32_t,
-                         int64_t, int32_t, void*, size_t, void*);
-typedef int (*cache_write_fn)(const void*, int64_t, int64_t, const void*, int64_t, int64_t, void*,
-                              void*, const int64_t*, int64_t, int32_t, int32_t, int32_t, int64_t,
-                              int32_t, void*);
+#include "mvattn.h"
 
-typedef int (*rope_write_fn)(const void*, int64_t, int64_t, void*, int64_t, int64_t, const void*,
-                             int64_t, int64_t, void*, int64_t, int64_t, const void*, int64_t,
-                             int64_t, void*, void*, const int64_t*, const int64_t*, const void*,
-                             const void*, int64_t, int64_t, int64_t, int32_t, int32_t, int32_t,
-                             int32_t, int64_t, int32_t, void*);
-
-typedef int (*plan_fn)(const void*, int32_t, const void*, int32_t, int64_t, int32_t, int32_t,
-                       int32_t, int64_t, int32_t, int32_t, int32_t, int32_t, int32_t*, int64_t,
-                       int32_t*, int64_t, int32_t*, int32_t*, void*);
+/* The entry points' types come from the header itself: a change there that
+ * this file does not follow fails the build instead of passing misordered
+ * arguments. */
+typedef __typeof__(&mv_paged_decode_write) decode_write_fn;
+typedef __typeof__(&mv_paged_decode) decode_fn;
+typedef __typeof__(&mv_kv_cache_write) cache_write_fn;
+typedef __typeof__(&mv_rope_kv_cache_write) rope_write_fn;
+typedef __typeof__(&mv_decode_plan) plan_fn;
 
 static decode_write_fn g_decode_write;
 static rope_write_fn g_rope_write;
@@ -269,4 +256,13 @@ static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, "_mvlaunch",
                                     "fast-call wrappers of libmvattn entry points", -1, methods,
                                     NULL, NULL, NULL, NULL};
 
-PyMODINIT_FUNC PyInit__mvlaunch(void) { return PyModule_Create(&module); }
+/* The module carries the ABI version of the header it was built against
+ * (ABI): the Python side binds it only to a library of the same version. */
+PyMODINIT_FUNC PyInit__mvlaunch(void) {
+  PyObject* m = PyModule_Create(&module);
+  if (m && PyModule_AddIntConstant(m, "ABI", MVATTN_ABI_VERSION) < 0) {
+    Py_DECREF(m);
+    return NULL;
+  }
+  return m;
+}

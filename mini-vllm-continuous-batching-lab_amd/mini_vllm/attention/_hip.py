@@ -11,10 +11,11 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+import warnings
 
 import torch  # noqa: F401  (must be loaded before the kernel library)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MV_OK = 0
 MV_ERR_INVALID_ARGUMENT = -1
@@ -26,6 +27,9 @@ MV_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 # status words (mvattn.h)
 MV_SLOTS_OUT_OF_RANGE = 0
 MV_SLOTS_DUPLICATES = 1
+MV_WRITE_CHECK_OWN_SLOT = 0
+MV_WRITE_CHECK_SHARED = 1
+MV_WRITE_CHECK_MAX_SEQS = 4096
 MV_PLAN_NUM_ITEMS = 0
 MV_PLAN_BAD_KV_LEN = 1
 MV_PLAN_INSUFFICIENT = 2
@@ -60,11 +64,13 @@ SIGNATURES = {
         _I64, _I32, _I32, _I32,    # num_tokens, num_kv_heads, head_dim, block_size
         _I64, _I32, _P,            # num_blocks, dtype, stream
     ]),
-    "mv_kv_slots_check": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "mv_kv_slots_check_workspace_bytes": (_SZ, [_I64]),
+    "mv_kv_slots_check": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _SZ, _P]),
+    "mv_decode_write_check_workspace_bytes": (_SZ, [_I32]),
     "mv_decode_write_check": (ctypes.c_int, [
         _P, _P, _I32, _I64,        # slot_mapping, block_table, bt_is_i64, bt_stride
         _P, _I32, _I32, _I32,      # kv_len, kv_len_is_i64, num_seqs, max_blocks
-        _I32, _P, _P,              # block_size, status, stream
+        _I32, _P, _P, _SZ, _P,     # block_size, status, workspace, workspace_bytes, stream
     ]),
     "mv_decode_plan": (ctypes.c_int, [
         _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride
@@ -186,6 +192,12 @@ def _bind_calls(lib: ctypes.CDLL) -> None:
     try:
         from . import _mvlaunch
     except ImportError:
+        _mvlaunch = None
+    if _mvlaunch is not None and getattr(_mvlaunch, "ABI", None) != ABI_VERSION:
+        # built against another header: its argument lists may differ
+        warnings.warn(f"{_mvlaunch.__file__}: built for ABI {getattr(_mvlaunch, 'ABI', None)}, "
+                      f"the library is ABI {ABI_VERSION}; calling through ctypes "
+                      f"(rebuild with build_lib.py)", RuntimeWarning, stacklevel=3)
         _mvlaunch = None
     if _mvlaunch is None:
         decode_write, decode, cache_write, rope_write, plan = ctypes_calls

@@ -124,20 +124,34 @@ _RETIRED_WORKSPACES: List[torch.Tensor] = []
 _WORKSPACE_LOCK = threading.Lock()
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Grow-only, never-freed per-device partial buffer of the decode
-    merge."""
-    ws = _WORKSPACES.get(device)
+def _grow_only(buffers: dict, device: torch.device, nbytes: int) -> torch.Tensor:
+    ws = buffers.get(device)
     if ws is not None and ws.numel() >= nbytes:
         return ws
     with _WORKSPACE_LOCK:
-        ws = _WORKSPACES.get(device)
+        ws = buffers.get(device)
         if ws is None or ws.numel() < nbytes:
             if ws is not None:
                 _RETIRED_WORKSPACES.append(ws)
             ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-            _WORKSPACES[device] = ws
+            buffers[device] = ws
     return ws
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Grow-only, never-freed per-device partial buffer of the decode
+    merge."""
+    return _grow_only(_WORKSPACES, device, nbytes)
+
+
+# Hash tables of the slot check (above 4096 tokens) and of the fused-write
+# check, per device: rebuilt by every call, kept like the merge workspaces
+# for the graphs that captured their address.
+_CHECK_WORKSPACES: dict = {}
+
+
+def _check_workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
+    return _grow_only(_CHECK_WORKSPACES, device, nbytes) if nbytes else None
 
 
 # ----------------------------------------------------------------------------
@@ -259,9 +273,12 @@ def _check_slots(slot_mapping: torch.Tensor, total_slots: int,
         return
     lib = _hip.load()
     status = torch.empty(2, dtype=torch.int32, device=device)
+    n = slot_mapping.numel()
+    ws_bytes = lib.mv_kv_slots_check_workspace_bytes(n)
+    ws = _check_workspace(device, ws_bytes)
     _hip.check(
         lib.mv_kv_slots_check(
-            _ptr(slot_mapping), slot_mapping.numel(), total_slots, _ptr(status), _stream(device)
+            _ptr(slot_mapping), n, total_slots, _ptr(status), _ptr(ws), ws_bytes, _stream(device)
         ),
         "mv_kv_slots_check",
     )
@@ -438,41 +455,59 @@ def _decode_metadata(block_table: torch.Tensor, kv_len_after: torch.Tensor,
 def _fused_write_ok(slot_mapping: torch.Tensor, block_table: torch.Tensor,
                     kv_len_after: torch.Tensor, block_size: int, device: torch.device,
                     capture: int) -> bool:
-    """Whether the decode with the KV write fused is exact for this batch:
-    every slot is -1 or the table position of its own sequence's token
-    ``kv_len_after - 1`` (``mv_decode_write_check``), as the block manager
-    lays them out. Eager: one device check per distinct (unmodified) slots /
-    table / lengths, read back. While capturing: True, with the check
-    recorded for ``check_deferred()`` (``AssertionError``)."""
+    """Whether the decode with the KV write fused is exact for this batch
+    (``mv_decode_write_check``): every slot is -1 or the table position of
+    its own sequence's token ``kv_len_after - 1``, as the block manager lays
+    them out, and no table entry of the batch reads a written slot other
+    than its own sequence's last position (blocks shared without
+    copy-on-write, as the reference's prefix cache shares a prompt's
+    partial last block, break that). Eager: one device check per distinct
+    (unmodified) slots / table / lengths, read back. While capturing: True,
+    with the check recorded for ``check_deferred()`` (``AssertionError``).
+    Batches of more than ``MV_WRITE_CHECK_MAX_SEQS`` sequences are not
+    checked and never fused."""
+    num_seqs = kv_len_after.shape[0]
+    if num_seqs > _hip.MV_WRITE_CHECK_MAX_SEQS:
+        return False
     name = "fused_graph" if capture else "fused"
     extra = (block_size, device, capture)
     hit = _cache_get(name, (slot_mapping, block_table, kv_len_after), extra)
     if hit is not None:
         return hit
     bt, kv = _decode_metadata(block_table, kv_len_after, device)
-    status = torch.empty(1, dtype=torch.int32, device=device)
+    lib = _hip.load()
+    status = torch.empty(2, dtype=torch.int32, device=device)
+    ws_bytes = lib.mv_decode_write_check_workspace_bytes(num_seqs)
+    ws = _check_workspace(device, ws_bytes)
     _hip.check(
-        _hip.load().mv_decode_write_check(
+        lib.mv_decode_write_check(
             _ptr(slot_mapping), _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
             bt.stride(0) if bt.dim() == 2 else 0, _ptr(kv), int(kv.dtype == torch.int64),
-            kv.shape[0], bt.shape[1] if bt.dim() == 2 else 0, block_size, _ptr(status),
-            _stream(device),
+            num_seqs, bt.shape[1] if bt.dim() == 2 else 0, block_size, _ptr(status),
+            _ptr(ws), ws_bytes, _stream(device),
         ),
         "mv_decode_write_check",
     )
 
     def raise_fused(st) -> None:
-        if st[0]:
+        own, shared = st
+        if own:
             raise AssertionError(
-                f"decode with the KV write fused: {st[0]} slot(s) are not their sequence's "
+                f"decode with the KV write fused: {own} slot(s) are not their sequence's "
                 f"position kv_len_after - 1; write the cache and decode in two calls"
+            )
+        if shared:
+            raise AssertionError(
+                f"decode with the KV write fused: {shared} block-table entr(y/ies) of the batch "
+                f"read a slot this call writes (a block shared between sequences); write the "
+                f"cache and decode in two calls"
             )
 
     if capture:
         _defer(capture, raise_fused, status)
         ok = True
     else:
-        ok = status.tolist()[0] == 0
+        ok = not any(status.tolist())
     _cache_put(name, (slot_mapping, block_table, kv_len_after), extra, ok)
     return ok
 
@@ -658,12 +693,13 @@ def hip_decode_attention(
     the step's KV write of those rows (``triton_cache_write``, with its
     checks): pool and output are those of ``hip_cache_write`` followed by
     this call without them. It is one launch when every slot is -1 or its
-    own sequence's position ``kv_len_after - 1`` and no other sequence of
-    the batch attends that slot -- the block manager's layout (a
-    sequence's last block is its own). A batch whose slots are elsewhere is
-    detected on the device and runs as the two calls; inside a captured
-    graph it is reported by ``check_deferred()`` (``AssertionError``)
-    instead. The cross-sequence condition is not checked.
+    own sequence's position ``kv_len_after - 1`` and no other table entry
+    of the batch reads that slot -- the block manager's layout (a
+    sequence's last block is its own). A batch that breaks either (slots
+    elsewhere, or a written block shared with another sequence that
+    attends the slot) is detected on the device and runs as the two calls;
+    inside a captured graph it is reported by ``check_deferred()``
+    (``AssertionError``) instead.
 
     With ``positions`` ``[total_decode]`` and the rotary tables ``cos`` /
     ``sin`` (``[max_positions, >= head_dim]``, the query dtype) as well, the
@@ -1491,7 +1527,12 @@ class AttentionBackendGPU(AttentionBackend):
         tokens and ``decode_attention(layer, query, ...)`` in one launch
         (the runner's two calls, qwen_runner.py:168-190, for the decode
         rows). ``key`` / ``value`` / ``slot_mapping`` are the decode rows
-        (``k[num_prefill:]`` ...); same results as the two calls."""
+        (``k[num_prefill:]`` ...). Output and pool are bit-identical to the
+        two calls: a batch whose slots do not lie at their own sequence's
+        last position, or that another sequence attends (a block shared
+        without copy-on-write), is found on the device and run as the two
+        calls (``hip_decode_attention``; inside a captured graph it is
+        reported by ``check_deferred()``)."""
         if query.shape[0] == 0:
             return query
         group = _find_group(attn_metadata, ("decode_gpu",))

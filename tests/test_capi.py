@@ -95,7 +95,7 @@ def test_every_declared_symbol_is_exported_and_typed(lib):
 
 
 def test_abi_queries(lib):
-    assert lib.mv_abi_version() == _hip.ABI_VERSION == 5
+    assert lib.mv_abi_version() == _hip.ABI_VERSION == 6
     assert lib.mv_decode_chunk_tokens(64, 2) == 64       # 4 waves x one 16-token tile
     assert lib.mv_decode_chunk_tokens(128, 0) == 64
     assert lib.mv_decode_chunk_tokens(96, 2) == 0
@@ -119,6 +119,52 @@ def test_prefill_tokens_per_group(lib):
     assert f(17, 1, 64, 2) == 0                      # more than 16 query heads per kv head
     assert f(14, 3, 64, 2) == 0                      # not a whole GQA group
     assert f(14, 2, 96, 2) == 0                      # head_dim
+
+
+def test_check_workspace_bytes(lib):
+    """The slot check needs no workspace up to 4096 tokens (one work group,
+    LDS); above, a hash table of 8-byte words, a power of two at least twice
+    the tokens. The fused-write check's writer table likewise, at least 64
+    words, and nothing beyond MV_WRITE_CHECK_MAX_SEQS sequences."""
+    f = lib.mv_kv_slots_check_workspace_bytes
+    assert f(0) == f(1) == f(4096) == 0
+    assert f(4097) == 16384 * 8
+    assert f(32768) == 65536 * 8
+    assert f(32769) == 131072 * 8
+    g = lib.mv_decode_write_check_workspace_bytes
+    assert g(0) == g(1) == g(32) == 64 * 8
+    assert g(33) == 128 * 8
+    assert g(4096) == 8192 * 8
+    assert g(4097) == 0 and g(-1) == 0
+
+
+def test_checks_reject_bad_arguments_on_host(lib):
+    """Argument checks of the two device checks return before any launch
+    (dummy or null pointers: nothing is read)."""
+    f = lib.mv_kv_slots_check
+    assert f(16, 10, 100, None, None, 0, None) == _hip.MV_ERR_INVALID_ARGUMENT  # null status
+    assert f(None, 10, 100, 16, None, 0, None) == _hip.MV_ERR_INVALID_ARGUMENT  # null slots
+    assert f(16, -1, 100, 16, None, 0, None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert f(16, 1 << 20, 100, 16, None, 0, None) == _hip.MV_ERR_UNSUPPORTED
+    assert f(16, 10, 1 << 44, 16, None, 0, None) == _hip.MV_ERR_UNSUPPORTED
+    # above 4096 tokens the workspace is required, and its size checked
+    need = lib.mv_kv_slots_check_workspace_bytes(5000)
+    assert f(16, 5000, 100, 16, None, 0, None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert b"workspace" in lib.mv_last_error()
+    assert f(16, 5000, 100, 16, 64, need - 8, None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert f(16, 5000, 100, 16, 68, need, None) == _hip.MV_ERR_INVALID_ARGUMENT  # misaligned
+    assert b"aligned" in lib.mv_last_error()
+
+    g = lib.mv_decode_write_check
+    need = lib.mv_decode_write_check_workspace_bytes(4)
+    assert g(16, 16, 1, 8, 16, 1, 4, 8, 16, None, 64, need, None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert g(16, 16, 1, 8, 16, 1, 4097, 8, 16, 16, 64, 1 << 20, None) == _hip.MV_ERR_UNSUPPORTED
+    assert g(16, 16, 1, 8, 16, 1, 4, 8, 12, 16, 64, need, None) == _hip.MV_ERR_UNSUPPORTED
+    assert g(16, 16, 1, 8, 16, 1, 4, 8, 1 << 21, 16, 64, need, None) == _hip.MV_ERR_UNSUPPORTED
+    assert g(None, 16, 1, 8, 16, 1, 4, 8, 16, 16, 64, need, None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert g(16, 16, 1, 8, 16, 1, 4, 8, 16, 16, None, need, None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert g(16, 16, 1, 8, 16, 1, 4, 8, 16, 16, 64, need - 8, None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert b"workspace" in lib.mv_last_error()
 
 
 def test_workspace_bytes(lib):
@@ -258,6 +304,8 @@ def test_fast_call_wrappers_match_the_header(lib):
         n = declared[name]
         with pytest.raises(TypeError, match=f"takes {n} arguments"):
             fn(*([0] * (n - 1)))
+    # built against this header's ABI
+    assert _mvlaunch.ABI == _hip.ABI_VERSION == lib.mv_abi_version()
     # num_kv_heads (argument 10 of mv_kv_cache_write) beyond int32
     args = [None, 0, 0, None, 0, 0, None, None, None, 0, 1 << 40, 64, 16, 1, 0, None]
     with pytest.raises(OverflowError):
