@@ -1,8 +1,8 @@
 // Device-coherent (agent-scope) word access for hand-offs between work
 // groups of one launch: `global_store/load ... sc1` on gfx950, visible
 // across the XCDs' separate L2 caches without any cache writeback or
-// invalidate. Used by the prefill kernel's key-split merge (the decode kernel
-// keeps its own copies beside its merge).
+// invalidate. Used by the decode kernel's split-K merge and the prefill
+// kernel's key-split merge.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -60,6 +60,7 @@
 #include <climits>
 #include <mutex>
 
+#include "mv_coherent.h"
 #include "mv_common.h"
 #include "mv_rope.h"
 #include "mv_tile.h"
@@ -166,28 +167,6 @@ struct DecodeArgs {
 };
 
 // --------------------------------------------------------------- MFMA ----
-
-// Device-coherent (agent-scope) 8-byte store / load: `global_store/load ... sc1`
-// on gfx950, visible across the XCDs' separate L2 caches without any cache
-// writeback or invalidate.
-__device__ __forceinline__ void store_coherent_u64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t load_coherent_u64(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t load_coherent_u32(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Two fp32 values in one 8-byte word (lo = first in memory).
-__device__ __forceinline__ uint64_t pack_f32x2(float lo, float hi) {
-  return static_cast<uint64_t>(__float_as_uint(lo)) | (static_cast<uint64_t>(__float_as_uint(hi)) << 32);
-}
-__device__ __forceinline__ float unpack_lo(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
-__device__ __forceinline__ float unpack_hi(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); }
 
 // Split-K partial O rows of 16-bit data in the data's own type: a partial
 // row is a convex combination of V rows, so the type holds it, and the

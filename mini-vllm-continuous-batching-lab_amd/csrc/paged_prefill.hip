@@ -158,9 +158,12 @@ struct PrefillArgs {
   // ranges, no split.
   int32_t item_ints;
   // The split's workspace: kPfMaxUnits int32 counters (parts done per
-  // unit, zero at rest), then per unit max parts blocks of kRowWaves * tpw
+  // unit, zero at rest), then per unit max_parts blocks of kRowWaves * tpw
   // * n_rep records (D normalised fp32 values, the fp32 (max, sum) pair).
+  // num_units / max_parts are the host-checked sizes it was allocated for;
+  // an item outside them is skipped, never addressed.
   char* ws;
+  int32_t num_units, max_parts;
 };
 
 template <int DTYPE, int D, typename BT>
@@ -197,6 +200,11 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     const int4 w2 = reinterpret_cast<const int4*>(a.work)[blockIdx.x * 2 + 1];
     kb0 = w2.x;
     kb1 = w2.y;
+    // a part must address a record block of the workspace the host sized
+    const int unit = w2.z, part = w2.w & 0xff, nparts = (w2.w >> 8) & 0xff;
+    if (nparts < 1 || part >= nparts ||
+        (nparts > 1 && (a.ws == nullptr || unit < 0 || unit >= a.num_units || nparts > a.max_parts)))
+      return;
   }
   const int64_t row = a.seqs[4 * seq];
   const int cached = static_cast<int>(a.seqs[4 * seq + 1]);
@@ -715,7 +723,7 @@ __global__ __launch_bounds__((PfTraits<DTYPE, D>::kWaves * 64)) void paged_prefi
     unit = w2.z;
     part = w2.w & 0xff;
     nparts = (w2.w >> 8) & 0xff;
-    max_parts = w2.w >> 16;
+    max_parts = a.max_parts;  // the record stride the workspace was sized for
   }
   constexpr int kRec = D + 2;  // floats per record: the row, then (max, sum)
   const int rows_cap = Tr::kRowWaves * a.tpw * n_rep_e;
@@ -1055,6 +1063,8 @@ int paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head
   }
   a.item_ints = 4;
   a.ws = nullptr;
+  a.num_units = 0;
+  a.max_parts = 1;
   if (parts) {
     a.item_ints = 8;
     if (parts->num_units < 0 || parts->num_units > kPfMaxUnits || parts->max_parts < 1 ||
@@ -1071,6 +1081,8 @@ int paged_prefill(const void* query, int64_t q_stride_tok, int64_t q_stride_head
       if (reinterpret_cast<uintptr_t>(parts->workspace) % 256)
         return fail(MV_ERR_INVALID_ARGUMENT, "mv_paged_prefill_parts: workspace not 256-byte aligned");
       a.ws = static_cast<char*>(parts->workspace);
+      a.num_units = parts->num_units;
+      a.max_parts = parts->max_parts;
     }
   }
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -259,6 +259,22 @@ def test_decode_rejects_unsupported_shapes_on_host(lib):
     assert lib.mv_paged_decode(*_decode_args()) == _hip.MV_ERR_INVALID_ARGUMENT
 
 
+def test_noalloc_rejects_batches_beyond_its_scratch_on_host(lib):
+    """mv_paged_decode_noalloc checks the merge's scratch need against its
+    static array before any HIP call: 4096 sequences x 32 query heads x 128
+    partitions of head_dim 128 are refused with null pointers, no device
+    touched."""
+    n, hq, d, parts = 4096, 32, 128, 128
+    assert lib.mv_paged_decode_workspace_bytes(n, hq, d, parts) > _hip.MV_DECODE_SCRATCH_BYTES
+    rc = lib.mv_paged_decode_noalloc(None, 0, 0, None, None, None, None, 0, 1, 64, parts, None,
+                                     None, 0, 0, 0.125, n, hq, 2, d, 16, 1, 2, None)
+    assert rc == _hip.MV_ERR_INVALID_ARGUMENT
+    assert b"static buffer" in lib.mv_last_error()
+    assert lib.mv_paged_decode_noalloc(None, 0, 0, None, None, None, None, 0, 1, 64, 1, None,
+                                       None, 0, 0, 0.125, -1, hq, 2, d, 16, 1, 2, None) \
+        == _hip.MV_ERR_INVALID_ARGUMENT
+
+
 def test_write_rejects_bad_sizes_on_host(lib):
     rc = lib.mv_kv_cache_write(None, 0, 0, None, 0, 0, None, None, None,
                                4, 0, 64, 16, 10, 2, None)

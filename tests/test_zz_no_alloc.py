@@ -5,8 +5,9 @@ one keeps its split-K partials in the library's static per-GPU scratch
 array instead of a caller's workspace, so the outputs must be bit-identical.
 Two calls in a row, the second on a smaller batch (the array keeps the
 first call's partials), each through the C ABI; device free memory is the
-same before and after a call; a batch whose merge needs more than the array
-holds is rejected before anything is launched.
+same before and after a call. (A batch whose merge needs more than the
+array holds is rejected in host code before anything is launched: that is
+tested without a GPU, in test_capi.py.)
 """
 
 import ctypes
@@ -61,12 +62,22 @@ def _both(case):
                "mv_paged_decode_noalloc")
     torch.cuda.synchronize()
     assert torch.equal(bits(ref.cpu()), bits(got_first.cpu()))
-    free_before = torch.cuda.mem_get_info()[0]
-    _hip.check(lib.mv_paged_decode_noalloc(*_args(d, plan, got), stream),
-               "mv_paged_decode_noalloc")
-    torch.cuda.synchronize()
-    free_after = torch.cuda.mem_get_info()[0]
-    return ref, got, free_before, free_after
+    # Free device memory is a device-wide figure that another process can
+    # move: a call passes when one of up to three readings around it is
+    # unchanged. torch's own allocator statistics must not move at all.
+    torch_before = torch.cuda.memory_stats()["allocated_bytes.all.current"]
+    readings = []
+    for _ in range(3):
+        free_before = torch.cuda.mem_get_info()[0]
+        _hip.check(lib.mv_paged_decode_noalloc(*_args(d, plan, got), stream),
+                   "mv_paged_decode_noalloc")
+        torch.cuda.synchronize()
+        free_after = torch.cuda.mem_get_info()[0]
+        readings.append((free_before, free_after))
+        if free_before == free_after:
+            break
+    assert torch.cuda.memory_stats()["allocated_bytes.all.current"] == torch_before
+    return ref, got, readings
 
 
 def test_noalloc_matches_decode_on_two_calls():
@@ -75,20 +86,7 @@ def test_noalloc_matches_decode_on_two_calls():
                                    ("fixed", [3000, 17, 1500, 640, 2222])), seed=4, nan_fill=True)
     for tag, case in (("c2", big), ("smaller", small)):
         say("noalloc decode", tag)
-        ref, got, free_before, free_after = _both(case)
+        ref, got, readings = _both(case)
         assert torch.equal(bits(ref.cpu()), bits(got.cpu())), tag
         assert not torch.isnan(got.float()).any(), tag
-        assert free_after == free_before, (tag, free_before, free_after)
-
-
-def test_noalloc_rejects_batches_beyond_its_scratch():
-    say("noalloc decode: oversized batch rejected")
-    lib = _hip.load()
-    # 4096 sequences x 32 query heads x 128 partitions of head_dim 128: far
-    # more partials than the static array holds; rejected before any launch
-    n, hq, d, parts = 4096, 32, 128, 128
-    assert lib.mv_paged_decode_workspace_bytes(n, hq, d, parts) > _hip.MV_DECODE_SCRATCH_BYTES
-    rc = lib.mv_paged_decode_noalloc(None, 0, 0, None, None, None, None, 0, 1, 64, parts, None,
-                                     None, 0, 0, 0.125, n, hq, 2, d, 16, 1, 2, None)
-    assert rc == _hip.MV_ERR_INVALID_ARGUMENT
-    assert b"static buffer" in lib.mv_last_error()
+        assert any(a == b for a, b in readings), (tag, readings)
