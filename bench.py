@@ -669,6 +669,25 @@ def main(argv=None) -> int:
         log(f"[bench] captured step {name} ({graph_layers} layers + plan): {us_graph:.1f} us GPU, "
             f"{us_graph_wall:.1f} us host-inclusive")
 
+    # The same step eager: new metadata tensors every step, as the
+    # reference's input builder makes them (here device copies of the
+    # step's tables, lengths, slots and positions), so the first layer
+    # plans and checks and reads the results back once, and 24 sub-layer
+    # calls follow; host-inclusive.
+    def eager_step(i):
+        b2, k2, s2, p2 = bt.clone(), kv.clone(), slots.clone(), pos.clone()
+        for _ in range(graph_layers):
+            L = rot.take()
+            hip_decode_attention(L["q"], L["k"], L["v"], b2, k2, bs, new_key=L["nk"],
+                                 new_value=L["nv"], slot_mapping=s2, positions=p2, cos=cos,
+                                 sin=sin)
+
+    for i in range(3):
+        eager_step(i)
+    us_eager_step = wall_loop(eager_step, max(5, args.steps // graph_layers))
+    log(f"[bench] eager step ({graph_layers} sub-layers, plan and checks at the first): "
+        f"{us_eager_step:.1f} us host-inclusive")
+
     # o_proj of the decode rows (qwen_runner.py:190-193): a [B, Hq*D] x
     # [Hq*D, hidden] GEMM (torch / hipBLASLt), for the fusion decision
     hidden = spec.num_q_heads * spec.head_dim
@@ -765,6 +784,7 @@ def main(argv=None) -> int:
             "us_per_layer": round(graphs["sublayer"][0] / graph_layers, 3),
             "host_inclusive_us_per_step": round(graphs["sublayer"][1], 2),
             "without_rope_us_per_step": round(graphs["write_decode"][0], 2),
+            "eager_host_inclusive_us_per_step": round(us_eager_step, 2),
         },
         "o_proj_gemm_us": round(us_oproj, 3),
         "prefill": prefill,

@@ -63,6 +63,14 @@ extern "C" {
 #define MV_WRITE_CHECK_SHARED 1   /* # table entries of the batch reading a slot written */
 #define MV_WRITE_CHECK_MAX_SEQS 4096
 
+/* Status words written by mv_decode_step_check (int32[MV_STEP_WORDS], device). */
+#define MV_STEP_SLOTS_OUT_OF_RANGE 0 /* as MV_SLOTS_OUT_OF_RANGE, over the decode slots */
+#define MV_STEP_SLOTS_DUPLICATES 1   /* as MV_SLOTS_DUPLICATES */
+#define MV_STEP_WRITE_OWN_SLOT 2     /* as MV_WRITE_CHECK_OWN_SLOT */
+#define MV_STEP_WRITE_SHARED 3       /* as MV_WRITE_CHECK_SHARED */
+#define MV_STEP_POSITIONS 4          /* # positions outside [0, max_positions) */
+#define MV_STEP_WORDS 8
+
 /* Status words written by mv_decode_plan (int32[8], device memory). */
 #define MV_PLAN_NUM_ITEMS 0     /* number of work groups (launch grid) */
 #define MV_PLAN_BAD_KV_LEN 1    /* # sequences with kv_len < 1 */
@@ -169,6 +177,35 @@ int mv_decode_write_check(const int64_t* slot_mapping, const void* block_table, 
                           int64_t bt_stride, const void* kv_len, int32_t kv_len_is_i64,
                           int32_t num_seqs, int32_t max_blocks, int32_t block_size,
                           int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The per-step checks of the fused decode layer call (mv_paged_decode_write,
+ * with or without its RoPE) in two launches, for one host read-back per
+ * step: over the step's num_seqs decode rows it writes status[MV_STEP_*]
+ * (int32[MV_STEP_WORDS], device; words 5-7 unused):
+ *   - the slot check of mv_kv_slots_check (out-of-range slots, duplicate
+ *     pairs) -- the reference's `slot_mapping.unique()` check of
+ *     `triton_cache_write` (paged_attention_gpu.py:126-135) and the range
+ *     check of `write_to_paged_cache` (cache_write.py:61-66);
+ *   - both counts of mv_decode_write_check (fused write precondition);
+ *   - with positions (int64 [num_seqs], else null: word 4 is 0 and no rows
+ *     are written): the positions check of mv_positions_check (the
+ *     reference's rotary table lookup, mini_vllm/model/rotary.py:64-65),
+ *     and cos_rows / sin_rows [num_seqs][head_dim] (contiguous, 16-byte
+ *     aligned) = the tables' rows (row stride table_stride elements,
+ *     16-byte aligned) at each position, clamped into [0, max_positions):
+ *     the rope_cos_rows / rope_sin_rows of mv_paged_decode_write.
+ * num_seqs <= MV_WRITE_CHECK_MAX_SEQS, block_size <= 2^20 and
+ * num_blocks * block_size < 2^44, else MV_ERR_UNSUPPORTED. `workspace` as
+ * for mv_decode_write_check (mv_decode_write_check_workspace_bytes).
+ */
+int mv_decode_step_check(const int64_t* slot_mapping, const void* block_table, int32_t bt_is_i64,
+                         int64_t bt_stride, const void* kv_len, int32_t kv_len_is_i64,
+                         int32_t num_seqs, int32_t max_blocks, int32_t block_size,
+                         int64_t num_blocks, const int64_t* positions, const void* cos_table,
+                         const void* sin_table, int64_t table_stride, int64_t max_positions,
+                         int32_t head_dim, int32_t dtype, void* cos_rows, void* sin_rows,
+                         int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Per-step decode metadata: validation, work split, work list.

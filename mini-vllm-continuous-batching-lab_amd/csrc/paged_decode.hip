@@ -1366,6 +1366,34 @@ struct NewRows {
   const void* rope_sin;
 };
 
+// What any plan of a batch can produce (the plan kernel's own rules):
+// its piece bound L never exceeds l_cap and never falls below
+// min(l_cap, kWaves) (l_cap >= 31 for block sizes >= 1); its groups number
+// at most the resident target when L comes from the search, else (L >= the
+// fair share, or L = l_cap) at most units + total tiles / L.
+struct PlanBounds {
+  int64_t groups, l_cap, max_parts;
+};
+inline PlanBounds plan_bounds(int32_t num_seqs, int32_t max_blocks, int32_t block_size,
+                              int32_t num_kv_heads, int32_t groups_per_cu, int32_t cu_count) {
+  const int bs_log2 = ilog2_exact(block_size);
+  const int64_t l_cap = std::max<int64_t>(
+      1, std::min<int64_t>(INT_MAX / 32, (static_cast<int64_t>(kIdCap - 1) << bs_log2) / kTile));
+  const int64_t max_tiles = (static_cast<int64_t>(max_blocks) * block_size + kTile - 1) / kTile;
+  const int64_t max_parts =
+      std::max<int64_t>(1, std::min<int64_t>(kMaxParts, (max_tiles + kWaves - 1) / kWaves));
+  const int64_t units = static_cast<int64_t>(num_kv_heads) * num_seqs;
+  // at least the plan's resident target (kFewUnitsPerCU per CU when its
+  // live units fit the CUs, else up to kManyUnitsPerCU)
+  const int gpc = std::max(1, groups_per_cu);
+  const int64_t target =
+      static_cast<int64_t>(units <= cu_count ? std::min(kFewUnitsPerCU, gpc)
+                                             : std::max(kFewUnitsPerCU, std::min(kManyUnitsPerCU, gpc))) *
+      std::max(1, cu_count);
+  const int64_t by_fair = units + std::max<int64_t>(target, (units * max_tiles + l_cap - 1) / l_cap);
+  return PlanBounds{std::min<int64_t>(by_fair, units * max_parts), l_cap, max_parts};
+}
+
 }  // namespace
 }  // namespace mv
 
@@ -1389,31 +1417,13 @@ extern "C" int mv_decode_graph_bounds(int32_t num_seqs, int32_t max_blocks, int3
   if (!is_pow2(block_size))
     return fail(MV_ERR_UNSUPPORTED, "mv_decode_graph_bounds: block_size %d is not a power of 2",
                 block_size);
-  // The plan's piece bound L never exceeds l_cap, and never falls below
-  // min(l_cap, kWaves) (l_cap >= 31 here); its groups number at most the
-  // resident target when L comes from the search, else (L >= the fair
-  // share, or L = l_cap) at most units + total tiles / L.
-  const int bs_log2 = ilog2_exact(block_size);
-  const int64_t l_cap = std::max<int64_t>(
-      1, std::min<int64_t>(INT_MAX / 32, (static_cast<int64_t>(kIdCap - 1) << bs_log2) / kTile));
-  const int64_t max_tiles = (static_cast<int64_t>(max_blocks) * block_size + kTile - 1) / kTile;
-  const int64_t max_parts =
-      std::max<int64_t>(1, std::min<int64_t>(kMaxParts, (max_tiles + kWaves - 1) / kWaves));
-  const int64_t units = static_cast<int64_t>(num_kv_heads) * num_seqs;
-  // at least the plan's resident target (kFewUnitsPerCU per CU when its
-  // live units fit the CUs, else up to kManyUnitsPerCU)
-  const int gpc = std::max(1, groups_per_cu);
-  const int64_t target =
-      static_cast<int64_t>(units <= cu_count ? std::min(kFewUnitsPerCU, gpc)
-                                             : std::max(kFewUnitsPerCU, std::min(kManyUnitsPerCU, gpc))) *
-      cu_count;
-  const int64_t by_fair = units + std::max<int64_t>(target, (units * max_tiles + l_cap - 1) / l_cap);
-  const int64_t groups = std::min<int64_t>(by_fair, units * max_parts);
-  if (groups > INT_MAX / 8)
+  const mv::PlanBounds pb = mv::plan_bounds(num_seqs, max_blocks, block_size, num_kv_heads,
+                                            groups_per_cu, cu_count);
+  if (pb.groups > INT_MAX / 8)
     return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_graph_bounds: batch too large");
-  out[0] = groups;
-  out[1] = l_cap * kTile;
-  out[2] = max_parts;
+  out[0] = pb.groups;
+  out[1] = pb.l_cap * kTile;
+  out[2] = pb.max_parts;
   return MV_OK;
 }
 
@@ -1501,10 +1511,14 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
     d.status = status;
     d.num_blocks = num_blocks;
     d.bs_log2 = a.bs_log2;
-    // one wave per slot the work list can hold, in one pass up to 4096 work groups
+    // one wave per slot the plan can fill (the same bound as a launch of
+    // fixed size), in one pass up to 4096 work groups
     constexpr int64_t kSlotsPerGroup = kIdsThreads / 64;
+    const int64_t slots = std::min<int64_t>(
+        work_capacity,
+        plan_bounds(num_seqs, max_blocks, block_size, num_kv_heads, groups_per_cu, cu_count).groups);
     const int grid = static_cast<int>(std::min<int64_t>(
-        4096, std::max<int64_t>(1, (work_capacity + kSlotsPerGroup - 1) / kSlotsPerGroup)));
+        4096, std::max<int64_t>(1, (slots + kSlotsPerGroup - 1) / kSlotsPerGroup)));
     if (bt_is_i64) decode_ids_kernel<int64_t><<<grid, kIdsThreads, 0, s>>>(d);
     else decode_ids_kernel<int32_t><<<grid, kIdsThreads, 0, s>>>(d);
   }

@@ -30,6 +30,12 @@ MV_SLOTS_DUPLICATES = 1
 MV_WRITE_CHECK_OWN_SLOT = 0
 MV_WRITE_CHECK_SHARED = 1
 MV_WRITE_CHECK_MAX_SEQS = 4096
+MV_STEP_SLOTS_OUT_OF_RANGE = 0
+MV_STEP_SLOTS_DUPLICATES = 1
+MV_STEP_WRITE_OWN_SLOT = 2
+MV_STEP_WRITE_SHARED = 3
+MV_STEP_POSITIONS = 4
+MV_STEP_WORDS = 8
 MV_PLAN_NUM_ITEMS = 0
 MV_PLAN_BAD_KV_LEN = 1
 MV_PLAN_INSUFFICIENT = 2
@@ -71,6 +77,14 @@ SIGNATURES = {
         _P, _P, _I32, _I64,        # slot_mapping, block_table, bt_is_i64, bt_stride
         _P, _I32, _I32, _I32,      # kv_len, kv_len_is_i64, num_seqs, max_blocks
         _I32, _P, _P, _SZ, _P,     # block_size, status, workspace, workspace_bytes, stream
+    ]),
+    "mv_decode_step_check": (ctypes.c_int, [
+        _P, _P, _I32, _I64,        # slot_mapping, block_table, bt_is_i64, bt_stride
+        _P, _I32, _I32, _I32,      # kv_len, kv_len_is_i64, num_seqs, max_blocks
+        _I32, _I64,                # block_size, num_blocks
+        _P, _P, _P, _I64, _I64,    # positions, cos, sin, table_stride, max_positions
+        _I32, _I32, _P, _P,        # head_dim, dtype, cos_rows, sin_rows
+        _P, _P, _SZ, _P,           # status, workspace, workspace_bytes, stream
     ]),
     "mv_decode_plan": (ctypes.c_int, [
         _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride

@@ -540,7 +540,6 @@ def plan_decode(
     ``check_deferred()`` after a replay instead. ``capture``: the current
     stream's capture id (0: not capturing), when the caller already knows it.
     """
-    lib = _hip.load()
     if device.index is None:  # "cuda" and "cuda:<current>" are one device: one cached plan
         device = torch.device(device.type, torch.cuda.current_device())
     split = _groups_per_cu(device, head_dim, dtype)
@@ -551,11 +550,47 @@ def plan_decode(
     cached = _cache_get(name, (block_table, kv_len_after), extra)
     if cached is not None:
         return cached
+    pending = _plan_launch(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
+                           dtype, num_kv_heads, split, capture)
+    if pending.fixed:
+        _defer(capture, pending.raise_plan, pending.status)
+        plan = _plan_finish(pending, None)
+    else:
+        plan = _plan_finish(pending, pending.status.tolist())
+    _cache_put(name, (block_table, kv_len_after), extra, plan)
+    return plan
+
+
+@dataclass
+class _PendingPlan:
+    """A plan launched but not yet read back (``_plan_launch``)."""
+
+    work: torch.Tensor
+    block_ids: torch.Tensor
+    counters: torch.Tensor
+    status: torch.Tensor  # MV_PLAN_WORDS words
+    extra: Optional[torch.Tensor]  # status words after the plan's, for the caller
+    status_all: torch.Tensor  # the plan's words, then the extra ones
+    cap: int
+    fixed: int
+    fixed_parts: int
+    raise_plan: Any
+
+
+def _plan_launch(block_table: torch.Tensor, kv_len_after: torch.Tensor, block_size: int,
+                 num_blocks: int, device: torch.device, head_dim: int, dtype: torch.dtype,
+                 num_kv_heads: int, split: Tuple[int, int], capture: int,
+                 extra_words: int = 0) -> _PendingPlan:
+    """Enqueue mv_decode_plan (no read-back). ``extra_words`` status words
+    follow the plan's in the same allocation, so a caller that launches
+    more checks reads everything back at once."""
+    lib = _hip.load()
     bt, kv = _decode_metadata(block_table, kv_len_after, device)
 
     num_seqs = kv.shape[0]
     max_blocks = bt.shape[1] if bt.dim() == 2 else 0
     fixed = 0
+    fixed_parts = 0
     if capture and num_seqs > 0 and max_blocks > 0:
         bounds = (ctypes.c_int64 * 3)()
         _hip.check(lib.mv_decode_graph_bounds(num_seqs, max_blocks, block_size, num_kv_heads,
@@ -573,7 +608,8 @@ def plan_decode(
     n_work, n_ids = 8 * max(cap, 1), -(-max(ids_cap, 4) // 4) * 4
     n_units = max(num_seqs * num_kv_heads, 1)
     n_cnt = -(-n_units // 4) * 4
-    buf = torch.empty(n_work + n_ids + n_cnt + _hip.MV_PLAN_WORDS, dtype=torch.int32, device=device)
+    n_status = _hip.MV_PLAN_WORDS + extra_words
+    buf = torch.empty(n_work + n_ids + n_cnt + n_status, dtype=torch.int32, device=device)
     base = buf.data_ptr()
     _hip.check(
         _hip.plan(
@@ -585,10 +621,8 @@ def plan_decode(
         ),
         "mv_decode_plan",
     )
-    work = buf[:n_work]
-    block_ids = buf[n_work:n_work + n_ids]
-    counters = buf[n_work + n_ids:n_work + n_ids + n_units]
-    status = buf[n_work + n_ids + n_cnt:]
+    s0 = n_work + n_ids + n_cnt
+    status_all = buf[s0:]
 
     def raise_plan(st) -> None:
         if st[_hip.MV_PLAN_BAD_KV_LEN]:
@@ -613,16 +647,23 @@ def plan_decode(
                 f"capacity {cap}"
             )
 
-    if fixed:
-        _defer(capture, raise_plan, status)
-        plan = DecodePlan(work, block_ids, counters, cap, fixed_parts, fixed)
-    else:
-        st = status.tolist()
-        raise_plan(st)
-        plan = DecodePlan(work, block_ids, counters, st[_hip.MV_PLAN_NUM_ITEMS],
-                          st[_hip.MV_PLAN_MAX_PARTS], st[_hip.MV_PLAN_PARTITION_TOKENS])
-    _cache_put(name, (block_table, kv_len_after), extra, plan)
-    return plan
+    return _PendingPlan(
+        work=buf[:n_work], block_ids=buf[n_work:n_work + n_ids],
+        counters=buf[n_work + n_ids:n_work + n_ids + n_units],
+        status=status_all[:_hip.MV_PLAN_WORDS],
+        extra=status_all[_hip.MV_PLAN_WORDS:] if extra_words else None, status_all=status_all,
+        cap=cap, fixed=fixed, fixed_parts=fixed_parts, raise_plan=raise_plan)
+
+
+def _plan_finish(p: _PendingPlan, st: Optional[List[int]]) -> DecodePlan:
+    """The DecodePlan of a launched plan: of fixed size (graph capture, its
+    checks deferred by the caller), or from its status words ``st`` read
+    back, raising for bad metadata."""
+    if p.fixed:
+        return DecodePlan(p.work, p.block_ids, p.counters, p.cap, p.fixed_parts, p.fixed)
+    p.raise_plan(st)
+    return DecodePlan(p.work, p.block_ids, p.counters, st[_hip.MV_PLAN_NUM_ITEMS],
+                      st[_hip.MV_PLAN_MAX_PARTS], st[_hip.MV_PLAN_PARTITION_TOKENS])
 
 
 def _rope_rows(positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, head_dim: int,
@@ -657,6 +698,161 @@ def _rope_rows(positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, he
             sin.index_select(0, idx)[:, :head_dim].contiguous())
     _cache_put(name, (positions, cos, sin), extra, rows)
     return rows
+
+
+def _fused_step_prepare(block_table: torch.Tensor, kv_len_after: torch.Tensor, block_size: int,
+                        num_blocks: int, device: torch.device, head_dim: int, dtype: torch.dtype,
+                        num_kv_heads: int, slot_mapping: torch.Tensor,
+                        positions: Optional[torch.Tensor], cos: Optional[torch.Tensor],
+                        sin: Optional[torch.Tensor], capture: int):
+    """A step's plan and checks for the fused decode layer call, launched
+    together and read back once (eager; captured: deferred): the plan
+    (``plan_decode``, unless the step's tables and lengths already have one)
+    and ``mv_decode_step_check`` -- the slot check (``_check_slots``), the
+    fused-write precondition (``_fused_write_ok``) and, with RoPE, the
+    positions check and the rotary rows (``_rope_rows``). Raises what those
+    raise, in that order, and fills their caches so that the step's other
+    layers, and the two-call sequence a failed precondition falls back to,
+    find them. Returns (plan, slots on the device as int64, whether the
+    fused launch is exact, the rotary rows or None)."""
+    if slot_mapping.device != device:
+        slot_mapping = slot_mapping.to(device)
+    if slot_mapping.dtype != torch.int64:
+        slot_mapping = slot_mapping.to(torch.int64)
+    slots = slot_mapping.contiguous()
+    num_seqs = kv_len_after.shape[0]
+    rope = positions is not None
+    if num_seqs > _hip.MV_WRITE_CHECK_MAX_SEQS:  # not checked: never fused
+        plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
+                           dtype, num_kv_heads, capture=capture)
+        _check_slots(slots, num_blocks * block_size, capture=capture)
+        return plan, slots, False, None
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    lib = _hip.load()
+    split = _groups_per_cu(device, head_dim, dtype)
+    g = "_graph" if capture else ""
+    plan_name = "plan" + g
+    plan_extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads, split, capture)
+    plan = _cache_get(plan_name, (block_table, kv_len_after), plan_extra)
+    total_slots = num_blocks * block_size
+    # the step's other layers (and a failed precondition's fallback): all
+    # of it from the checks' caches, nothing launched
+    if plan is not None and _cache_get("slots" + g, (slots,), (total_slots, capture)) is not None:
+        fused_ok = _cache_get("fused" + g, (slots, block_table, kv_len_after),
+                              (block_size, device, capture))
+        rows = None
+        if rope:
+            rows = _cache_get("rope_rows" + g, (positions, cos, sin), (head_dim, dtype, device, capture))
+        if fused_ok is not None and (rows is not None or not rope):
+            return plan, slots, fused_ok, rows
+    pending = None
+    if plan is None:
+        pending = _plan_launch(block_table, kv_len_after, block_size, num_blocks, device,
+                               head_dim, dtype, num_kv_heads, split, capture,
+                               extra_words=_hip.MV_STEP_WORDS)
+        status = pending.extra
+    else:
+        status = torch.empty(_hip.MV_STEP_WORDS, dtype=torch.int32, device=device)
+    bt, kv = _decode_metadata(block_table, kv_len_after, device)
+    pos = rows = None
+    max_pos = 0
+    if rope:
+        assert cos.dim() == 2 and cos.shape == sin.shape and cos.shape[1] >= head_dim, (
+            f"rotary tables {tuple(cos.shape)} / {tuple(sin.shape)} do not cover head_dim {head_dim}"
+        )
+        assert cos.dtype == dtype and sin.dtype == dtype, f"rotary tables {cos.dtype} != {dtype}"
+        assert cos.device == device and sin.device == device
+        pos = positions
+        if pos.device != device:
+            pos = pos.to(device)
+        if pos.dtype != torch.int64:
+            pos = pos.to(torch.int64)
+        pos = pos.contiguous()
+        tc, ts = cos, sin
+        if (tc.stride(1) != 1 or ts.stride(1) != 1 or tc.stride(0) != ts.stride(0)
+                or (tc.stride(0) * tc.element_size()) % 16 or tc.data_ptr() % 16
+                or ts.data_ptr() % 16):
+            tc, ts = tc.contiguous(), ts.contiguous()
+        max_pos = tc.shape[0]
+        rows = (torch.empty(num_seqs, head_dim, dtype=dtype, device=device),
+                torch.empty(num_seqs, head_dim, dtype=dtype, device=device))
+    ws_bytes = lib.mv_decode_write_check_workspace_bytes(num_seqs)
+    ws = _check_workspace(device, ws_bytes)
+    _hip.check(
+        lib.mv_decode_step_check(
+            _ptr(slots), _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
+            bt.stride(0) if bt.dim() == 2 else 0, _ptr(kv), int(kv.dtype == torch.int64),
+            num_seqs, bt.shape[1] if bt.dim() == 2 else 0, block_size, num_blocks,
+            _ptr(pos), _ptr(tc) if rope else None, _ptr(ts) if rope else None,
+            tc.stride(0) if rope else 0, max_pos, head_dim, _hip.MV_DTYPE[dtype],
+            _ptr(rows[0]) if rope else None, _ptr(rows[1]) if rope else None, _ptr(status),
+            _ptr(ws), ws_bytes, _stream(device),
+        ),
+        "mv_decode_step_check",
+    )
+
+    def raise_slots(st) -> None:
+        bad, dups = st[_hip.MV_STEP_SLOTS_OUT_OF_RANGE], st[_hip.MV_STEP_SLOTS_DUPLICATES]
+        if bad:
+            raise IndexError(
+                f"slot_mapping has {bad} slot(s) out of range [0, {total_slots}) "
+                f"(-1 marks a skipped token)"
+            )
+        if dups:
+            raise AssertionError(
+                f"Duplicate slots in slot_mapping: {dups} duplicate pair(s). "
+                f"The HIP cache write forbids duplicate slots."
+            )
+
+    def raise_fused(st) -> None:
+        own, shared = st[_hip.MV_STEP_WRITE_OWN_SLOT], st[_hip.MV_STEP_WRITE_SHARED]
+        if own:
+            raise AssertionError(
+                f"decode with the KV write fused: {own} slot(s) are not their sequence's "
+                f"position kv_len_after - 1; write the cache and decode in two calls"
+            )
+        if shared:
+            raise AssertionError(
+                f"decode with the KV write fused: {shared} block-table entr(y/ies) of the batch "
+                f"read a slot this call writes (a block shared between sequences); write the "
+                f"cache and decode in two calls"
+            )
+
+    def raise_positions(st) -> None:
+        if st[_hip.MV_STEP_POSITIONS]:
+            raise IndexError(f"{st[_hip.MV_STEP_POSITIONS]} position(s) outside the rotary "
+                             f"tables [0, {max_pos})")
+
+    if capture:
+        if pending is not None:
+            _defer(capture, pending.raise_plan, pending.status)
+            plan = _plan_finish(pending, None)
+        _defer(capture, raise_slots, status)
+        _defer(capture, raise_fused, status)
+        if rope:
+            _defer(capture, raise_positions, status)
+        fused_ok = True
+    else:
+        st = (pending.status_all if pending is not None else status).tolist()
+        if pending is not None:
+            plan = _plan_finish(pending, st[:_hip.MV_PLAN_WORDS])
+            st = st[_hip.MV_PLAN_WORDS:]
+        raise_slots(st)
+        if rope:
+            raise_positions(st)
+        fused_ok = not (st[_hip.MV_STEP_WRITE_OWN_SLOT] or st[_hip.MV_STEP_WRITE_SHARED])
+    # the checks' own caches: the step's other layers and the two-call
+    # fallback look them up
+    if pending is not None:
+        _cache_put(plan_name, (block_table, kv_len_after), plan_extra, plan)
+    _cache_put("slots" + g, (slots,), (total_slots, capture), True)
+    _cache_put("fused" + g, (slots, block_table, kv_len_after), (block_size, device, capture),
+               fused_ok)
+    if rope:
+        _cache_put("positions" + g, (pos,), (max_pos, capture), True)
+        _cache_put("rope_rows" + g, (positions, cos, sin), (head_dim, dtype, device, capture), rows)
+    return plan, slots, fused_ok, rows
 
 
 def hip_decode_attention(
@@ -742,10 +938,36 @@ def hip_decode_attention(
     # one lookup (same tensors at the same in-place versions).
     step = None
     step_extra = (block_size, num_blocks, device, head_dim, dtype, num_kv_heads)
-    if new_key is not None and slot_mapping is not None and not capture:
-        step = _cache_get("fused_step", (slot_mapping, block_table, kv_len_after), step_extra)
+    fused = new_key is not None
+    rope = positions is not None
+    fused_ok = True
+    rope_rows = None
+    if fused:
+        assert new_value is not None and slot_mapping is not None
+        nshape = new_key.shape
+        assert nshape == (total_decode, num_kv_heads, head_dim), (
+            f"new_key {tuple(nshape)} != ({total_decode}, {num_kv_heads}, {head_dim})"
+        )
+        assert new_value.shape == nshape
+        assert new_key.dtype == dtype and new_value.dtype == dtype
+        assert new_key.device == device and new_value.device == device
+        if rope:
+            assert cos is not None and sin is not None
+            assert positions.shape == (total_decode,)
+        if not capture:
+            step = _cache_get("fused_step", (slot_mapping, block_table, kv_len_after), step_extra)
     if step is not None:
-        plan = step[0]
+        plan, slot_mapping = step
+    elif fused:
+        # the step's plan and checks: launched together, read back once
+        slots_given = slot_mapping
+        assert slot_mapping.shape == (total_decode,)
+        plan, slot_mapping, fused_ok, rope_rows = _fused_step_prepare(
+            block_table, kv_len_after, block_size, num_blocks, device, head_dim, dtype,
+            num_kv_heads, slot_mapping, positions, cos, sin, capture)
+        if fused_ok and not capture:
+            _cache_put("fused_step", (slots_given, block_table, kv_len_after), step_extra,
+                       (plan, slot_mapping))
     else:
         plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
                            dtype, num_kv_heads, capture=capture)
@@ -762,36 +984,8 @@ def hip_decode_attention(
         ws_bytes = plan.ws_bytes[num_q_heads] = lib.mv_paged_decode_workspace_bytes(
             total_decode, num_q_heads, head_dim, plan.max_parts)
     ws = _workspace(device, ws_bytes) if ws_bytes else None
-    if new_key is not None:
-        assert new_value is not None and slot_mapping is not None
-        nshape = new_key.shape
-        assert nshape == (total_decode, num_kv_heads, head_dim), (
-            f"new_key {tuple(nshape)} != ({total_decode}, {num_kv_heads}, {head_dim})"
-        )
-        assert new_value.shape == nshape
-        assert new_key.dtype == dtype and new_value.dtype == dtype
-        assert new_key.device == device and new_value.device == device
-        rope = positions is not None
-        if rope:
-            assert cos is not None and sin is not None
-            assert positions.shape == (total_decode,)
-        if step is not None:
-            slot_mapping = step[1]
-        else:
-            slots_given = slot_mapping
-            assert slot_mapping.shape == (total_decode,)
-            if slot_mapping.device != device:
-                slot_mapping = slot_mapping.to(device)
-            if slot_mapping.dtype != torch.int64:
-                slot_mapping = slot_mapping.to(torch.int64)
-            slot_mapping = slot_mapping.contiguous()
-            _check_slots(slot_mapping, num_blocks * block_size, capture=capture)
-            fused_ok = _fused_write_ok(slot_mapping, block_table, kv_len_after, block_size,
-                                       device, capture)
-            if fused_ok and not capture:
-                _cache_put("fused_step", (slots_given, block_table, kv_len_after), step_extra,
-                           (plan, slot_mapping))
-        if step is None and not fused_ok:
+    if fused:
+        if not fused_ok:
             if rope:  # the unfused sequence: rope + write, then decode of the rotated query
                 query, _ = hip_rope_kv_cache_write(query, new_key, new_value, positions, cos, sin,
                                                    key_cache, value_cache, slot_mapping,
@@ -803,7 +997,8 @@ def hip_decode_attention(
                                         block_size)
         rope_cos = rope_sin = None
         if rope:
-            rope_cos, rope_sin = _rope_rows(positions, cos, sin, head_dim, dtype, device, capture)
+            rope_cos, rope_sin = rope_rows if rope_rows is not None else _rope_rows(
+                positions, cos, sin, head_dim, dtype, device, capture)
         nk, nv = _aligned_rows(new_key), _aligned_rows(new_value)
         _hip.check(
             _hip.decode_write(

@@ -167,6 +167,34 @@ def test_checks_reject_bad_arguments_on_host(lib):
     assert b"workspace" in lib.mv_last_error()
 
 
+def test_step_check_rejects_bad_arguments_on_host(lib):
+    f = lib.mv_decode_step_check
+    need = lib.mv_decode_write_check_workspace_bytes(4)
+
+    def call(**kw):
+        a = dict(slots=16, bt=16, bt64=1, bts=8, kv=16, kv64=1, n=4, mb=8, bs=16, nb=100,
+                 pos=None, cos=None, sin=None, tstride=0, maxpos=0, d=64, dt=2, rc=None, rs=None,
+                 st=16, ws=64, wsb=need, stream=None)
+        a.update(kw)
+        return f(*a.values())
+
+    assert call(st=None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert call(n=4097) == _hip.MV_ERR_UNSUPPORTED
+    assert call(bs=12) == _hip.MV_ERR_UNSUPPORTED
+    assert call(nb=1 << 41) == _hip.MV_ERR_UNSUPPORTED  # 2^45 slots
+    assert call(slots=None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert call(ws=None) == _hip.MV_ERR_INVALID_ARGUMENT
+    assert call(wsb=need - 8) == _hip.MV_ERR_INVALID_ARGUMENT
+    # positions need the tables, rows, a dtype and whole 16-byte rows, aligned
+    assert call(pos=16) == _hip.MV_ERR_INVALID_ARGUMENT
+    full = dict(pos=16, cos=64, sin=128, tstride=64, maxpos=100, rc=256, rs=512)
+    assert call(**{**full, "d": 4, "dt": 2}) == _hip.MV_ERR_INVALID_ARGUMENT  # 8-byte rows
+    assert call(**{**full, "cos": 72}) == _hip.MV_ERR_INVALID_ARGUMENT      # misaligned table
+    assert b"aligned" in lib.mv_last_error()
+    assert call(**{**full, "tstride": 32}) == _hip.MV_ERR_INVALID_ARGUMENT  # stride < head_dim
+    assert call(**{**full, "dt": 9}) == _hip.MV_ERR_INVALID_ARGUMENT
+
+
 def test_workspace_bytes(lib):
     assert lib.mv_paged_decode_workspace_bytes(64, 14, 64, 1) == 0
     o = 64 * 14 * 8 * 64 * 4

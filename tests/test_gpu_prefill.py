@@ -105,6 +105,18 @@ def test_prefill_matches_oracle(shape):
     assert err <= TOL[dt], err
 
 
+def test_bench_step_shape():
+    """The bench's own prefill step: 4 sequences x (1536 cached + 512 chunk)
+    at the Qwen2-0.5B shape in bf16 (256 whole work groups, every stage of
+    the lazy softmax reference), in a fused QKV buffer as the runner has it."""
+    say("prefill: bench step 4 x (1536 + 512)")
+    c = _case(14, 2, 64, 16, torch.bfloat16, [1536] * 4, [512] * 4, seed=9, fused=True)
+    out = _run(c)
+    assert not torch.isnan(out).any()
+    err = (out - _ref(c)).abs().max().item()
+    assert err <= TOL[torch.bfloat16], err
+
+
 def test_fused_qkv_views():
     say("prefill fused qkv")
     c = _case(14, 2, 64, 16, torch.bfloat16, [40, 0, 333], [77, 16, 50], seed=2, fused=True)

@@ -307,3 +307,70 @@ def test_slot_check_in_the_write_wrapper_at_32k_tokens():
     dup[-1] = dup[0]
     with pytest.raises(AssertionError, match="Duplicate"):
         pg.hip_cache_write(k, k, kc, vc, dup.to(DEV), bs)
+
+
+def _separate(slots, bt, kv, bs, nb, pos, max_pos):
+    """The three separate checks' words, through their own entry points."""
+    lib = _hip.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    s = _slots_status(slots, nb * bs)
+    w = device_counts(slots, bt, kv, bs)
+    st = torch.full((1,), -7, dtype=torch.int32, device=DEV)
+    p = pos.to(DEV)
+    _hip.check(lib.mv_positions_check(_ptr(p), p.numel(), max_pos, _ptr(st), stream),
+               "mv_positions_check")
+    torch.cuda.synchronize()
+    return list(s) + list(w) + [int(st.item())]
+
+
+@pytest.mark.parametrize("seed,nseq,bs,max_blocks,pool,idx,dt,d", [
+    (0, 64, 16, 8, 60, torch.int64, torch.bfloat16, 64),
+    (1, 256, 16, 6, 300, torch.int32, torch.float16, 128),
+    (2, 33, 4, 20, 90, torch.int64, torch.float32, 64),
+    (3, 4096, 16, 3, 3000, torch.int64, torch.bfloat16, 128),
+])
+def test_step_check_equals_the_separate_checks(seed, nseq, bs, max_blocks, pool, idx, dt, d):
+    """mv_decode_step_check (one work group, then the shared-read grid)
+    gives the words of mv_kv_slots_check, mv_decode_write_check and
+    mv_positions_check on the same inputs, and rows equal to the tables'
+    rows at the clamped positions (bit for bit)."""
+    say("step check", seed, nseq, bs, idx, dt, d)
+    slots, bt, kv = shared_layout(seed, nseq, bs, max_blocks, pool)
+    g = torch.Generator().manual_seed(seed)
+    max_pos = 4000
+    pos = torch.randint(0, max_pos, (nseq,), generator=g)
+    pos[:3] = torch.tensor([-1, max_pos, max_pos + 9])[: min(3, nseq)]
+    slots = torch.as_tensor(slots)
+    slots[0] = pool * bs + 5  # out of the pool
+    cos = torch.randn(max_pos, d + 32, generator=g).to(dt).to(DEV)  # a wider table row
+    sin = torch.randn(max_pos, d + 32, generator=g).to(dt).to(DEV)
+    btt, kvt = torch.from_numpy(bt).to(idx).to(DEV), torch.from_numpy(kv).to(idx).to(DEV)
+    want = _separate(slots, btt, kvt, bs, pool, pos, max_pos)
+    lib = _hip.load()
+    sd, pd = slots.to(DEV), pos.to(DEV)
+    rows_c = torch.full((nseq, d), float("nan"), dtype=dt, device=DEV)
+    rows_s = torch.full((nseq, d), float("nan"), dtype=dt, device=DEV)
+    st = torch.full((_hip.MV_STEP_WORDS,), -7, dtype=torch.int32, device=DEV)
+    nbytes = lib.mv_decode_write_check_workspace_bytes(nseq)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _hip.check(lib.mv_decode_step_check(
+        _ptr(sd), _ptr(btt), int(idx == torch.int64), btt.stride(0), _ptr(kvt),
+        int(idx == torch.int64), nseq, max_blocks, bs, pool, _ptr(pd), _ptr(cos), _ptr(sin),
+        cos.stride(0), max_pos, d, _hip.MV_DTYPE[dt], _ptr(rows_c), _ptr(rows_s), _ptr(st),
+        _ptr(ws), nbytes, stream), "mv_decode_step_check")
+    torch.cuda.synchronize()
+    got = st.tolist()
+    assert got[:5] == want, (got, want)
+    assert got[1] > 0 and got[4] == min(3, nseq) and got[0] >= 1  # the planted cases count
+    idx_c = pd.clamp(0, max_pos - 1)
+    assert torch.equal(bits(rows_c.cpu()), bits(cos.index_select(0, idx_c)[:, :d].cpu()))
+    assert torch.equal(bits(rows_s.cpu()), bits(sin.index_select(0, idx_c)[:, :d].cpu()))
+    # without positions: no rows, word 4 zero
+    st2 = torch.full((_hip.MV_STEP_WORDS,), -7, dtype=torch.int32, device=DEV)
+    _hip.check(lib.mv_decode_step_check(
+        _ptr(sd), _ptr(btt), int(idx == torch.int64), btt.stride(0), _ptr(kvt),
+        int(idx == torch.int64), nseq, max_blocks, bs, pool, None, None, None, 0, 0, d,
+        _hip.MV_DTYPE[dt], None, None, _ptr(st2), _ptr(ws), nbytes, stream), "mv_decode_step_check")
+    torch.cuda.synchronize()
+    assert st2.tolist()[:5] == want[:4] + [0]
