@@ -13,12 +13,19 @@
  * libmvattn.so (bind()). They return the entry point's status code; the
  * caller reads mv_last_error() as for the ctypes call.
  *
+ * decode_write_step takes the arguments of mv_paged_decode_write that
+ * stay the same for every layer of a decode step (plan, slots, rotary
+ * rows, sizes, workspace) packed once per step in a bytes object of
+ * STEP_WORDS 64-bit words (step_words() below gives the order), and per
+ * call only the layer's tensors: 16 arguments instead of 35.
+ *
  * Host code only (plain C, no HIP): built by build_lib.build_launcher().
  */
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <string.h>
 
 #include "mvattn.h"
 
@@ -96,6 +103,66 @@ static PyObject* decode_write(PyObject* self, PyObject* const* a, Py_ssize_t n) 
                                 rope_cos, rope_sin, key_cache, value_cache, work, ids, ids_cap,
                                 groups, part_tokens, max_parts, counters, out, o_st, o_sh, scale,
                                 num_seqs, hq, hkv, d, bs, num_blocks, dtype, ws, ws_bytes, stream);
+  return PyLong_FromLong(rc);
+}
+
+/* The step words of decode_write_step: the arguments of
+ * mv_paged_decode_write that do not change between the layers of a step,
+ * in its order, each as one little-endian 64-bit word (scale as a double). */
+enum {
+  SW_SLOTS, SW_ROPE_COS, SW_ROPE_SIN, SW_WORK, SW_IDS, SW_IDS_CAP, SW_GROUPS, SW_PART_TOKENS,
+  SW_MAX_PARTS, SW_COUNTERS, SW_SCALE, SW_NUM_SEQS, SW_HQ, SW_HKV, SW_D, SW_BS, SW_NUM_BLOCKS,
+  SW_DTYPE, SW_WS, SW_WS_BYTES, STEP_WORDS
+};
+
+static int step_i32(const int64_t* w, int i, int32_t* out) {
+  if (w[i] < INT32_MIN || w[i] > INT32_MAX) {
+    PyErr_Format(PyExc_OverflowError, "_mvlaunch.decode_write_step: step word %d does not fit int32", i);
+    return -1;
+  }
+  *out = (int32_t)w[i];
+  return 0;
+}
+
+/* decode_write_step(step, query, q_st, q_sh, nk, nk_st, nk_sh, nv, nv_st,
+ * nv_sh, key_cache, value_cache, out, o_st, o_sh, stream):
+ * mv_paged_decode_write with the step's words and this layer's tensors. */
+static PyObject* decode_write_step(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (check_nargs("decode_write_step", n, 16, (const void*)g_decode_write)) return NULL;
+  if (!PyBytes_Check(a[0]) || PyBytes_GET_SIZE(a[0]) != (Py_ssize_t)(STEP_WORDS * sizeof(int64_t))) {
+    PyErr_SetString(PyExc_TypeError, "_mvlaunch.decode_write_step: step must be bytes of STEP_WORDS words");
+    return NULL;
+  }
+  int64_t w[STEP_WORDS];
+  memcpy(w, PyBytes_AS_STRING(a[0]), sizeof w);
+  double scale;
+  memcpy(&scale, &w[SW_SCALE], sizeof scale);
+  int32_t groups, part_tokens, max_parts, num_seqs, hq, hkv, d, bs, dtype;
+  if (step_i32(w, SW_GROUPS, &groups) || step_i32(w, SW_PART_TOKENS, &part_tokens) ||
+      step_i32(w, SW_MAX_PARTS, &max_parts) || step_i32(w, SW_NUM_SEQS, &num_seqs) ||
+      step_i32(w, SW_HQ, &hq) || step_i32(w, SW_HKV, &hkv) || step_i32(w, SW_D, &d) ||
+      step_i32(w, SW_BS, &bs) || step_i32(w, SW_DTYPE, &dtype))
+    return NULL;
+  const void* query = arg_ptr(a[1]);
+  const int64_t q_st = arg_i64(a[2]), q_sh = arg_i64(a[3]);
+  const void* nk = arg_ptr(a[4]);
+  const int64_t nk_st = arg_i64(a[5]), nk_sh = arg_i64(a[6]);
+  const void* nv = arg_ptr(a[7]);
+  const int64_t nv_st = arg_i64(a[8]), nv_sh = arg_i64(a[9]);
+  void* key_cache = arg_ptr(a[10]);
+  void* value_cache = arg_ptr(a[11]);
+  void* out = arg_ptr(a[12]);
+  const int64_t o_st = arg_i64(a[13]), o_sh = arg_i64(a[14]);
+  void* stream = arg_ptr(a[15]);
+  if (PyErr_Occurred()) return NULL;
+  const int rc = g_decode_write(
+      query, q_st, q_sh, nk, nk_st, nk_sh, nv, nv_st, nv_sh, (const int64_t*)(intptr_t)w[SW_SLOTS],
+      (const void*)(intptr_t)w[SW_ROPE_COS], (const void*)(intptr_t)w[SW_ROPE_SIN], key_cache,
+      value_cache, (const int32_t*)(intptr_t)w[SW_WORK], (const int32_t*)(intptr_t)w[SW_IDS],
+      w[SW_IDS_CAP], groups, part_tokens, max_parts, (int32_t*)(intptr_t)w[SW_COUNTERS], out, o_st,
+      o_sh, (float)scale, num_seqs, hq, hkv, d, bs, w[SW_NUM_BLOCKS], dtype,
+      (void*)(intptr_t)w[SW_WS], (size_t)w[SW_WS_BYTES], stream);
   return PyLong_FromLong(rc);
 }
 
@@ -241,6 +308,8 @@ static PyMethodDef methods[] = {
     {"bind", (PyCFunction)(void (*)(void))bind, METH_FASTCALL, "bind the entry points"},
     {"decode_write", (PyCFunction)(void (*)(void))decode_write, METH_FASTCALL,
      "mv_paged_decode_write with its 35 arguments"},
+    {"decode_write_step", (PyCFunction)(void (*)(void))decode_write_step, METH_FASTCALL,
+     "mv_paged_decode_write from a step's packed words and one layer's 15 arguments"},
     {"decode", (PyCFunction)(void (*)(void))decode, METH_FASTCALL,
      "mv_paged_decode with its 26 arguments"},
     {"cache_write", (PyCFunction)(void (*)(void))cache_write, METH_FASTCALL,
@@ -260,7 +329,8 @@ static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, "_mvlaunch",
  * (ABI): the Python side binds it only to a library of the same version. */
 PyMODINIT_FUNC PyInit__mvlaunch(void) {
   PyObject* m = PyModule_Create(&module);
-  if (m && PyModule_AddIntConstant(m, "ABI", MVATTN_ABI_VERSION) < 0) {
+  if (m && (PyModule_AddIntConstant(m, "ABI", MVATTN_ABI_VERSION) < 0 ||
+            PyModule_AddIntConstant(m, "STEP_WORDS", STEP_WORDS) < 0)) {
     Py_DECREF(m);
     return NULL;
   }

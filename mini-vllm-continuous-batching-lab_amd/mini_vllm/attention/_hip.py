@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 import threading
 import warnings
 
@@ -197,10 +198,32 @@ decode = None        # mv_paged_decode
 cache_write = None   # mv_kv_cache_write
 rope_write = None    # mv_rope_kv_cache_write
 plan = None          # mv_decode_plan
+# mv_paged_decode_write from a step's packed words (step_words()) and one
+# layer's tensors; None without _mvlaunch (the wrappers then call
+# decode_write with all 35 arguments).
+decode_write_step = None
+
+# The step words' layout (csrc/py_launch.c): mv_paged_decode_write's
+# step-constant arguments in its order, one little-endian 64-bit word each,
+# the scale as a double.
+STEP_WORDS_FORMAT = "<10qd9q"
+STEP_WORDS = 20
+
+
+def step_words(slots: int, rope_cos: int, rope_sin: int, work: int, ids: int, ids_cap: int,
+               groups: int, part_tokens: int, max_parts: int, counters: int, scale: float,
+               num_seqs: int, hq: int, hkv: int, head_dim: int, block_size: int,
+               num_blocks: int, dtype_code: int, ws: int, ws_bytes: int) -> bytes:
+    """The step-constant arguments of mv_paged_decode_write (addresses as
+    ints; None or 0 for a null pointer) packed for decode_write_step."""
+    return struct.pack(STEP_WORDS_FORMAT, slots or 0, rope_cos or 0, rope_sin or 0, work or 0,
+                       ids or 0, ids_cap, groups, part_tokens, max_parts, counters or 0, scale,
+                       num_seqs, hq, hkv, head_dim, block_size, num_blocks, dtype_code, ws or 0,
+                       ws_bytes)
 
 
 def _bind_calls(lib: ctypes.CDLL) -> None:
-    global decode_write, decode, cache_write, rope_write, plan
+    global decode_write, decode, cache_write, rope_write, plan, decode_write_step
     ctypes_calls = (lib.mv_paged_decode_write, lib.mv_paged_decode, lib.mv_kv_cache_write,
                     lib.mv_rope_kv_cache_write, lib.mv_decode_plan)
     try:
@@ -215,11 +238,14 @@ def _bind_calls(lib: ctypes.CDLL) -> None:
         _mvlaunch = None
     if _mvlaunch is None:
         decode_write, decode, cache_write, rope_write, plan = ctypes_calls
+        decode_write_step = None
         return
     _mvlaunch.bind(*(ctypes.cast(fn, ctypes.c_void_p).value for fn in ctypes_calls))
     decode_write, decode, cache_write, rope_write, plan = (
         _mvlaunch.decode_write, _mvlaunch.decode, _mvlaunch.cache_write, _mvlaunch.rope_write,
         _mvlaunch.plan)
+    decode_write_step = (_mvlaunch.decode_write_step
+                         if getattr(_mvlaunch, "STEP_WORDS", None) == STEP_WORDS else None)
 
 
 def load(path: str | None = None) -> ctypes.CDLL:

@@ -956,8 +956,17 @@ def hip_decode_attention(
             assert positions.shape == (total_decode,)
         if not capture:
             step = _cache_get("fused_step", (slot_mapping, block_table, kv_len_after), step_extra)
+    templates = None
     if step is not None:
-        plan, slot_mapping = step
+        plan, slot_mapping, templates = step
+        if _hip.decode_write_step is not None and total_decode and plan.num_groups:
+            # the step's packed launch words, for these query heads and
+            # rotary rows, while the merge workspace they point at is current
+            rows = _rope_rows(positions, cos, sin, head_dim, dtype, device, 0) if rope else None
+            words = templates.get((num_q_heads, id(rows[0]) if rope else 0))
+            if words is not None and (words[1] is None or _WORKSPACES.get(device) is words[1]):
+                return _decode_write_step(words[0], query, new_key, new_value, key_cache,
+                                          value_cache, device)
     elif fused:
         # the step's plan and checks: launched together, read back once
         slots_given = slot_mapping
@@ -966,8 +975,9 @@ def hip_decode_attention(
             block_table, kv_len_after, block_size, num_blocks, device, head_dim, dtype,
             num_kv_heads, slot_mapping, positions, cos, sin, capture)
         if fused_ok and not capture:
+            templates = {}
             _cache_put("fused_step", (slots_given, block_table, kv_len_after), step_extra,
-                       (plan, slot_mapping))
+                       (plan, slot_mapping, templates))
     else:
         plan = plan_decode(block_table, kv_len_after, block_size, num_blocks, device, head_dim,
                            dtype, num_kv_heads, capture=capture)
@@ -1000,6 +1010,17 @@ def hip_decode_attention(
             rope_cos, rope_sin = rope_rows if rope_rows is not None else _rope_rows(
                 positions, cos, sin, head_dim, dtype, device, capture)
         nk, nv = _aligned_rows(new_key), _aligned_rows(new_value)
+        if templates is not None and _hip.decode_write_step is not None:
+            # the other layers of the step launch from these words
+            words = _hip.step_words(
+                _ptr(slot_mapping), _ptr(rope_cos), _ptr(rope_sin), _ptr(plan.work),
+                _ptr(plan.block_ids), plan.block_ids.numel(), plan.num_groups,
+                plan.partition_tokens, plan.max_parts, _ptr(plan.counters),
+                float(head_dim ** -0.5), total_decode, num_q_heads, num_kv_heads, head_dim,
+                block_size, num_blocks, _hip.MV_DTYPE[dtype], _ptr(ws),
+                ws.numel() if ws is not None else 0)
+            templates[(num_q_heads, id(rope_cos) if rope else 0)] = (
+                words, ws, (rope_cos, rope_sin) if rope else None)
         _hip.check(
             _hip.decode_write(
                 _ptr(query), query.stride(0), query.stride(1),
@@ -1028,6 +1049,39 @@ def hip_decode_attention(
             _ptr(ws), ws.numel() if ws is not None else 0, _stream(device),
         ),
         "mv_paged_decode",
+    )
+    return output
+
+
+def _row_args(x: torch.Tensor):
+    """(x, address, row stride, head stride) with 16-byte aligned,
+    head_dim-contiguous rows (a copy only if not)."""
+    st = x.stride()
+    p = x.data_ptr()
+    eb = x.element_size()
+    if st[2] != 1 or (st[0] * eb) % 16 or (st[1] * eb) % 16 or p % 16:
+        x = x.contiguous()
+        st = x.stride()
+        p = x.data_ptr()
+    return x, p, st[0], st[1]
+
+
+def _decode_write_step(words: bytes, query: torch.Tensor, new_key: torch.Tensor,
+                       new_value: torch.Tensor, key_cache: torch.Tensor,
+                       value_cache: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """A layer of a step whose fused launch was already made once: the
+    step's packed words (plan, slots, rotary rows, sizes, workspace) and
+    this layer's tensors."""
+    output = torch.empty_like(query, memory_format=torch.contiguous_format)
+    q, qp, q_st, q_sh = _row_args(query)
+    nk, nkp, nk_st, nk_sh = _row_args(new_key)
+    nv, nvp, nv_st, nv_sh = _row_args(new_value)
+    o_st = output.stride()
+    _hip.check(
+        _hip.decode_write_step(words, qp, q_st, q_sh, nkp, nk_st, nk_sh, nvp, nv_st, nv_sh,
+                               key_cache.data_ptr(), value_cache.data_ptr(), output.data_ptr(),
+                               o_st[0], o_st[1], _stream(device)),
+        "mv_paged_decode_write",
     )
     return output
 

@@ -11,6 +11,7 @@ import os
 import re
 
 import pytest
+import torch
 
 from mini_vllm.attention import _hip
 
@@ -354,3 +355,51 @@ def test_fast_call_wrappers_match_the_header(lib):
     args = [None, 0, 0, None, 0, 0, None, None, None, 0, 1 << 40, 64, 16, 1, 0, None]
     with pytest.raises(OverflowError):
         _mvlaunch.cache_write(*args)
+
+
+def test_step_words_reach_the_entry_point_in_order(lib):
+    """decode_write_step (a step's packed words plus one layer's tensors)
+    calls mv_paged_decode_write with exactly the arguments the 35-argument
+    fast call passes: the entry point is replaced by a ctypes stand-in of
+    the header's signature that records what it receives (no GPU)."""
+    from mini_vllm.attention import _mvlaunch
+
+    assert _mvlaunch.STEP_WORDS == _hip.STEP_WORDS
+    restype, argtypes = _hip.SIGNATURES["mv_paged_decode_write"]
+    seen = []
+
+    def record(*args):
+        seen.append(args)
+        return 7
+
+    stand_in = ctypes.CFUNCTYPE(restype, *argtypes)(record)
+    others = [ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+              for name in ("mv_paged_decode", "mv_kv_cache_write", "mv_rope_kv_cache_write",
+                           "mv_decode_plan")]
+    step = dict(slots=0x1000, rope_cos=0x2000, rope_sin=None, work=0x3000, ids=0x4000, ids_cap=516,
+                groups=510, part_tokens=288, max_parts=8, counters=0x5000, scale=0.125,
+                num_seqs=64, hq=14, hkv=2, head_dim=64, block_size=16, num_blocks=9000,
+                dtype_code=_hip.MV_DTYPE[torch.bfloat16], ws=0x6000, ws_bytes=1 << 20)
+    layer = (0x10, 896, 64, 0x20, 128, 64, 0x30, 256, 64, 0x40, 0x50, 0x60, 896, 64, 0x70)
+    try:
+        _mvlaunch.bind(ctypes.cast(stand_in, ctypes.c_void_p).value, *others)
+        words = _hip.step_words(**step)
+        assert len(words) == 8 * _hip.STEP_WORDS
+        assert _mvlaunch.decode_write_step(words, *layer) == 7
+        full = [0x10, 896, 64, 0x20, 128, 64, 0x30, 256, 64, 0x1000, 0x2000, None, 0x40, 0x50,
+                0x3000, 0x4000, 516, 510, 288, 8, 0x5000, 0x60, 896, 64, 0.125, 64, 14, 2, 64, 16,
+                9000, _hip.MV_DTYPE[torch.bfloat16], 0x6000, 1 << 20, 0x70]
+        assert _mvlaunch.decode_write(*full) == 7
+        assert len(seen) == 2 and seen[0] == seen[1]
+        # a step of the wrong size, or a 32-bit word out of range, is refused
+        with pytest.raises(TypeError, match="STEP_WORDS"):
+            _mvlaunch.decode_write_step(words[:-8], *layer)
+        with pytest.raises(OverflowError, match="step word 12"):
+            _mvlaunch.decode_write_step(_hip.step_words(**{**step, "hq": 1 << 33}), *layer)
+        with pytest.raises(TypeError, match="takes 16 arguments"):
+            _mvlaunch.decode_write_step(words, *layer[:-1])
+        assert len(seen) == 2
+    finally:
+        _hip._bind_calls(lib)
+    assert _hip.decode_write is _mvlaunch.decode_write
+    assert _hip.decode_write_step is _mvlaunch.decode_write_step

@@ -225,7 +225,76 @@ def test_ctypes_route_matches_the_fast_calls(monkeypatch):
     fast = run()
     lib = _hip.load()
     monkeypatch.setattr(_hip, "decode_write", lib.mv_paged_decode_write)
+    monkeypatch.setattr(_hip, "decode_write_step", None)
     monkeypatch.setattr(_hip, "decode", lib.mv_paged_decode)
     monkeypatch.setattr(_hip, "cache_write", lib.mv_kv_cache_write)
     slow = run()
     _same(fast, slow)
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_layers_of_a_step_launch_from_the_step_words(monkeypatch, rope):
+    """After a step's first fused layer call its other layers launch from
+    the step's packed words (decode_write_step: plan, slots, rotary rows,
+    sizes and workspace packed once, then only the layer's tensors). Every
+    layer -- its own query, new rows and pool -- is bit-identical to its
+    two calls, including a layer after the merge workspace grew (the words
+    then point at a retired buffer and are rebuilt)."""
+    from mini_vllm.attention import _hip
+    from mini_vllm.attention import paged_attention_gpu as pg
+    from oracle.rotary_ref import RotaryTables
+    from mini_vllm.attention.paged_attention_gpu import hip_rope_kv_cache_write
+
+    if _hip.load() is None or _hip.decode_write_step is None:
+        pytest.skip("fast-call extension not built")
+    say("decode+write: step words", "rope" if rope else "no rope")
+    real = _hip.decode_write_step
+    calls = []
+
+    def counted(*args):
+        calls.append(args[0])
+        return real(*args)
+
+    monkeypatch.setattr(_hip, "decode_write_step", counted)
+    case = make_case("c2", seed=8, nan_fill=False)
+    spec = case.layout.spec
+    bs = spec.block_size
+    d = to_device(case)
+    pos = d.kv_len - 1
+    tables = RotaryTables(spec.head_dim, 1000000.0, 4096, spec.dtype)
+    cos, sin = tables.cos.to(DEV), tables.sin.to(DEV)
+    extra = dict(positions=pos, cos=cos, sin=sin) if rope else {}
+    g = torch.Generator(device=DEV).manual_seed(8)
+
+    def layer(i):
+        q = torch.randn(d.query.shape, device=DEV, generator=g).to(spec.dtype)
+        nk = torch.randn(d.new_key.shape, device=DEV, generator=g).to(spec.dtype)
+        nv = torch.randn(d.new_value.shape, device=DEV, generator=g).to(spec.dtype)
+        kc1, vc1 = d.key_cache.clone(), d.value_cache.clone()
+        if rope:
+            q_rot, _ = hip_rope_kv_cache_write(q, nk, nv, pos, cos, sin, kc1, vc1,
+                                               d.slot_mapping, bs, return_key=False)
+        else:
+            q_rot = q
+            hip_cache_write(nk, nv, kc1, vc1, d.slot_mapping, bs)
+        ref = hip_decode_attention(q_rot, kc1, vc1, d.block_table, d.kv_len, bs)
+        kc2, vc2 = d.key_cache.clone(), d.value_cache.clone()
+        out = hip_decode_attention(q, kc2, vc2, d.block_table, d.kv_len, bs, new_key=nk,
+                                   new_value=nv, slot_mapping=d.slot_mapping, **extra)
+        torch.cuda.synchronize()
+        _same((ref, kc1, vc1), (out, kc2, vc2))
+
+    for i in range(3):
+        layer(i)
+    assert len(calls) == 2, "layers 2 and 3 of the step launch from its words"
+    # a larger batch elsewhere grows the merge workspace (here: asking for
+    # one byte more than it holds); the step's words are rebuilt
+    dev = d.query.device
+    ws0 = pg._WORKSPACES.get(dev)
+    assert ws0 is not None
+    ws = pg._workspace(dev, ws0.numel() + 1)
+    assert ws is not ws0
+    layer(3)
+    layer(4)
+    assert len(calls) == 3 and calls[1] == calls[0] and calls[2] != calls[1]
+    assert pg._WORKSPACES.get(dev) is ws
