@@ -118,7 +118,8 @@ struct Traits : TileGeom<DTYPE, D> {
   static constexpr int kWaveEpilogueBytes = (kMaxGroup * kORowStride + 2 * kMaxGroup) * 4;
   static constexpr int kFlagOffset = kIdsOffset;
   static constexpr int kRopeOffset = kTilesEnd;  // cos row, then sin row (kRowBytes each)
-  static constexpr int kLdsBytes = kRopeOffset + 2 * kRowBytes;
+  static constexpr int kNewOffset = kRopeOffset + 2 * kRowBytes;  // new K row, then V row (fused write)
+  static constexpr int kLdsBytes = kNewOffset + 2 * kRowBytes;
   static_assert(kWaveEpilogueBytes <= kWaveLds, "a wave's epilogue fits its tile buffers");
   static_assert(kStages >= 2 && kStages <= 4, "tile stages");
   // Work groups one CU holds (160 KiB of LDS on gfx950), and the matching
@@ -270,11 +271,14 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   // is done. When that slot is the token's table position (as the block
   // manager lays it out) the token's row in the LDS tile is overwritten
   // with the new rows -- the bytes the write stores -- before it is used;
-  // otherwise the token is the one read from the pool. Wave new_wave (the
-  // one whose tile holds the token) keeps the rows in registers: lanes
-  // [0, RP) the K row's 16-byte pieces, [RP, 2 RP) the V row's, loaded
-  // before any tile copy so the loop's vmcnt waits still count only tile
-  // copies; the tile copies themselves are those of the plain kernel.
+  // otherwise the token is the one read from the pool. The rows arrive in
+  // LDS with the Q rows (wave 0's copies, before any tile copy); wave
+  // new_wave (the one whose tile holds the token) then keeps them in
+  // registers, lanes [0, RP) the K row's 16-byte pieces, [RP, 2 RP) the V
+  // row's, and with the fused RoPE rotates the K row there, before its
+  // tile loop: off the tail of the sequence's last piece (0.6 us per
+  // layer call when it was done at the last tile). The tile copies
+  // themselves are those of the plain kernel.
   const bool last_piece = FUSED && part == n_parts - 1;
   const int new_wave = ((tok_end - 1 - tok_begin) / kTile) % kWaves;
   int64_t new_slot = -1;
@@ -282,14 +286,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const bool new_lane = wave == new_wave && lane < 2 * RP;
   const int new_pc = lane < RP ? lane : lane - RP;
   if constexpr (FUSED) {
-    if (last_piece) {
-      new_slot = a.slots[b];
-      if (new_lane) {
-        const char* src = lane < RP ? a.new_k + b * a.nk_st + h * a.nk_sh
-                                    : a.new_v + b * a.nv_st + h * a.nv_sh;
-        new_piece = *reinterpret_cast<const uint4*>(src + new_pc * 16);
-      }
-    }
+    if (last_piece) new_slot = a.slots[b];
   }
 
   // ---- Q rows of the group -> LDS (wave 0). Rows r >= n_rep repeat row
@@ -312,6 +309,14 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       const char* src = (lane < RP ? a.rope_cos : a.rope_sin) + static_cast<int64_t>(b) * Tr::kRowBytes +
                         (lane < RP ? lane : lane - RP) * 16;
       copy_to_lds_16B(src, __builtin_amdgcn_readfirstlane(lds0 + Tr::kRopeOffset));
+    }
+    // the sequence's new K and V rows (fused write, last piece): lanes
+    // [0, RP) the K row's pieces, [RP, 2 RP) the V row's, to the LDS rows
+    // after the cos and sin rows
+    if (FUSED && last_piece && lane < 2 * RP) {
+      const char* src = (lane < RP ? a.new_k + b * a.nk_st + h * a.nk_sh : a.new_v + b * a.nv_st + h * a.nv_sh) +
+                        new_pc * 16;
+      copy_to_lds_16B(src, __builtin_amdgcn_readfirstlane(lds0 + Tr::kNewOffset));
     }
   }
 
@@ -511,21 +516,6 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       // replaced when the slot is the token's table position (checked here,
       // long after the slot's load was issued)
       if (last_piece && k == n_chunks - 1 && wave == new_wave) {
-        if constexpr (ROPE) {
-          // RoPE of the new key row (lanes [0, RP)): chunk pc pairs with
-          // chunk pc ^ RP/2 of the other half; cos / sin at its own dims
-          uint4 partner;
-          partner.x = __shfl_xor(new_piece.x, RP / 2);
-          partner.y = __shfl_xor(new_piece.y, RP / 2);
-          partner.z = __shfl_xor(new_piece.z, RP / 2);
-          partner.w = __shfl_xor(new_piece.w, RP / 2);
-          if (lane < RP) {
-            const char* rope = s_lds + Tr::kRopeOffset;
-            const uint4 c = *reinterpret_cast<const uint4*>(rope + lane * 16);
-            const uint4 sn = *reinterpret_cast<const uint4*>(rope + Tr::kRowBytes + lane * 16);
-            new_piece = rotate_chunk<DTYPE>(new_piece, partner, c, sn, lane < RP / 2);
-          }
-        }
         const int lt = tok_end - 1;
         const int id = s_ids[min((lt >> a.bs_log2) - first_blk, kIdCap - 1)];
         if (id >= 0 && new_slot == (static_cast<int64_t>(id) << a.bs_log2) + (lt & bs_mask) &&
@@ -547,7 +537,8 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   if constexpr (S > 3) {
     if (2 < n_chunks) valid[2] = issue_tile(2, IntC<2>{});
   }
-  // Q landed once wave 0's copies older than these tiles are done.
+  // Q (and the rotary and new rows) landed once wave 0's copies older than
+  // these tiles are done.
   asm volatile("" ::: "memory");
   if (wave == 0) wait_vmcnt_groups<2 * L, S - 1>(min(S - 1, n_chunks));
   __syncthreads();  // Q rows visible to every wave
@@ -569,6 +560,27 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       const uint4 cs = *reinterpret_cast<const uint4*>(rope + pc * 16);
       const uint4 sn = *reinterpret_cast<const uint4*>(rope + Tr::kRowBytes + pc * 16);
       qr[c] = rotate_chunk<DTYPE>(qr[c], partner, cs, sn, g < 2);
+    }
+  }
+  if constexpr (FUSED) {
+    if (last_piece && wave == new_wave) {  // wave-uniform
+      // the new rows, landed with the Q rows (the barrier above)
+      if (new_lane) new_piece = *reinterpret_cast<const uint4*>(s_lds + Tr::kNewOffset + lane * 16);
+      if constexpr (ROPE) {
+        // RoPE of the new key row (lanes [0, RP)): chunk pc pairs with
+        // chunk pc ^ RP/2 of the other half; cos / sin at its own dims
+        uint4 partner;
+        partner.x = __shfl_xor(new_piece.x, RP / 2);
+        partner.y = __shfl_xor(new_piece.y, RP / 2);
+        partner.z = __shfl_xor(new_piece.z, RP / 2);
+        partner.w = __shfl_xor(new_piece.w, RP / 2);
+        if (lane < RP) {
+          const char* rope = s_lds + Tr::kRopeOffset;
+          const uint4 c = *reinterpret_cast<const uint4*>(rope + lane * 16);
+          const uint4 sn = *reinterpret_cast<const uint4*>(rope + Tr::kRowBytes + lane * 16);
+          new_piece = rotate_chunk<DTYPE>(new_piece, partner, c, sn, lane < RP / 2);
+        }
+      }
     }
   }
   for (int k = 0; k < n_chunks; k += S) {
