@@ -177,6 +177,9 @@ struct DecodeArgs {
 #ifndef MV_DECODE_PARTIALS16
 #define MV_DECODE_PARTIALS16 1
 #endif
+#ifndef MV_DECODE_EARLY_V
+#define MV_DECODE_EARLY_V 1
+#endif
 
 // A tile keeps p = exp2(s - m) with the head's reference m unchanged when
 // every head's tile sum lies in [kLazyMin, kLazyMax].
@@ -393,6 +396,12 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   auto compute_tile = [&](int k, int st) __attribute__((always_inline)) {
     const char* k_tile = wave_tiles + st * Tr::kStageBytes;
     const char* v_tile = k_tile + Tr::kTileBytes;
+    // 16-bit types: the P V operands are read from LDS with the K operands,
+    // at the start of the tile (MV_DECODE_EARLY_V), not after the softmax:
+    // the PV MFMAs then wait for no LDS round trip of their own
+    constexpr bool kEarlyV = DTYPE != MV_DTYPE_F32 && MV_DECODE_EARLY_V;
+    s16x4 vb[D / 16];
+    if constexpr (kEarlyV) read_v_operands<DTYPE, D>(v_tile, g, t, vb);
     // the MFMAs start from -m / (scale log2 e): acc * scale log2 e = s - m
     const float c0 = -m_run * a.inv_scale_log2;
     f32x4 acc = {c0, c0, c0, c0};
@@ -482,7 +491,14 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
         for (int c = 0; c < D / 16; ++c) o[c][e] *= ar;
       }
     }
-    mfma_pv<DTYPE, D>(p, v_tile, g, t, o);
+    if constexpr (kEarlyV) {
+      s16x4 pa[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pa[0][e] = static_cast<short>(from_f32<DTYPE>(p[e]));
+      mfma_pv_operands<DTYPE, D, 1>(pa, vb, reinterpret_cast<f32x4(&)[1][D / 16]>(o));
+    } else {
+      mfma_pv<DTYPE, D>(p, v_tile, g, t, o);
+    }
   };
 
   // Zeroes the V slots of tokens that were not loaded (P is 0 there, but
