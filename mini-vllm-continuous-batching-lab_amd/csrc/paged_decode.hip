@@ -270,8 +270,8 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const uint32_t wave_tiles_lds = lds0 + wave * Tr::kWaveLds;
 
   // ---- fused KV write (FUSED): the work group holding sequence b's last
-  // token stores the new K / V rows of b into slot slots[b] once its loop
-  // is done. When that slot is the token's table position (as the block
+  // token stores the new K / V rows of b into slot slots[b] before its tile
+  // loop. When that slot is the token's table position (as the block
   // manager lays it out) the token's row in the LDS tile is overwritten
   // with the new rows -- the bytes the write stores -- before it is used;
   // otherwise the token is the one read from the pool. The rows arrive in
@@ -526,7 +526,10 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     asm volatile("" ::: "memory");
     wait_vmcnt_groups<2 * L, S - 1>(n_chunks - 1 - k);
     asm volatile("" ::: "memory");
-    zero_invalid_v(ST, valid[ST]);
+    // (only where a slot of this wave holds no token: a piece's last tile,
+    // or a block id outside the pool; at every tile this cost c4 0.25 and
+    // c5 0.6 us per layer call)
+    if (__builtin_amdgcn_ballot_w64(valid[ST] != (1u << L) - 1u) != 0) zero_invalid_v(ST, valid[ST]);
     if constexpr (FUSED) {
       // the new token's row: last chunk, wave new_wave, row (tok_end - 1) % 16,
       // replaced when the slot is the token's table position (checked here,
@@ -597,6 +600,20 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
           new_piece = rotate_chunk<DTYPE>(new_piece, partner, c, sn, lane < RP / 2);
         }
       }
+      // the KV write of the new token (-1 skips), issued here rather than
+      // after the tile loop, where the merge's wait for its stores would
+      // also wait for this one (0.13 us of a c2 layer call). The tile copy
+      // of the slot's own row may read the old row, the new one or a mix:
+      // its LDS row is replaced with these rows before it is used, and no
+      // other table entry of the batch reads the slot (the precondition).
+      // Older than every tile copy, the store only makes the loop's vmcnt
+      // waits wait for it too.
+      if (new_lane && new_slot >= 0 && new_slot < a.total_slots) {
+        const int64_t blk = new_slot >> a.bs_log2;
+        const int64_t row = ((blk * a.num_kv_heads + h) << a.bs_log2) + (new_slot & bs_mask);
+        char* dst = const_cast<char*>(lane < RP ? a.k_cache : a.v_cache) + row * Tr::kRowBytes;
+        *reinterpret_cast<uint4*>(dst + new_pc * 16) = new_piece;
+      }
     }
   }
   for (int k = 0; k < n_chunks; k += S) {
@@ -610,15 +627,6 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     if constexpr (S > 3) {
       if (k + 3 >= n_chunks) break;
       step(k + 3, IntC<3>{});
-    }
-  }
-
-  if constexpr (FUSED) {  // the KV write of the new token (-1 skips)
-    if (last_piece && new_lane && new_slot >= 0 && new_slot < a.total_slots) {
-      const int64_t blk = new_slot >> a.bs_log2;
-      const int64_t row = ((blk * a.num_kv_heads + h) << a.bs_log2) + (new_slot & bs_mask);
-      char* dst = const_cast<char*>(lane < RP ? a.k_cache : a.v_cache) + row * Tr::kRowBytes;
-      *reinterpret_cast<uint4*>(dst + new_pc * 16) = new_piece;
     }
   }
 
