@@ -249,8 +249,10 @@ int mv_decode_step_check(const int64_t* slot_mapping, const void* block_table, i
  * reads the status on the host, e.g. inside a captured HIP graph: the
  * lists take that bound's stride, and the work_items slots from
  * status[MV_PLAN_NUM_ITEMS] up to work_capacity get sequence -1, which the
- * decode kernel skips. Enqueues the plan (one work group) and the block-id
- * list (many work groups); never synchronises.
+ * decode kernel skips. Enqueues the plan and the block-id lists: one
+ * launch when num_seqs <= 64 and num_seqs * max_blocks <= 8192, else a
+ * plan launch (one work group) and an id-list launch (many work groups);
+ * never synchronises.
  */
 int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                    int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs, int32_t max_blocks,

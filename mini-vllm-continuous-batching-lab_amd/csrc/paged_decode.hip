@@ -832,6 +832,10 @@ constexpr int kPlanWaves = kPlanThreads / 64;
 constexpr int kDealMax = 1024;       // work groups sorted and dealt to CUs in shared memory
 constexpr int kPlanSeqCache = 4096;  // kv lengths held in shared memory
 constexpr int kWaveSearchSeqs = 256; // one wave runs the piece-bound search up to this batch
+constexpr int kWavePlanSeqs = 64;     // decode_plan_wave_kernel (one sequence per lane) up to this batch
+constexpr int kWavePlanWaves = 4;     // its waves (a power of 2)
+constexpr int64_t kFusedTableEntries = 8192;  // plan and ids in one launch up to this table size
+constexpr int64_t kFusedSlots = 4096;         // ... and this many slots (one wave each)
 constexpr int kIdsThreads = 256;     // block-id kernel: threads per work group
 static_assert(kPlanThreads == kDealMax, "the deal holds one group (and one bucket) per thread");
 
@@ -927,6 +931,86 @@ __device__ inline int2 piece_range(int kv, int np, int j) {
     t1 = static_cast<int>(static_cast<int64_t>(j + 1) * tiles / np) * kTile;
   }
   return make_int2(t0, min(kv, t1));
+}
+
+// Step 2 of the plan, shared by both plan kernels: the resident target and
+// the range the piece bound L (in 16-token tiles) is searched in.
+//   Resident slots to fill: 2 per CU when there is at most one (sequence,
+//   kv head) unit per CU -- fewer, longer pieces per CU stream at a
+//   steadier rate per CU than three or four (measured on c2/c3-like
+//   batches), and the split-K merge has fewer partials -- otherwise up to
+//   kManyUnitsPerCU (3 beat the 4 that LDS allows at D=64 on the c4 batch).
+//   A piece spans at most kIdCap table entries (they are staged in LDS):
+//   L <= l_cap, hard. At least one tile per wave per piece and at most
+//   kMaxParts pieces per sequence: L >= l_min, soft.
+// n / d for n >= 0, d > 0: a 32-bit division when both fit (the usual
+// case; the 64-bit expansion is a long dependent chain).
+__device__ inline int64_t div_nonneg(int64_t n, int64_t d) {
+  if (((n | d) >> 32) == 0) return static_cast<uint32_t>(n) / static_cast<uint32_t>(d);
+  return n / d;
+}
+
+struct PieceRules {
+  int64_t target;
+  int l_cap, l_min, l_top, l_fair;
+};
+__device__ inline PieceRules piece_rules(int groups_per_cu, int cu_count, int bs_log2, int64_t units,
+                                         int64_t total_tiles, int most_tiles, int hkv) {
+  PieceRules r;
+  const int per_cu = units <= cu_count ? vmin(kFewUnitsPerCU, vmax(1, groups_per_cu))
+                                       : vmin(kManyUnitsPerCU, vmax(1, groups_per_cu));
+  r.target = static_cast<int64_t>(per_cu) * vmax(1, cu_count);
+  r.l_cap = static_cast<int>(vmax<int64_t>(
+      1, vmin<int64_t>(INT_MAX / 32, ((static_cast<int64_t>(kIdCap - 1)) << bs_log2) / kTile)));
+  r.l_min = vmin(r.l_cap, vmax(kWaves, (most_tiles + kMaxParts - 1) / kMaxParts));
+  r.l_top = vmin(r.l_cap, vmax(r.l_min, most_tiles));
+  r.l_fair = static_cast<int>(vmin<int64_t>(
+      r.l_cap, vmax<int64_t>(r.l_min, div_nonneg(total_tiles * hkv + r.target - 1, r.target))));
+  return r;
+}
+
+// The smallest l in [l_min, l_top] whose groups fit the target (see
+// decode_plan_kernel, step 2). groups(l) = hkv * sum ceil(tiles_b / l)
+// lies in [hkv * total / l, hkv * total / l + units), so no l below
+// ceil(hkv * total / target) fits and every l from
+// ceil(hkv * total / (target - units)) on does: the search runs between
+// the two (a handful of steps, not log2(l_top)). `known` holds groups(l)
+// for the returned l when the search evaluated it, else -1.
+template <typename F>
+__device__ inline int pick_piece_bound(const PieceRules& r, int64_t units, int64_t total_tiles, int hkv,
+                                       F&& groups_at, int64_t& known) {
+  known = -1;
+  int lo = vmin(r.l_fair, r.l_top), hi = r.l_top;
+  bool top_fits = false;
+  if (r.target > units) {
+    const int64_t l_fit = div_nonneg(total_tiles * hkv + (r.target - units) - 1, r.target - units);
+    if (l_fit <= r.l_top) {
+      hi = vmax(lo, static_cast<int>(l_fit));
+      top_fits = true;
+    }
+  }
+  if (!top_fits) {
+    known = groups_at(r.l_top);
+    if (known > r.target) {  // more sequences than slots: several rounds
+      known = -1;
+      return r.l_fair;
+    }
+  }
+  while (lo < hi) {
+    const int mid = lo + (hi - lo) / 2;
+    const int64_t g = groups_at(mid);
+    if (g <= r.target) {
+      hi = mid;
+      known = g;
+    } else {
+      lo = mid + 1;
+    }
+  }
+  if (lo > 2 * r.l_fair) {
+    known = -1;
+    return vmax(r.l_min, vmin(r.l_cap, 2 * r.l_fair));
+  }
+  return lo;
 }
 
 // One work group builds the per-step decode plan:
@@ -1029,62 +1113,11 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   const int64_t units = live_seqs * hkv;  // (sequence, kv head) pairs
 
   // ---- 2. piece bound L (tiles)
-  // Resident slots to fill: 2 per CU when there is at most one (sequence,
-  // kv head) unit per CU -- fewer, longer pieces per CU stream at a
-  // steadier rate per CU than three or four (measured on c2/c3-like
-  // batches), and the split-K merge has fewer partials -- otherwise up to
-  // kManyUnitsPerCU (3 beat the 4 that LDS allows at D=64 on the c4 batch).
-  const int per_cu = units <= a.cu_count ? vmin(kFewUnitsPerCU, vmax(1, a.groups_per_cu))
-                                         : vmin(kManyUnitsPerCU, vmax(1, a.groups_per_cu));
-  const int64_t target = static_cast<int64_t>(per_cu) * vmax(1, a.cu_count);
-  // hard: a piece spans at most kIdCap table entries (they are staged in LDS)
-  const int l_cap = static_cast<int>(vmax<int64_t>(
-      1, vmin<int64_t>(INT_MAX / 32, ((static_cast<int64_t>(kIdCap - 1)) << a.bs_log2) / kTile)));
-  // soft: at least one tile per wave per piece, at most kMaxParts pieces per sequence
-  const int l_min = vmin(l_cap, vmax(kWaves, (most_tiles + kMaxParts - 1) / kMaxParts));
-  const int l_top = vmin(l_cap, vmax(l_min, most_tiles));
-  const int l_fair = static_cast<int>(vmin<int64_t>(
-      l_cap, vmax<int64_t>(l_min, (total_tiles * hkv + target - 1) / target)));
-  // smallest l in [l_min, l_top] whose groups fit the target (see above).
-  // groups(l) = hkv * sum ceil(tiles_b / l) lies in [hkv * total / l,
-  // hkv * total / l + units), so no l below ceil(hkv * total / target)
-  // fits and every l from ceil(hkv * total / (target - units)) on does:
-  // the search runs between the two (a handful of steps, not log2(l_top)).
-  // `known` holds groups(hi) once evaluated (-1 before), so it returns
-  // groups(l) when the search evaluated it.
+  const PieceRules rules =
+      piece_rules(a.groups_per_cu, a.cu_count, a.bs_log2, units, total_tiles, most_tiles, hkv);
+  const int64_t target = rules.target;
   auto pick = [&](auto&& groups_at, int64_t& known) -> int {
-    known = -1;
-    int lo = vmin(l_fair, l_top), hi = l_top;
-    bool top_fits = false;
-    if (target > units) {
-      const int64_t l_fit = (total_tiles * hkv + (target - units) - 1) / (target - units);
-      if (l_fit <= l_top) {
-        hi = vmax(lo, static_cast<int>(l_fit));
-        top_fits = true;
-      }
-    }
-    if (!top_fits) {
-      known = groups_at(l_top);
-      if (known > target) {  // more sequences than slots: several rounds
-        known = -1;
-        return l_fair;
-      }
-    }
-    while (lo < hi) {
-      const int mid = lo + (hi - lo) / 2;
-      const int64_t g = groups_at(mid);
-      if (g <= target) {
-        hi = mid;
-        known = g;
-      } else {
-        lo = mid + 1;
-      }
-    }
-    if (lo > 2 * l_fair) {
-      known = -1;
-      return vmax(l_min, vmin(l_cap, 2 * l_fair));
-    }
-    return lo;
+    return pick_piece_bound(rules, units, total_tiles, hkv, groups_at, known);
   };
   int lb;
   int64_t num_groups;
@@ -1291,6 +1324,45 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
   }
 }
 
+// Slot s's block-id list (step 5 of the plan): ids[s * n, (s + 1) * n) with
+// n = per_item (a multiple of 4, at most kIdCap) holds the pool blocks of
+// its piece in entries [0, span) and -1 for an entry outside the pool; -1
+// fills the rest of the last group of four. Entries past that are not
+// written: the decode kernel uses only [0, span) (with a fixed piece bound
+// n is the widest piece's span, so most of each list is never written).
+// One wave writes the list, 4 ids per lane per pass (at most 2 passes of
+// 256). Returns this lane's count of bad entries among the reads of a kv
+// head 0 piece's own blocks (a block belongs to the one piece that holds
+// its first token, so over all slots each needed table entry counts once).
+template <typename BT>
+__device__ inline int write_slot_ids(const BT* btp, int64_t bt_stride, int num_seqs, int max_blocks,
+                                     int64_t num_blocks, int bs_log2, int per_item, int32_t* ids,
+                                     int64_t slot, int4 w0, int4 w1, int lane) {
+  const int first = w1.x >> bs_log2;
+  const int last = (w1.y - 1) >> bs_log2;
+  // the bounds hold for every entry the plan writes
+  const bool seq_ok = w0.x >= 0 && w0.x < num_seqs;
+  const BT* row = btp + (seq_ok ? static_cast<int64_t>(w0.x) * bt_stride : 0);
+  int4* out = reinterpret_cast<int4*>(ids + slot * per_item);
+  const int span = seq_ok ? vmax(0, last - first + 1) : 0;
+  const int n_write = vmin(per_item, (span + 3) & ~3);
+  int bad = 0;
+  for (int k0 = 4 * lane; k0 < n_write; k0 += 4 * 64) {
+    int32_t v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = first + k0 + e;
+      const bool read = seq_ok && m <= last && m >= 0 && m < max_blocks;
+      const int64_t blk = read ? static_cast<int64_t>(row[m]) : -1;
+      const bool in_pool = blk >= 0 && blk < num_blocks;
+      bad += read && w0.y == 0 && (static_cast<int64_t>(m) << bs_log2) >= w1.x && !in_pool;
+      v[e] = in_pool ? static_cast<int32_t>(blk) : -1;
+    }
+    out[k0 >> 2] = make_int4(v[0], v[1], v[2], v[3]);
+  }
+  return bad;
+}
+
 struct IdsArgs {
   const void* block_table;
   int64_t bt_stride;
@@ -1303,20 +1375,11 @@ struct IdsArgs {
   int32_t bs_log2;
 };
 
-// Step 5 of the plan, over many CUs: slot s's list ids[s * n, (s + 1) * n)
-// (n = status[MV_PLAN_IDS_PER_ITEM], a multiple of 4, at most kIdCap)
-// holds the pool blocks of its piece in entries [0, span) and -1 for an
-// entry outside the pool; -1 fills the rest of the last group of four.
-// Entries past that are not written: the decode kernel uses only [0, span)
-// (with a fixed piece bound n is the widest piece's span, so most of each
-// list is never written). One wave writes one slot's list, 4 ids per lane
-// per pass (at most 2 passes of 256). The slot follows from blockIdx and the
-// wave alone, so its work entry loads beside the status word: two
-// dependent round trips (entry and status, then the table) before the
-// stores. The pieces of kv head 0 read every block of every valid
-// sequence, and a block belongs to the one piece that holds its first
-// token: counting the bad entries among those reads checks each table
-// entry a sequence needs exactly once.
+// Step 5 of the plan, over many CUs, after a plan kernel: one wave per slot
+// (write_slot_ids). The slot follows from blockIdx and the wave alone, so
+// its work entry loads beside the status word: two dependent round trips
+// (entry and status, then the table) before the stores. The bad entries
+// counted are added to status[MV_PLAN_BAD_BLOCK].
 template <typename BT>
 __global__ __launch_bounds__(kIdsThreads) void decode_ids_kernel(IdsArgs a) {
   constexpr int kSlotsPerGroup = kIdsThreads / 64;
@@ -1330,29 +1393,351 @@ __global__ __launch_bounds__(kIdsThreads) void decode_ids_kernel(IdsArgs a) {
     const int per_item = a.status[MV_PLAN_IDS_PER_ITEM];  // -1: no list this step
     const int groups = a.status[MV_PLAN_NUM_ITEMS];
     if (per_item <= 0 || slot >= groups) break;  // uniform per wave; later slots are larger
-    const int first = w1.x >> a.bs_log2;
-    const int last = (w1.y - 1) >> a.bs_log2;
-    // the bounds hold for every entry the plan writes
-    const bool seq_ok = w0.x >= 0 && w0.x < a.num_seqs;
-    const BT* row = btp + (seq_ok ? static_cast<int64_t>(w0.x) * a.bt_stride : 0);
-    int4* out = reinterpret_cast<int4*>(a.ids + slot * per_item);
-    const int span = seq_ok ? vmax(0, last - first + 1) : 0;
-    const int n_write = vmin(per_item, (span + 3) & ~3);
-    for (int k0 = 4 * lane; k0 < n_write; k0 += 4 * 64) {
-      int32_t v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = first + k0 + e;
-        const bool read = seq_ok && m <= last && m >= 0 && m < a.max_blocks;
-        const int64_t blk = read ? static_cast<int64_t>(row[m]) : -1;
-        const bool in_pool = blk >= 0 && blk < a.num_blocks;
-        bad += read && w0.y == 0 && (static_cast<int64_t>(m) << a.bs_log2) >= w1.x && !in_pool;
-        v[e] = in_pool ? static_cast<int32_t>(blk) : -1;
-      }
-      out[k0 >> 2] = make_int4(v[0], v[1], v[2], v[3]);
-    }
+    bad += write_slot_ids(btp, a.bt_stride, a.num_seqs, a.max_blocks, a.num_blocks, a.bs_log2, per_item,
+                          a.ids, slot, w0, w1, lane);
   }
   if (bad) atomicAdd(&a.status[MV_PLAN_BAD_BLOCK], bad);
+}
+
+// What each wave of decode_plan_wave_kernel computes by itself, lane b
+// holding sequence b (and, for a dealt plan, size bucket b).
+struct WavePlan {
+  bool mine, kv_ok;  // lane b < num_seqs; its kv_len is usable
+  int64_t kv_raw;
+  int kv, tiles, np, q, r;  // np pieces of q or q + 1 tiles (r of them q + 1)
+  int ka, kb, na, nb;       // buckets of the (q + 1)- and q-tile pieces, groups in each
+  int pre_a, pre_b;         // dealt: first positions of the sequence's groups in ka, kb
+  int item0;                // natural order: first item
+  int start, cnt;           // dealt: first position and groups of bucket `lane`
+  // uniform
+  int lb, part_tokens, max_parts, per_item, most_tiles, rounds, cus;
+  int least_kv, bad_kv, short_table;
+  int64_t num_groups, used_groups;
+  bool deal, listed, fixed;
+};
+
+// Steps 1-3 of the plan for at most kWavePlanSeqs sequences, by each wave
+// on its own (no barrier, no shared counts): lengths, the piece bound
+// (decode_plan_kernel's rules) and the deal's positions. In the deal the
+// groups are sorted by size into buckets (L - size) >> shift of 2^shift
+// tiles, at most 64 (exact sizes up to L = 64 tiles, one bucket per
+// lane); a group's position is its bucket's start + the groups of the
+// bucket in earlier sequences + its index among its sequence's groups of
+// the bucket (one scan per bucket in use, four at a time: few, the pieces
+// of a batch differ little in size).
+template <typename KV>
+__device__ inline void wave_plan_lengths(const PlanArgs& a, WavePlan& p, int lane) {
+  const KV* kvp = static_cast<const KV*>(a.kv_len);
+  const int64_t bs = int64_t(1) << a.bs_log2;
+  // ---- 1. lengths (kv_len outside [1, INT_MAX / 2] or beyond the table
+  // row: no piece reads the sequence)
+  p.mine = lane < a.num_seqs;
+  p.kv_raw = p.mine ? static_cast<int64_t>(kvp[lane]) : 1;
+  p.kv_ok = p.kv_raw >= 1 && p.kv_raw <= INT_MAX / 2 && (p.kv_raw + bs - 1) / bs <= a.max_blocks;
+  p.kv = p.mine && p.kv_ok ? static_cast<int>(p.kv_raw) : 0;
+  p.tiles = (p.kv + kTile - 1) / kTile;
+}
+
+// Steps 2-3 after wave_plan_lengths; the deal's positions only when
+// `positions`.
+__device__ inline void wave_plan_rest(const PlanArgs& a, WavePlan& p, int* s_count, int lane, bool positions) {
+  const int hkv = a.num_kv_heads;
+  s_count[lane] = 0;
+  const int64_t total_tiles = wave_sum64(p.tiles);
+  const int live_seqs = wave_sum(p.kv > 0);
+  p.most_tiles = wave_max(p.tiles);
+  p.least_kv =
+      wave_min(p.mine ? static_cast<int>(vmax<int64_t>(vmin<int64_t>(p.kv_raw, INT_MAX), INT_MIN)) : INT_MAX);
+  p.bad_kv = wave_sum(p.mine && p.kv_raw < 1);
+  p.short_table = wave_sum(p.mine && p.kv_raw >= 1 && !p.kv_ok);
+  const int64_t units = static_cast<int64_t>(live_seqs) * hkv;
+
+  // ---- 2. piece bound L (tiles)
+  const PieceRules rules =
+      piece_rules(a.groups_per_cu, a.cu_count, a.bs_log2, units, total_tiles, p.most_tiles, hkv);
+  const bool narrow = static_cast<int64_t>(kWavePlanSeqs) * p.most_tiles < (int64_t(1) << 30);
+  const int tiles = p.tiles;
+  auto groups_at = [&](int l) -> int64_t {
+    const int n = static_cast<int>(static_cast<uint32_t>(tiles + l - 1) / static_cast<uint32_t>(l));
+    return (narrow ? static_cast<int64_t>(wave_sum(n)) : wave_sum64(n)) * hkv;
+  };
+  p.lb = pick_piece_bound(rules, units, total_tiles, hkv, groups_at, p.num_groups);
+  if (p.num_groups < 0) p.num_groups = groups_at(p.lb);
+  p.part_tokens = p.lb * kTile;
+  p.np = static_cast<int>(static_cast<uint32_t>(p.tiles + p.lb - 1) / static_cast<uint32_t>(p.lb));
+  p.max_parts = wave_max(p.np);
+
+  // ---- what the entries and id lists hold (as in decode_plan_kernel)
+  p.deal = p.num_groups <= kDealMax && p.num_groups <= rules.target && a.cu_count > 0;
+  p.used_groups = vmin<int64_t>(p.num_groups, a.work_cap);
+  p.fixed = a.fixed_part_tokens > 0;
+  p.per_item = ids_per_item(p.fixed ? a.fixed_part_tokens : p.part_tokens, a.bs_log2);
+  const int64_t n_ids = p.used_groups * p.per_item;
+  p.listed = p.used_groups == p.num_groups && n_ids <= a.ids_cap && n_ids <= INT_MAX &&
+             (!p.fixed || p.part_tokens <= a.fixed_part_tokens);
+  p.cus = vmax(1, a.cu_count);
+  p.rounds = static_cast<int>(div_nonneg(p.num_groups + p.cus - 1, p.cus));
+
+  // ---- 3. sizes, buckets, positions
+  p.q = p.np > 0 ? p.tiles / p.np : 0;
+  p.r = p.np > 0 ? p.tiles - p.q * p.np : 0;
+  int shift = 0;
+  while (((p.lb - 1) >> shift) >= 64) ++shift;
+  p.kb = p.np > 0 ? (p.lb - p.q) >> shift : 0;
+  p.ka = p.r > 0 ? (p.lb - p.q - 1) >> shift : p.kb;
+  p.na = p.ka == p.kb ? p.np * hkv : p.r * hkv;
+  p.nb = p.ka == p.kb ? 0 : (p.np - p.r) * hkv;
+  p.pre_a = p.pre_b = p.item0 = p.start = p.cnt = 0;
+  if (!positions) return;
+  if (p.listed && p.deal) {
+    // the buckets in use (flags in LDS, this wave's own copy), then in
+    // ascending order, four at a time (independent scans): the groups of
+    // bucket k in earlier sequences, its total and its start
+    if (p.na > 0) s_count[p.ka] = 1;
+    if (p.nb > 0) s_count[p.kb] = 1;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's own LDS stores
+    __builtin_amdgcn_wave_barrier();
+    uint64_t used = __builtin_amdgcn_ballot_w64(s_count[lane] != 0);
+    int run = 0;  // positions taken by the buckets before
+    while (used != 0) {
+      int k[4], c[4], incl[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        k[u] = used != 0 ? __builtin_ctzll(used) : 64;
+        used &= used - 1;
+        c[u] = (p.ka == k[u] ? p.na : 0) + (p.kb == k[u] ? p.nb : 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) incl[u] = wave_scan_sum(c[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int before = incl[u] - c[u] + run;
+        if (p.ka == k[u]) p.pre_a = before;
+        if (p.kb == k[u]) p.pre_b = before;
+        const int total = __builtin_amdgcn_readlane(incl[u], 63);
+        if (lane == k[u]) {
+          p.start = run;
+          p.cnt = total;
+        }
+        run += total;
+      }
+    }
+  } else if (p.listed) {
+    p.item0 = wave_scan_sum(p.np) - p.np;  // sums at most num_groups <= INT_MAX / 4 (listed)
+  }
+}
+
+// First tile, token range and whether piece j of a sequence of np pieces
+// (q or q + 1 tiles, r of them q + 1) has q + 1 tiles, with bb = the
+// (q + 1)-tile pieces before it, floor(j r / np).
+struct PieceSpan {
+  int bb, tok0, tok1;
+  bool big;
+};
+__device__ inline PieceSpan piece_span(int kv, int np, int q, int r, int j, bool wide) {
+  PieceSpan ps;
+  int rem;
+  if (!wide) {
+    const uint32_t jr = static_cast<uint32_t>(j) * static_cast<uint32_t>(r);
+    ps.bb = static_cast<int>(jr / static_cast<uint32_t>(np));
+    rem = static_cast<int>(jr - static_cast<uint32_t>(ps.bb) * static_cast<uint32_t>(np));
+  } else {
+    const int64_t jr = static_cast<int64_t>(j) * r;
+    ps.bb = static_cast<int>(jr / np);
+    rem = static_cast<int>(jr - static_cast<int64_t>(ps.bb) * np);
+  }
+  ps.big = rem + r >= np;
+  const int t0 = j * q + ps.bb;
+  ps.tok0 = t0 * kTile;
+  ps.tok1 = vmin(kv, (t0 + q + (ps.big ? 1 : 0)) * kTile);
+  return ps;
+}
+
+// The plan of a batch of at most kWavePlanSeqs sequences (decode_plan_kernel
+// for larger ones): the same rules and outputs, with every step a wave
+// operation (the 1024-thread group of decode_plan_kernel spends 1.0-1.4 us
+// on each of its five barrier-bound phases at c2). Each wave works the
+// plan out by itself (wave_plan_lengths, wave_plan_rest), so no wave
+// waits for another.
+//   IDS = false: one work group; its waves write the entries of pieces
+//     j / rep = wave (mod waves), rep lanes per sequence, and
+//     decode_ids_kernel follows with the id lists.
+//   IDS = true (a table of at most kFusedTableEntries entries): work group
+//     0 writes the status, zeroes the counters and marks unused slots;
+//     work group 1 checks every table entry the lengths use (from the
+//     lengths alone) and writes the status's bad-entry count; wave w of
+//     work group g >= 2 takes slot 4 (g - 2) + w, finds its piece from the
+//     positions (the inverse of the deal or the natural order) and writes
+//     its entry and id list. Plan and ids are then one launch.
+template <typename KV, typename BT, bool IDS>
+__global__ __launch_bounds__(64 * kWavePlanWaves) void decode_plan_wave_kernel(PlanArgs a) {
+  __shared__ int s_count[kWavePlanWaves][64];  // size buckets in use, one copy per wave
+  __shared__ int64_t s_bad[kWavePlanWaves];
+  constexpr int kThreads = 64 * kWavePlanWaves;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const BT* btp = static_cast<const BT*>(a.block_table);
+  const int64_t bs = int64_t(1) << a.bs_log2;
+  const int hkv = a.num_kv_heads;
+  WavePlan p;
+  wave_plan_lengths<KV>(a, p, lane);
+  // The table check counts the entries the lengths use (rows b < num_seqs,
+  // entries j < ceil(kv_b / bs), kv_b = 0 for an unusable length) outside
+  // the pool: rep lanes per row, lane l taking row l / rep and its entries
+  // j = l % rep + rep * (wave + waves * i), kCheckBatch loads in flight at
+  // a time. It needs the lengths only: with IDS work group 1 runs it and
+  // writes status[MV_PLAN_BAD_BLOCK] alone; without, it runs when there
+  // are no lists (decode_ids_kernel counts otherwise).
+  auto table_check = [&]() __attribute__((always_inline)) -> int64_t {
+    constexpr int kCheckBatch = 16;
+    const int nblk = static_cast<int>((p.kv + bs - 1) / bs);
+    const int rep = vmax(1, kWavePlanSeqs / a.num_seqs);
+    const int row = lane / rep < a.num_seqs ? lane / rep : -1;
+    const int n = __shfl(nblk, row < 0 ? 0 : row);
+    const int stride = rep * kWavePlanWaves;
+    const int first = lane - (lane / rep) * rep + rep * wave;
+    const BT* src = btp + static_cast<int64_t>(row < 0 ? 0 : row) * a.bt_stride;
+    const int most = wave_max(row >= 0 ? n : 0);
+    int64_t bad = 0;
+    for (int j0 = first; j0 - first < most; j0 += kCheckBatch * stride) {  // uniform trips
+      int64_t blk[kCheckBatch];
+#pragma unroll
+      for (int u = 0; u < kCheckBatch; ++u) {
+        const int j = j0 + u * stride;
+        blk[u] = row >= 0 && j < n ? static_cast<int64_t>(src[j]) : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kCheckBatch; ++u) bad += blk[u] < 0 || blk[u] >= a.num_blocks;
+    }
+    bad = wave_sum64(bad);
+    if (lane == 0) s_bad[wave] = bad;
+    __syncthreads();
+    bad = 0;
+#pragma unroll
+    for (int w = 0; w < kWavePlanWaves; ++w) bad += s_bad[w];
+    return bad;
+  };
+  if (IDS && blockIdx.x == 1) {
+    const int64_t bad = a.num_seqs > 0 ? table_check() : 0;
+    if (threadIdx.x == 0) a.status[MV_PLAN_BAD_BLOCK] = static_cast<int32_t>(vmin<int64_t>(bad, INT_MAX));
+    return;
+  }
+  wave_plan_rest(a, p, s_count[wave], lane, !(IDS && blockIdx.x == 0));
+  const bool wide = p.most_tiles >= (1 << 16);  // j * r may exceed 32 bits
+
+  if (IDS && blockIdx.x > 1) {
+    // ---- one slot per wave: its piece, entry and id list
+    const int64_t slot = static_cast<int64_t>(blockIdx.x - 2) * kWavePlanWaves + wave;
+    if (!p.listed || slot >= p.num_groups || slot >= a.work_cap) return;
+    int b, j, h;
+    if (p.deal) {
+      const int s32 = static_cast<int>(slot);
+      const int rd = static_cast<int>(static_cast<uint32_t>(s32) / static_cast<uint32_t>(p.cus));
+      const int cs = s32 - rd * p.cus;
+      const int pos = rd * p.cus + (((p.rounds - 1 - rd) & 1) == 0 ? cs : p.cus - 1 - cs);
+      // bucket k holding pos (lane = bucket), then the sequence whose
+      // groups of k hold it (lane = sequence)
+      const int k = __builtin_ctzll(__builtin_amdgcn_ballot_w64(p.start <= pos && pos < p.start + p.cnt));
+      const bool in_a = p.ka == k && p.pre_a <= pos && pos < p.pre_a + p.na;
+      const bool in_b = p.kb == k && p.pre_b <= pos && pos < p.pre_b + p.nb;
+      b = __builtin_ctzll(__builtin_amdgcn_ballot_w64(in_a || in_b));
+      const bool big_b = __builtin_amdgcn_ballot_w64(in_a) != 0;  // in the (q + 1)-tile bucket
+      const int idx = pos - __builtin_amdgcn_readlane(big_b ? p.pre_a : p.pre_b, b);
+      const int np = __builtin_amdgcn_readlane(p.np, b), r = __builtin_amdgcn_readlane(p.r, b);
+      const bool same = __builtin_amdgcn_readlane(p.ka, b) == __builtin_amdgcn_readlane(p.kb, b);
+      const int i = idx / hkv;
+      h = idx - i * hkv;
+      // the i-th piece of b in its bucket: all pieces when both sizes share
+      // it; else the i-th (q + 1)-tile piece, ceil((i + 1) np / r) - 1, or
+      // the i-th q-tile piece, floor(i np / (np - r))
+      if (same) j = i;
+      else if (big_b) j = static_cast<int>(div_nonneg(static_cast<int64_t>(i + 1) * np + r - 1, r)) - 1;
+      else j = static_cast<int>(div_nonneg(static_cast<int64_t>(i) * np, np - r));
+    } else {
+      const int item = static_cast<int>(slot / hkv);
+      h = static_cast<int>(slot - static_cast<int64_t>(item) * hkv);
+      b = __builtin_ctzll(__builtin_amdgcn_ballot_w64(p.mine && p.item0 <= item && item < p.item0 + p.np));
+      j = item - __builtin_amdgcn_readlane(p.item0, b);
+    }
+    const int kv = __builtin_amdgcn_readlane(p.kv, b), np = __builtin_amdgcn_readlane(p.np, b);
+    const PieceSpan ps = piece_span(kv, np, __builtin_amdgcn_readlane(p.q, b), __builtin_amdgcn_readlane(p.r, b),
+                                    j, wide);
+    const int4 w0 = make_int4(b, h, j, np);
+    const int4 w1 = make_int4(ps.tok0, ps.tok1, 0, 0);
+    if (lane == 0) {
+      int4* w = reinterpret_cast<int4*>(a.work + 8 * slot);
+      w[0] = w0;
+      w[1] = w1;
+    }
+    write_slot_ids(btp, a.bt_stride, a.num_seqs, a.max_blocks, a.num_blocks, a.bs_log2, p.per_item, a.ids, slot,
+                   w0, w1, lane);
+    return;
+  }
+
+  if (!IDS && p.listed && a.num_seqs > 0) {
+    // ---- 4. entries: rep lanes per sequence, lane l taking sequence l /
+    // rep and its pieces j = l % rep + rep * (wave + waves * i)
+    const int rep = vmax(1, kWavePlanSeqs / a.num_seqs);
+    const int sb = lane / rep, m = lane - sb * rep;
+    const bool act = sb < a.num_seqs;
+    const int src = act ? sb : 0;
+    const int kv_s = __shfl(p.kv, src), np_s = __shfl(p.np, src), q_s = __shfl(p.q, src), r_s = __shfl(p.r, src);
+    const int ka_s = __shfl(p.ka, src), kb_s = __shfl(p.kb, src);
+    const int pa_s = __shfl(p.pre_a, src), pb_s = __shfl(p.pre_b, src), item0_s = __shfl(p.item0, src);
+    const int cus = p.cus;
+    const int stride = rep * kWavePlanWaves;
+    const int trips = (p.max_parts + stride - 1) / stride;
+    for (int it = 0; it < trips; ++it) {  // wave-uniform trip count
+      const int j = m + rep * (wave + kWavePlanWaves * it);
+      if (!act || j >= np_s) continue;
+      const PieceSpan ps = piece_span(kv_s, np_s, q_s, r_s, j, wide);
+      // the kv heads' groups of piece j take consecutive positions
+      const int pos0 = ka_s == kb_s ? pa_s + j * hkv : ps.big ? pa_s + ps.bb * hkv : pb_s + (j - ps.bb) * hkv;
+      int rd = p.deal ? static_cast<int>(static_cast<uint32_t>(pos0) / static_cast<uint32_t>(cus)) : 0;
+      int c = pos0 - rd * cus;
+      for (int h = 0; h < hkv; ++h, ++c) {
+        int64_t slot;
+        if (p.deal) {
+          if (c == cus) {
+            ++rd;
+            c = 0;
+          }
+          const bool forward = ((p.rounds - 1 - rd) & 1) == 0;
+          slot = static_cast<int64_t>(rd) * cus + (forward ? c : cus - 1 - c);
+        } else {
+          slot = static_cast<int64_t>(item0_s + j) * hkv + h;
+        }
+        if (slot < a.work_cap) {
+          int4* w = reinterpret_cast<int4*>(a.work + 8 * slot);
+          w[0] = make_int4(sb, h, j, np_s);
+          w[1] = make_int4(ps.tok0, ps.tok1, 0, 0);
+        }
+      }
+    }
+  }
+
+  // ---- 5. unused slots (a launch of fixed size, or lists that do not
+  // fit: then every slot), the merge counters, the table check without
+  // lists (IDS: work group 1) and the status
+  if (p.fixed || !p.listed) {
+    for (int64_t slot = (p.listed ? p.used_groups : 0) + threadIdx.x; slot < a.work_cap; slot += kThreads) {
+      int4* w = reinterpret_cast<int4*>(a.work + 8 * slot);
+      w[0] = make_int4(-1, 0, 0, 0);
+      w[1] = make_int4(0, 0, 0, 0);
+    }
+  }
+  for (int64_t i = threadIdx.x; i < static_cast<int64_t>(a.num_seqs) * hkv; i += kThreads) a.counters[i] = 0;
+  const int64_t bad = !IDS && !p.listed && a.num_seqs > 0 ? table_check() : 0;
+  if (threadIdx.x == 0) {
+    a.status[MV_PLAN_NUM_ITEMS] = static_cast<int32_t>(vmin<int64_t>(p.num_groups, INT_MAX));
+    a.status[MV_PLAN_BAD_KV_LEN] = p.bad_kv;
+    a.status[MV_PLAN_INSUFFICIENT] = p.short_table;
+    if (!IDS) a.status[MV_PLAN_BAD_BLOCK] = static_cast<int32_t>(vmin<int64_t>(bad, INT_MAX));
+    a.status[MV_PLAN_MAX_PARTS] = p.max_parts;
+    a.status[MV_PLAN_MIN_KV_LEN] = a.num_seqs > 0 ? p.least_kv : 0;
+    a.status[MV_PLAN_PARTITION_TOKENS] = p.part_tokens;
+    a.status[MV_PLAN_IDS_PER_ITEM] = p.listed ? p.per_item : -1;
+  }
 }
 
 // ------------------------------------------------------------- dispatch ---
@@ -1527,7 +1912,35 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
   a.counters = counters;
   a.status = status;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (kv_len_is_i64) {
+  // slots the plan can fill (the same bound as a launch of fixed size)
+  const int64_t slots = std::min<int64_t>(
+      work_capacity, plan_bounds(num_seqs, max_blocks, block_size, num_kv_heads, groups_per_cu, cu_count).groups);
+  const bool wave_plan = num_seqs <= kWavePlanSeqs;
+  // plan and id lists in one launch: a small table (work group 0 checks all
+  // of it) and lists to write; one wave per slot after work group 0
+  const bool fused = wave_plan && num_seqs > 0 && block_ids_capacity > 0 &&
+                     static_cast<int64_t>(num_seqs) * max_blocks <= kFusedTableEntries &&
+                     slots <= kFusedSlots;
+  if (fused) {
+    const unsigned grid = 2 + static_cast<unsigned>((slots + kWavePlanWaves - 1) / kWavePlanWaves);
+    if (kv_len_is_i64) {
+      if (bt_is_i64) decode_plan_wave_kernel<int64_t, int64_t, true><<<grid, 64 * kWavePlanWaves, 0, s>>>(a);
+      else decode_plan_wave_kernel<int64_t, int32_t, true><<<grid, 64 * kWavePlanWaves, 0, s>>>(a);
+    } else {
+      if (bt_is_i64) decode_plan_wave_kernel<int32_t, int64_t, true><<<grid, 64 * kWavePlanWaves, 0, s>>>(a);
+      else decode_plan_wave_kernel<int32_t, int32_t, true><<<grid, 64 * kWavePlanWaves, 0, s>>>(a);
+    }
+    return check_launch("mv_decode_plan");
+  }
+  if (wave_plan) {
+    if (kv_len_is_i64) {
+      if (bt_is_i64) decode_plan_wave_kernel<int64_t, int64_t, false><<<1, 64 * kWavePlanWaves, 0, s>>>(a);
+      else decode_plan_wave_kernel<int64_t, int32_t, false><<<1, 64 * kWavePlanWaves, 0, s>>>(a);
+    } else {
+      if (bt_is_i64) decode_plan_wave_kernel<int32_t, int64_t, false><<<1, 64 * kWavePlanWaves, 0, s>>>(a);
+      else decode_plan_wave_kernel<int32_t, int32_t, false><<<1, 64 * kWavePlanWaves, 0, s>>>(a);
+    }
+  } else if (kv_len_is_i64) {
     if (bt_is_i64) decode_plan_kernel<int64_t, int64_t><<<1, kPlanThreads, 0, s>>>(a);
     else decode_plan_kernel<int64_t, int32_t><<<1, kPlanThreads, 0, s>>>(a);
   } else {
@@ -1547,12 +1960,8 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
     d.status = status;
     d.num_blocks = num_blocks;
     d.bs_log2 = a.bs_log2;
-    // one wave per slot the plan can fill (the same bound as a launch of
-    // fixed size), in one pass up to 4096 work groups
+    // one wave per slot the plan can fill, in one pass up to 4096 work groups
     constexpr int64_t kSlotsPerGroup = kIdsThreads / 64;
-    const int64_t slots = std::min<int64_t>(
-        work_capacity,
-        plan_bounds(num_seqs, max_blocks, block_size, num_kv_heads, groups_per_cu, cu_count).groups);
     const int grid = static_cast<int>(std::min<int64_t>(
         4096, std::max<int64_t>(1, (slots + kSlotsPerGroup - 1) / kSlotsPerGroup)));
     if (bt_is_i64) decode_ids_kernel<int64_t><<<grid, kIdsThreads, 0, s>>>(d);

@@ -185,6 +185,54 @@ def test_bad_entry_in_a_second_id_pass_raises():
         hip_decode_attention(q, kc, kc, bt, kv, 1)
 
 
+def _plan_lists(bt, kv, bs, pool, hkv):
+    plan = plan_decode(bt, kv, bs, pool, DEV, 64, torch.bfloat16, hkv)
+    torch.cuda.synchronize()
+    g = plan.num_groups
+    stride = ((plan.partition_tokens + bs - 1) // bs + 1 + 3) // 4 * 4
+    work = plan.work[: 8 * g].view(g, 8).cpu()
+    ids = []
+    for slot, w in enumerate(work.tolist()):
+        span4 = min(stride, ((w[5] - 1) // bs - w[4] // bs + 1 + 3) // 4 * 4)
+        ids.append(plan.block_ids[slot * stride:slot * stride + span4].cpu())
+    return plan, work, ids
+
+
+@pytest.mark.parametrize("hkv,max_kv", [(2, 2048), (16, 100)])
+def test_one_launch_plan_matches_two_launches(hkv, max_kv):
+    """Up to 64 sequences over a table of at most 8192 entries, the plan
+    and the id lists are one launch (decode_plan_wave_kernel with its id
+    groups); the same lengths over a wider table (unused columns of -1)
+    take the plan kernel followed by decode_ids_kernel. Both give the same
+    work list and the same id lists, dealt (2 kv heads, c2-like lengths)
+    and in natural order (16 kv heads: more groups than the resident
+    target); a table entry outside the pool raises on both."""
+    g = torch.Generator().manual_seed(7)
+    n, bs = 64, 16
+    kv = torch.randint(1, max_kv + 1, (n,), generator=g, dtype=torch.int32)
+    width = (max_kv + bs - 1) // bs
+    pad = max(1, 8192 // n + 1 - width)  # the wide table holds over 8192 entries
+    assert n * width <= 8192 < n * (width + pad)
+    pool = n * width + 3
+    bt = torch.randperm(pool, generator=g)[: n * width].view(n, width).to(torch.int32)
+    wide = torch.cat([bt, torch.full((n, pad), -1, dtype=torch.int32)], dim=1)
+    say("plan: one launch against two,", n, "sequences,", hkv, "kv heads")
+    one = _plan_lists(bt.to(DEV), kv.to(DEV), bs, pool, hkv)
+    two = _plan_lists(wide.to(DEV), kv.to(DEV), bs, pool, hkv)
+    assert (one[0].num_groups, one[0].partition_tokens, one[0].max_parts) == \
+        (two[0].num_groups, two[0].partition_tokens, two[0].max_parts)
+    assert torch.equal(one[1], two[1])
+    assert all(torch.equal(x, y) for x, y in zip(one[2], two[2]))
+    dealt = one[0].num_groups <= 2 * _cus()
+    say(f"  groups {one[0].num_groups} P {one[0].partition_tokens} dealt {dealt}")
+    assert dealt == (hkv == 2)
+    for table in (bt, wide):
+        bad = table.clone()
+        bad[5, 0] = pool
+        with pytest.raises(IndexError, match="pool blocks"):
+            plan_decode(bad.to(DEV), kv.to(DEV), bs, pool, DEV, 64, torch.bfloat16, hkv)
+
+
 def test_write_through_dlpack_alias_needs_invalidation():
     """A length written through a DLPack alias leaves the tensor's in-place
     version unchanged, so the step's cached plan is reused as it is;
