@@ -452,7 +452,7 @@ def cpu_baseline(spec, layout, layer, budget_s=8.0):
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "paged_decode_write_kernel_{workload}_traffic.md")
 KERNEL_SOURCES = ("csrc/paged_decode.hip", "csrc/mv_tile.h", "csrc/mv_common.h",
-                  "csrc/mv_coherent.h", "csrc/mv_rope.h")
+                  "csrc/mv_coherent.h", "csrc/mv_rope.h", "csrc/mv_step_check.h")
 COPY_BYTES = 256 << 20
 
 

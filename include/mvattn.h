@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MVATTN_ABI_VERSION 6
+#define MVATTN_ABI_VERSION 7
 
 /* Element types of query / key / value / cache / output. */
 #define MV_DTYPE_F32 0
@@ -260,6 +260,33 @@ int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_
                    int32_t groups_per_cu, int32_t cu_count, int32_t fixed_partition_tokens,
                    int32_t* work_items, int64_t work_capacity, int32_t* block_ids,
                    int64_t block_ids_capacity, int32_t* counters, int32_t* status, void* stream);
+
+/*
+ * mv_decode_plan and mv_decode_step_check of one fused decode step
+ * (mv_paged_decode_write), enqueued together: the arguments of the first
+ * (kv_len ... status, the plan's words) and then those of the second that
+ * the first does not already give (slot_mapping, positions ... status as
+ * step_status, workspace as check_workspace), with the same meaning and
+ * the same results, errors and outputs as the two calls in that order.
+ * It replaces what those two replace in the reference: the metadata
+ * checks of `triton_decode_attention` (paged_attention_gpu.py:294-300) and
+ * `gather_paged_kv` (cache_read.py:60-67), and the slot checks of
+ * `triton_cache_write` (:126-135). With at most 64 sequences over a table
+ * of at most 8192 entries the plan, its block-id lists and the step check
+ * are one launch (and the shared-read scan a second); otherwise it is the
+ * launches of the two calls. Never synchronises.
+ */
+int mv_decode_plan_step_check(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
+                              int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs,
+                              int32_t max_blocks, int32_t block_size, int64_t num_blocks,
+                              int32_t num_kv_heads, int32_t groups_per_cu, int32_t cu_count,
+                              int32_t fixed_partition_tokens, int32_t* work_items,
+                              int64_t work_capacity, int32_t* block_ids, int64_t block_ids_capacity,
+                              int32_t* counters, int32_t* status, const int64_t* slot_mapping,
+                              const int64_t* positions, const void* cos_table, const void* sin_table,
+                              int64_t table_stride, int64_t max_positions, int32_t head_dim,
+                              int32_t dtype, void* cos_rows, void* sin_rows, int32_t* step_status,
+                              void* check_workspace, size_t check_workspace_bytes, void* stream);
 
 /*
  * Sizes of a decode launch of fixed size, for batches of at most num_seqs

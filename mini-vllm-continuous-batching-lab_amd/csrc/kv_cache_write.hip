@@ -12,6 +12,7 @@
 // and V chunks in the same grid. It is a bitwise copy, so the result is
 // bit-identical to the reference scatter for every dtype.
 #include "mv_common.h"
+#include "mv_step_check.h"
 
 namespace mv {
 namespace {
@@ -97,40 +98,11 @@ __global__ __launch_bounds__(256) void kv_cache_write_kernel(WriteArgs a) {
 // least twice as many entries as slots, so every probe sequence ends.
 // Up to kSlotsLdsMax slots one work group does it in LDS; beyond, a grid
 // does it in a workspace table cleared by a fill kernel first.
-constexpr int kSlotCountShift = 44;
-constexpr uint64_t kSlotKeyMask = (uint64_t(1) << kSlotCountShift) - 1;
 constexpr int kSlotsLdsMax = 4096;
 constexpr int kSlotsLdsEntries = 2 * kSlotsLdsMax;  // 64 KiB of LDS
 constexpr int kSlotsCheckThreads = 1024;
 constexpr int kSlotsGridThreads = 256;
 constexpr int64_t kSlotsMax = (int64_t(1) << (64 - kSlotCountShift)) - 1;  // count field
-
-__device__ __forceinline__ uint32_t hash64(uint64_t k) {
-  return static_cast<uint32_t>((k * 0x9E3779B97F4A7C15ull) >> 29);
-}
-
-// Inserts `key` (slot + 1); returns the number of equal keys inserted
-// before it. `table` is LDS or global memory; the atomics are the
-// address space's own.
-template <typename Word>
-__device__ __forceinline__ uint64_t count_insert(Word* table, uint32_t hmask, uint64_t key) {
-  uint32_t h = hash64(key) & hmask;
-  const unsigned long long first = (1ull << kSlotCountShift) | key;
-  while (true) {
-    const unsigned long long old = atomicCAS(reinterpret_cast<unsigned long long*>(&table[h]), 0ull, first);
-    if (old == 0) return 0;
-    if ((old & kSlotKeyMask) == key) {
-      const unsigned long long prev =
-          atomicAdd(reinterpret_cast<unsigned long long*>(&table[h]), 1ull << kSlotCountShift);
-      return prev >> kSlotCountShift;
-    }
-    h = (h + 1) & hmask;
-  }
-}
-
-__device__ __forceinline__ int32_t saturate_i32(uint64_t v) {
-  return v > static_cast<uint64_t>(INT_MAX) ? INT_MAX : static_cast<int32_t>(v);
-}
 
 __global__ __launch_bounds__(kSlotsCheckThreads) void slots_check_lds_kernel(
     const int64_t* slots, int32_t n, int64_t total_slots, uint32_t hmask, int32_t* status) {
@@ -201,120 +173,10 @@ __global__ __launch_bounds__(kSlotsGridThreads) void slots_check_grid_kernel(
   }
 }
 
-inline uint32_t pow2_at_least(int64_t v) {
-  uint32_t h = 1;
-  while (h < v) h <<= 1;
-  return h;
-}
-
-// ---------------------------------------------------------------------------
-// Fused decode + KV write precondition (mv_paged_decode_write).
-//
-// Phase 1 (one work group): counts the sequences whose slot is neither -1
-// nor the table position of their own token kv_len - 1 (status[0]), and
-// puts every other writer b -- slot s_b in block k_b at offset o_b -- into
-// a hash table keyed by k_b + 1 whose value is the minimum of
-// (o_b << 12) | b over the writers of that block, as 64-bit words
-// ((k_b + 1) << 32) | value (0: empty). Built in LDS, then stored to the
-// workspace.
-// Phase 2 (a grid of (sequence c, 256 table entries)): an entry j that c
-// attends (j < ceil(kv_c / bs)) whose block is in the table is counted
-// (status[1]) when the block's smallest written offset lies below c's
-// limit in that block, min(bs, kv_c - j bs), unless that writer is c itself
-// at its own last position. That is exact: a write at offset o is read
-// through entry (c, j) iff o < the limit, and if the smallest-offset writer
-// is c's own last position, every other writer of the block is either not
-// attended by c or writes c's very slot (a duplicate slot). Phase 2 does
-// not count c's own entry in that last case; phase 1 does, once per block
-// whose smallest written offset has two or more writers, so that status[1]
-// is exactly the number of attended entries (c, j) through which c reads a
-// slot that some writer other than c-at-its-last-entry writes.
-constexpr int kWriteCheckThreads = 1024;
-constexpr int kWriteCheckEntries = 2 * MV_WRITE_CHECK_MAX_SEQS;  // 64 KiB of LDS
-constexpr int kWriterSeqBits = 12;  // MV_WRITE_CHECK_MAX_SEQS = 1 << 12
-constexpr int kWriterMaxBlockLog2 = 20;  // offsets < 2^20 fit the value's upper bits
-static_assert(kWriterMaxBlockLog2 + kWriterSeqBits <= 32, "writer value bits");
-constexpr int kSharedCheckThreads = 256;
-static_assert(MV_WRITE_CHECK_MAX_SEQS == (1 << kWriterSeqBits), "writer index bits");
-
-__device__ __forceinline__ uint32_t hash32(uint32_t k) { return (k * 0x9E3779B1u) >> 7; }
-
-// Phase 1 for one work group of kWriteCheckThreads threads (called by
-// every thread): builds the writers' table in `table` (LDS, hmask + 1
-// entries) and stores it to `writers`; returns, in every thread, the
-// own-slot failures and the blocks whose smallest written offset has two or
-// more writers. `dup_blocks` (LDS, kWriteCheckEntries / 32 words) and
-// `s_red` (LDS, 2 ints) are scratch.
-template <typename KV, typename BT>
-__device__ __forceinline__ int2 build_writers(const int64_t* slots, const BT* bt, int64_t bt_stride,
-                                              const KV* kv_len, int32_t num_seqs, int32_t max_blocks,
-                                              int32_t bs_log2, uint64_t* writers, uint32_t hmask,
-                                              uint64_t* table, uint32_t* dup_blocks, int* s_red) {
-  constexpr int kMine = MV_WRITE_CHECK_MAX_SEQS / kWriteCheckThreads;
-  for (uint32_t i = threadIdx.x; i <= hmask; i += kWriteCheckThreads) table[i] = 0;
-  for (uint32_t i = threadIdx.x; i < kWriteCheckEntries / 32; i += kWriteCheckThreads) dup_blocks[i] = 0;
-  if (threadIdx.x == 0) { s_red[0] = 0; s_red[1] = 0; }
-  __syncthreads();
-  int bad = 0;
-  uint64_t mine[kMine];  // this thread's writers' words (0: none)
-#pragma unroll
-  for (int i = 0; i < kMine; ++i) mine[i] = 0;
-#pragma unroll
-  for (int i = 0; i < kMine; ++i) {
-    const int b = static_cast<int>(threadIdx.x) + i * kWriteCheckThreads;
-    if (b >= num_seqs) continue;
-    const int64_t s = slots[b];
-    if (s == -1) continue;
-    const int64_t kv = static_cast<int64_t>(kv_len[b]);
-    const int64_t e = (kv - 1) >> bs_log2;
-    const int64_t off = (kv - 1) & ((int64_t(1) << bs_log2) - 1);
-    bool ok = kv >= 1 && e < max_blocks;
-    int64_t blk = -1;
-    if (ok) {
-      blk = static_cast<int64_t>(bt[b * bt_stride + e]);
-      // ids that cannot be keyed lie far outside any pool
-      ok = blk >= 0 && blk < int64_t(0xFFFFFFFF) && s == (blk << bs_log2) + off;
-    }
-    if (!ok) { ++bad; continue; }
-    const uint64_t key = static_cast<uint64_t>(blk + 1) << 32;
-    const uint64_t word = key | (static_cast<uint64_t>(off) << kWriterSeqBits) | static_cast<uint64_t>(b);
-    mine[i] = word;
-    uint32_t h = hash32(static_cast<uint32_t>(blk + 1)) & hmask;
-    while (true) {
-      const unsigned long long old = atomicCAS(reinterpret_cast<unsigned long long*>(&table[h]), 0ull,
-                                               static_cast<unsigned long long>(key | 0xFFFFFFFFull));
-      if (old == 0 || (old & 0xFFFFFFFF00000000ull) == key) {
-        // the same key in the high bits: the word's minimum is the value's
-        atomicMin(reinterpret_cast<unsigned long long*>(&table[h]), static_cast<unsigned long long>(word));
-        break;
-      }
-      h = (h + 1) & hmask;
-    }
-  }
-  if (bad) atomicAdd(&s_red[0], bad);
-  __syncthreads();
-  // A writer at its block's smallest written offset that is not the
-  // block's minimum word writes the minimum writer's slot too.
-  constexpr uint64_t kSeqMask = (1u << kWriterSeqBits) - 1;
-#pragma unroll
-  for (int i = 0; i < kMine; ++i) {
-    const uint64_t word = mine[i];
-    if (!word) continue;
-    uint32_t h = hash32(static_cast<uint32_t>(word >> 32)) & hmask;
-    while ((table[h] ^ word) >> 32) h = (h + 1) & hmask;  // present: inserted above
-    const uint64_t least = table[h];
-    if (((least ^ word) & 0xFFFFFFFFull) >> kWriterSeqBits == 0 && (least & kSeqMask) != (word & kSeqMask))
-      atomicOr(&dup_blocks[h >> 5], 1u << (h & 31));
-  }
-  __syncthreads();
-  int dups = 0;
-  for (uint32_t i = threadIdx.x; i < kWriteCheckEntries / 32; i += kWriteCheckThreads)
-    dups += __popc(dup_blocks[i]);
-  if (dups) atomicAdd(&s_red[1], dups);
-  for (uint32_t i = threadIdx.x; i <= hmask; i += kWriteCheckThreads) writers[i] = table[i];
-  __syncthreads();
-  return make_int2(s_red[0], s_red[1]);
-}
+// The fused-write precondition (phases 1 and 2) and the step check are
+// described, and phase 1 and the step check's body defined, in
+// mv_step_check.h (the decode plan's one-launch form runs the step check
+// too).
 
 template <typename KV, typename BT>
 __global__ __launch_bounds__(kWriteCheckThreads) void decode_write_check_kernel(
@@ -323,34 +185,13 @@ __global__ __launch_bounds__(kWriteCheckThreads) void decode_write_check_kernel(
   __shared__ uint64_t table[kWriteCheckEntries];
   __shared__ uint32_t dup_blocks[kWriteCheckEntries / 32];
   __shared__ int s_red[2];
-  const int2 r = build_writers(slots, bt, bt_stride, kv_len, num_seqs, max_blocks, bs_log2, writers,
-                               hmask, table, dup_blocks, s_red);
+  const int2 r = build_writers<kWriteCheckThreads, MV_WRITE_CHECK_MAX_SEQS>(
+      slots, bt, bt_stride, kv_len, num_seqs, max_blocks, bs_log2, writers, hmask, table, dup_blocks, s_red);
   if (threadIdx.x == 0) {
     status[MV_WRITE_CHECK_OWN_SLOT] = r.x;
     status[MV_WRITE_CHECK_SHARED] = r.y;
   }
 }
-
-// The fused decode step's checks in one work group (mv_decode_step_check):
-// the slot check of the step's decode slots (as slots_check_lds_kernel),
-// phase 1 of the fused-write check (build_writers), the positions check
-// and the gather of the rotary tables' rows at each position (clamped into
-// the tables; out-of-range positions are counted).
-struct StepCheckArgs {
-  const int64_t* slots;
-  const void* bt;
-  const void* kv_len;
-  const int64_t* positions;  // null: no positions check, no rows
-  const char* cos;
-  const char* sin;
-  char* cos_rows;
-  char* sin_rows;
-  uint64_t* writers;
-  int32_t* status;  // MV_STEP_* words
-  int64_t bt_stride, total_slots, max_positions, table_stride;  // table_stride in bytes
-  int32_t num_seqs, max_blocks, bs_log2, row_bytes;
-  uint32_t slot_hmask, writer_hmask;
-};
 
 template <typename KV, typename BT>
 __global__ __launch_bounds__(kWriteCheckThreads) void decode_step_check_kernel(StepCheckArgs a) {
@@ -358,49 +199,10 @@ __global__ __launch_bounds__(kWriteCheckThreads) void decode_step_check_kernel(S
   __shared__ uint64_t table[kWriteCheckEntries];
   __shared__ uint32_t dup_blocks[kWriteCheckEntries / 32];
   __shared__ int s_red[2];
-  __shared__ int s_bad, s_pos_bad;
+  __shared__ int s_cnt[2];
   __shared__ unsigned long long s_pairs;
-  for (uint32_t i = threadIdx.x; i <= a.slot_hmask; i += kWriteCheckThreads) slot_table[i] = 0;
-  if (threadIdx.x == 0) { s_bad = 0; s_pairs = 0; s_pos_bad = 0; }
-  // rotary rows: chunk i of 16 bytes of row b of table tb (the loads of
-  // every chunk go out before any other work waits on memory)
-  int pos_bad = 0;
-  if (a.positions) {
-    const int cpr = a.row_bytes / 16;
-    const int n = 2 * a.num_seqs * cpr;
-    for (int i = threadIdx.x; i < n; i += kWriteCheckThreads) {
-      const int tb = i / (a.num_seqs * cpr);
-      const int r = i - tb * a.num_seqs * cpr;
-      const int b = r / cpr, c = r - b * cpr;
-      const int64_t p = a.positions[b];
-      if (tb == 0 && c == 0) pos_bad += p < 0 || p >= a.max_positions;
-      const int64_t row = p < 0 ? 0 : (p >= a.max_positions ? a.max_positions - 1 : p);
-      const uint4 v = *reinterpret_cast<const uint4*>((tb ? a.sin : a.cos) + row * a.table_stride + c * 16);
-      *reinterpret_cast<uint4*>((tb ? a.sin_rows : a.cos_rows) + static_cast<int64_t>(b) * a.row_bytes + c * 16) = v;
-    }
-  }
-  __syncthreads();
-  int bad = 0;
-  uint64_t pairs = 0;
-  for (int x = threadIdx.x; x < a.num_seqs; x += kWriteCheckThreads) {
-    const int64_t s = a.slots[x];
-    if (s == -1) continue;
-    if (s < 0 || s >= a.total_slots) { ++bad; continue; }
-    pairs += count_insert(slot_table, a.slot_hmask, static_cast<uint64_t>(s) + 1);
-  }
-  if (bad) atomicAdd(&s_bad, bad);
-  if (pairs) atomicAdd(&s_pairs, static_cast<unsigned long long>(pairs));
-  if (pos_bad) atomicAdd(&s_pos_bad, pos_bad);
-  const int2 r = build_writers(a.slots, static_cast<const BT*>(a.bt), a.bt_stride,
-                               static_cast<const KV*>(a.kv_len), a.num_seqs, a.max_blocks, a.bs_log2,
-                               a.writers, a.writer_hmask, table, dup_blocks, s_red);
-  if (threadIdx.x == 0) {  // build_writers ends on a barrier: the counts are complete
-    a.status[MV_STEP_SLOTS_OUT_OF_RANGE] = s_bad;
-    a.status[MV_STEP_SLOTS_DUPLICATES] = saturate_i32(s_pairs);
-    a.status[MV_STEP_WRITE_OWN_SLOT] = r.x;
-    a.status[MV_STEP_WRITE_SHARED] = r.y;
-    a.status[MV_STEP_POSITIONS] = s_pos_bad;
-  }
+  step_check_body<KV, BT, kWriteCheckThreads, MV_WRITE_CHECK_MAX_SEQS>(a, slot_table, table, dup_blocks, s_red,
+                                                                       s_cnt, &s_pairs);
 }
 
 template <typename KV, typename BT>
@@ -623,6 +425,111 @@ extern "C" int mv_decode_write_check(const int64_t* slot_mapping, const void* bl
   return check_launch("mv_decode_write_check");
 }
 
+namespace mv {
+
+int step_check_prepare(const char* who, const int64_t* slot_mapping, const void* block_table,
+                       int64_t bt_stride, const void* kv_len, int32_t num_seqs, int32_t max_blocks,
+                       int32_t block_size, int64_t num_blocks, const int64_t* positions,
+                       const void* cos_table, const void* sin_table, int64_t table_stride,
+                       int64_t max_positions, int32_t head_dim, int32_t dtype, void* cos_rows,
+                       void* sin_rows, int32_t* status, void* workspace, size_t workspace_bytes,
+                       StepCheckArgs* a) {
+  static_assert(MV_STEP_WRITE_SHARED - MV_STEP_WRITE_OWN_SLOT ==
+                    MV_WRITE_CHECK_SHARED - MV_WRITE_CHECK_OWN_SLOT,
+                "phase 2 adds to the step's shared-read word");
+  if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "%s: null status", who);
+  if (num_seqs < 0 || max_blocks < 0 || num_blocks < 0)
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: negative size", who);
+  if (num_seqs > MV_WRITE_CHECK_MAX_SEQS)
+    return fail(MV_ERR_UNSUPPORTED, "%s: %d sequences (at most %d)", who, num_seqs, MV_WRITE_CHECK_MAX_SEQS);
+  if (!is_pow2(block_size) || ilog2_exact(block_size) > kWriterMaxBlockLog2)
+    return fail(MV_ERR_UNSUPPORTED, "%s: block_size %d is not a power of 2 up to 2^%d", who, block_size,
+                kWriterMaxBlockLog2);
+  const int64_t total_slots = num_blocks * block_size;
+  if (total_slots >= static_cast<int64_t>(kSlotKeyMask))
+    return fail(MV_ERR_UNSUPPORTED, "%s: %lld slots in the pool (fewer than 2^44)", who,
+                (long long)total_slots);
+  if (num_seqs > 0 && (!slot_mapping || !kv_len || (max_blocks > 0 && !block_table)))
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: null pointer", who);
+  const int eb = dtype_bytes(dtype);
+  if (positions) {
+    if (eb == 0 || head_dim <= 0 || (head_dim * eb) % 16 || max_positions <= 0 || !cos_table ||
+        !sin_table || !cos_rows || !sin_rows)
+      return fail(MV_ERR_INVALID_ARGUMENT,
+                  "%s: rotary rows need the tables, the rows, a dtype and a head_dim of whole "
+                  "16-byte pieces", who);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(cos_table) | reinterpret_cast<uintptr_t>(sin_table) |
+                         reinterpret_cast<uintptr_t>(cos_rows) | reinterpret_cast<uintptr_t>(sin_rows) |
+                         static_cast<uintptr_t>(table_stride * eb);
+    if (al % 16) return fail(MV_ERR_INVALID_ARGUMENT, "%s: rotary tables or rows not 16-byte aligned", who);
+    if (table_stride < head_dim)
+      return fail(MV_ERR_INVALID_ARGUMENT, "%s: table stride %lld < head_dim %d", who,
+                  (long long)table_stride, head_dim);
+  }
+  const size_t need = mv_decode_write_check_workspace_bytes(num_seqs);
+  if (!workspace || workspace_bytes < need)
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: %d sequences need a %zu-byte workspace (got %zu)", who,
+                num_seqs, need, workspace ? workspace_bytes : size_t(0));
+  if (reinterpret_cast<uintptr_t>(workspace) % 8)
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: workspace not 8-byte aligned", who);
+  const int mb = block_table ? max_blocks : 0;
+  if ((mb + kSharedCheckThreads - 1) / kSharedCheckThreads > 65535)
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: %d table columns is too many", who, mb);
+  a->slots = slot_mapping;
+  a->bt = block_table;
+  a->kv_len = kv_len;
+  a->positions = positions;
+  a->cos = static_cast<const char*>(cos_table);
+  a->sin = static_cast<const char*>(sin_table);
+  a->cos_rows = static_cast<char*>(cos_rows);
+  a->sin_rows = static_cast<char*>(sin_rows);
+  a->writers = static_cast<uint64_t*>(workspace);
+  a->status = status;
+  a->bt_stride = bt_stride;
+  a->total_slots = total_slots;
+  a->max_positions = max_positions;
+  a->table_stride = table_stride * eb;
+  a->num_seqs = num_seqs;
+  a->max_blocks = mb;
+  a->bs_log2 = ilog2_exact(block_size);
+  a->row_bytes = head_dim * eb;
+  a->slot_hmask = pow2_at_least(std::max<int64_t>(64, 2 * int64_t(num_seqs))) - 1;
+  a->writer_hmask = static_cast<uint32_t>(need / sizeof(uint64_t)) - 1;
+  return MV_OK;
+}
+
+int step_check_scan(const StepCheckArgs& a, int32_t bt_is_i64, int32_t kv_len_is_i64, hipStream_t s) {
+  const unsigned chunks = static_cast<unsigned>((a.max_blocks + kSharedCheckThreads - 1) / kSharedCheckThreads);
+  if (a.num_seqs == 0 || chunks == 0) return MV_OK;
+  const dim3 grid(static_cast<unsigned>(a.num_seqs), chunks);
+#define MV_SCAN(KV, BT)                                                                              \
+  decode_shared_slot_kernel<KV, BT><<<grid, kSharedCheckThreads, 0, s>>>(                            \
+      static_cast<const BT*>(a.bt), a.bt_stride, static_cast<const KV*>(a.kv_len), a.max_blocks,    \
+      a.bs_log2, a.writers, a.writer_hmask, a.status + MV_STEP_WRITE_OWN_SLOT)
+  if (kv_len_is_i64) {
+    if (bt_is_i64) MV_SCAN(int64_t, int64_t);
+    else MV_SCAN(int64_t, int32_t);
+  } else {
+    if (bt_is_i64) MV_SCAN(int32_t, int64_t);
+    else MV_SCAN(int32_t, int32_t);
+  }
+#undef MV_SCAN
+  return MV_OK;
+}
+
+int step_check_launch(const StepCheckArgs& a, int32_t bt_is_i64, int32_t kv_len_is_i64, hipStream_t s) {
+  if (kv_len_is_i64) {
+    if (bt_is_i64) decode_step_check_kernel<int64_t, int64_t><<<1, kWriteCheckThreads, 0, s>>>(a);
+    else decode_step_check_kernel<int64_t, int32_t><<<1, kWriteCheckThreads, 0, s>>>(a);
+  } else {
+    if (bt_is_i64) decode_step_check_kernel<int32_t, int64_t><<<1, kWriteCheckThreads, 0, s>>>(a);
+    else decode_step_check_kernel<int32_t, int32_t><<<1, kWriteCheckThreads, 0, s>>>(a);
+  }
+  return step_check_scan(a, bt_is_i64, kv_len_is_i64, s);
+}
+
+}  // namespace mv
+
 extern "C" int mv_decode_step_check(const int64_t* slot_mapping, const void* block_table,
                                     int32_t bt_is_i64, int64_t bt_stride, const void* kv_len,
                                     int32_t kv_len_is_i64, int32_t num_seqs, int32_t max_blocks,
@@ -633,91 +540,12 @@ extern "C" int mv_decode_step_check(const int64_t* slot_mapping, const void* blo
                                     void* cos_rows, void* sin_rows, int32_t* status,
                                     void* workspace, size_t workspace_bytes, void* stream) {
   using namespace mv;
-  static_assert(MV_STEP_WRITE_SHARED - MV_STEP_WRITE_OWN_SLOT ==
-                    MV_WRITE_CHECK_SHARED - MV_WRITE_CHECK_OWN_SLOT,
-                "phase 2 adds to the step's shared-read word");
-  if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_step_check: null status");
-  if (num_seqs < 0 || max_blocks < 0 || num_blocks < 0)
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_step_check: negative size");
-  if (num_seqs > MV_WRITE_CHECK_MAX_SEQS)
-    return fail(MV_ERR_UNSUPPORTED, "mv_decode_step_check: %d sequences (at most %d)", num_seqs,
-                MV_WRITE_CHECK_MAX_SEQS);
-  if (!is_pow2(block_size) || ilog2_exact(block_size) > kWriterMaxBlockLog2)
-    return fail(MV_ERR_UNSUPPORTED,
-                "mv_decode_step_check: block_size %d is not a power of 2 up to 2^%d", block_size,
-                kWriterMaxBlockLog2);
-  const int64_t total_slots = num_blocks * block_size;
-  if (total_slots >= static_cast<int64_t>(kSlotKeyMask))
-    return fail(MV_ERR_UNSUPPORTED, "mv_decode_step_check: %lld slots in the pool (fewer than 2^44)",
-                (long long)total_slots);
-  if (num_seqs > 0 && (!slot_mapping || !kv_len || (max_blocks > 0 && !block_table)))
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_step_check: null pointer");
-  const int eb = dtype_bytes(dtype);
-  if (positions) {
-    if (eb == 0 || head_dim <= 0 || (head_dim * eb) % 16 || max_positions <= 0 || !cos_table ||
-        !sin_table || !cos_rows || !sin_rows)
-      return fail(MV_ERR_INVALID_ARGUMENT,
-                  "mv_decode_step_check: rotary rows need the tables, the rows, a dtype and a "
-                  "head_dim of whole 16-byte pieces");
-    const uintptr_t al = reinterpret_cast<uintptr_t>(cos_table) | reinterpret_cast<uintptr_t>(sin_table) |
-                         reinterpret_cast<uintptr_t>(cos_rows) | reinterpret_cast<uintptr_t>(sin_rows) |
-                         static_cast<uintptr_t>(table_stride * eb);
-    if (al % 16)
-      return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_step_check: rotary tables or rows not 16-byte aligned");
-    if (table_stride < head_dim)
-      return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_step_check: table stride %lld < head_dim %d",
-                  (long long)table_stride, head_dim);
-  }
-  const size_t need = mv_decode_write_check_workspace_bytes(num_seqs);
-  if (!workspace || workspace_bytes < need)
-    return fail(MV_ERR_INVALID_ARGUMENT,
-                "mv_decode_step_check: %d sequences need a %zu-byte workspace (got %zu)", num_seqs,
-                need, workspace ? workspace_bytes : size_t(0));
-  if (reinterpret_cast<uintptr_t>(workspace) % 8)
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_step_check: workspace not 8-byte aligned");
-  const int mb = block_table ? max_blocks : 0;
-  const unsigned chunks = static_cast<unsigned>((mb + kSharedCheckThreads - 1) / kSharedCheckThreads);
-  if (chunks > 65535)
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_step_check: %d table columns is too many", mb);
   StepCheckArgs a;
-  a.slots = slot_mapping;
-  a.bt = block_table;
-  a.kv_len = kv_len;
-  a.positions = positions;
-  a.cos = static_cast<const char*>(cos_table);
-  a.sin = static_cast<const char*>(sin_table);
-  a.cos_rows = static_cast<char*>(cos_rows);
-  a.sin_rows = static_cast<char*>(sin_rows);
-  a.writers = static_cast<uint64_t*>(workspace);
-  a.status = status;
-  a.bt_stride = bt_stride;
-  a.total_slots = total_slots;
-  a.max_positions = max_positions;
-  a.table_stride = table_stride * eb;
-  a.num_seqs = num_seqs;
-  a.max_blocks = mb;
-  a.bs_log2 = ilog2_exact(block_size);
-  a.row_bytes = head_dim * eb;
-  a.slot_hmask = pow2_at_least(std::max<int64_t>(64, 2 * int64_t(num_seqs))) - 1;
-  a.writer_hmask = static_cast<uint32_t>(need / sizeof(uint64_t)) - 1;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(num_seqs), chunks);
-  const bool scan = num_seqs > 0 && chunks > 0;
-#define MV_STEP_CHECK(KV, BT)                                                                     \
-  do {                                                                                            \
-    decode_step_check_kernel<KV, BT><<<1, kWriteCheckThreads, 0, s>>>(a);                         \
-    if (scan)                                                                                     \
-      decode_shared_slot_kernel<KV, BT><<<grid, kSharedCheckThreads, 0, s>>>(                     \
-          static_cast<const BT*>(block_table), bt_stride, static_cast<const KV*>(kv_len), mb,      \
-          a.bs_log2, a.writers, a.writer_hmask, status + MV_STEP_WRITE_OWN_SLOT);                 \
-  } while (0)
-  if (kv_len_is_i64) {
-    if (bt_is_i64) MV_STEP_CHECK(int64_t, int64_t);
-    else MV_STEP_CHECK(int64_t, int32_t);
-  } else {
-    if (bt_is_i64) MV_STEP_CHECK(int32_t, int64_t);
-    else MV_STEP_CHECK(int32_t, int32_t);
-  }
-#undef MV_STEP_CHECK
+  if (const int rc = step_check_prepare("mv_decode_step_check", slot_mapping, block_table, bt_stride, kv_len,
+                                        num_seqs, max_blocks, block_size, num_blocks, positions, cos_table,
+                                        sin_table, table_stride, max_positions, head_dim, dtype, cos_rows,
+                                        sin_rows, status, workspace, workspace_bytes, &a))
+    return rc;
+  step_check_launch(a, bt_is_i64, kv_len_is_i64, static_cast<hipStream_t>(stream));
   return check_launch("mv_decode_step_check");
 }

@@ -63,6 +63,7 @@
 #include "mv_coherent.h"
 #include "mv_common.h"
 #include "mv_rope.h"
+#include "mv_step_check.h"
 #include "mv_tile.h"
 
 namespace mv {
@@ -1565,12 +1566,16 @@ __device__ inline PieceSpan piece_span(int kv, int np, int q, int r, int j, bool
 //   IDS = true (a table of at most kFusedTableEntries entries): work group
 //     0 writes the status, zeroes the counters and marks unused slots;
 //     work group 1 checks every table entry the lengths use (from the
-//     lengths alone) and writes the status's bad-entry count; wave w of
-//     work group g >= 2 takes slot 4 (g - 2) + w, finds its piece from the
-//     positions (the inverse of the deal or the natural order) and writes
-//     its entry and id list. Plan and ids are then one launch.
-template <typename KV, typename BT, bool IDS>
-__global__ __launch_bounds__(64 * kWavePlanWaves) void decode_plan_wave_kernel(PlanArgs a) {
+//     lengths alone) and writes the status's bad-entry count; with CHECK,
+//     work group 2 runs the fused decode step's checks (step_check_body,
+//     arguments `c`: its own status words and rows, so it shares nothing
+//     with the plan); wave w of the work groups g after those takes slot
+//     4 (g - first) + w, finds its piece from the positions (the inverse of
+//     the deal or the natural order) and writes its entry and id list. Plan,
+//     ids and checks are then one launch.
+template <typename KV, typename BT, bool IDS, bool CHECK>
+__global__ __launch_bounds__(64 * kWavePlanWaves) void decode_plan_wave_kernel(PlanArgs a, StepCheckArgs c) {
+  static_assert(IDS || !CHECK, "the step check rides on the one-launch plan");
   __shared__ int s_count[kWavePlanWaves][64];  // size buckets in use, one copy per wave
   __shared__ int64_t s_bad[kWavePlanWaves];
   constexpr int kThreads = 64 * kWavePlanWaves;
@@ -1579,6 +1584,21 @@ __global__ __launch_bounds__(64 * kWavePlanWaves) void decode_plan_wave_kernel(P
   const BT* btp = static_cast<const BT*>(a.block_table);
   const int64_t bs = int64_t(1) << a.bs_log2;
   const int hkv = a.num_kv_heads;
+  if constexpr (CHECK) {
+    if (blockIdx.x == 2) {
+      // slot and writer tables of at most kWavePlanSeqs sequences: the host
+      // sizes both to pow2(max(64, 2 num_seqs)) <= 128 entries
+      __shared__ uint64_t s_slot_table[2 * kWavePlanSeqs];
+      __shared__ uint64_t s_writers[2 * kWavePlanSeqs];
+      __shared__ uint32_t s_dup[2 * kWavePlanSeqs / 32];
+      __shared__ int s_red[2], s_cnt[2];
+      __shared__ unsigned long long s_pairs;
+      step_check_body<KV, BT, 64 * kWavePlanWaves, kWavePlanSeqs>(c, s_slot_table, s_writers, s_dup, s_red, s_cnt,
+                                                                   &s_pairs);
+      return;
+    }
+  }
+  constexpr unsigned kFirstSlotGroup = CHECK ? 3 : 2;
   WavePlan p;
   wave_plan_lengths<KV>(a, p, lane);
   // The table check counts the entries the lengths use (rows b < num_seqs,
@@ -1625,9 +1645,9 @@ __global__ __launch_bounds__(64 * kWavePlanWaves) void decode_plan_wave_kernel(P
   wave_plan_rest(a, p, s_count[wave], lane, !(IDS && blockIdx.x == 0));
   const bool wide = p.most_tiles >= (1 << 16);  // j * r may exceed 32 bits
 
-  if (IDS && blockIdx.x > 1) {
+  if (IDS && blockIdx.x >= kFirstSlotGroup) {
     // ---- one slot per wave: its piece, entry and id list
-    const int64_t slot = static_cast<int64_t>(blockIdx.x - 2) * kWavePlanWaves + wave;
+    const int64_t slot = static_cast<int64_t>(blockIdx.x - kFirstSlotGroup) * kWavePlanWaves + wave;
     if (!p.listed || slot >= p.num_groups || slot >= a.work_cap) return;
     int b, j, h;
     if (p.deal) {
@@ -1868,6 +1888,134 @@ extern "C" size_t mv_paged_decode_workspace_bytes(int32_t num_seqs, int32_t num_
   return ((o + 255) / 256) * 256 + ml;
 }
 
+namespace mv {
+namespace {
+
+// Validates mv_decode_plan's arguments and fills `a`.
+int plan_prepare(const char* who, const void* kv_len, const void* block_table, int64_t bt_stride,
+                 int32_t num_seqs, int32_t max_blocks, int32_t block_size, int64_t num_blocks,
+                 int32_t num_kv_heads, int32_t groups_per_cu, int32_t cu_count,
+                 int32_t fixed_partition_tokens, int32_t* work_items, int64_t work_capacity,
+                 int32_t* block_ids, int64_t block_ids_capacity, int32_t* counters, int32_t* status,
+                 PlanArgs* a) {
+  if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "%s: null status", who);
+  if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0 || block_ids_capacity < 0 ||
+      num_blocks < 0 || num_kv_heads <= 0)
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: bad sizes", who);
+  if (!is_pow2(block_size))
+    return fail(MV_ERR_UNSUPPORTED, "%s: block_size %d is not a power of 2", who, block_size);
+  if (num_seqs > 0 && (!kv_len || !counters || (max_blocks > 0 && !block_table)))
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: null pointer", who);
+  if ((work_capacity > 0 && !work_items) || (block_ids_capacity > 0 && !block_ids))
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: null work list", who);
+  const int64_t ids_need =
+      mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, work_capacity);
+  if (block_ids_capacity < ids_need)
+    return fail(MV_ERR_INVALID_ARGUMENT, "%s: block_ids capacity %lld < %lld", who,
+                static_cast<long long>(block_ids_capacity), static_cast<long long>(ids_need));
+  a->kv_len = kv_len;
+  a->block_table = block_table;
+  a->bt_stride = bt_stride;
+  a->num_seqs = num_seqs;
+  a->max_blocks = max_blocks;
+  a->bs_log2 = ilog2_exact(block_size);
+  a->num_kv_heads = num_kv_heads;
+  a->groups_per_cu = groups_per_cu;
+  a->cu_count = cu_count;
+  a->fixed_part_tokens = fixed_partition_tokens;
+  a->num_blocks = num_blocks;
+  a->work = work_items;
+  a->work_cap = work_capacity;
+  a->ids = block_ids;
+  a->ids_cap = block_ids_capacity;
+  a->counters = counters;
+  a->status = status;
+  return MV_OK;
+}
+
+template <typename KV, typename BT, bool IDS, bool CHECK>
+void launch_wave_plan(unsigned grid, const PlanArgs& a, const StepCheckArgs& c, hipStream_t s) {
+  decode_plan_wave_kernel<KV, BT, IDS, CHECK><<<grid, 64 * kWavePlanWaves, 0, s>>>(a, c);
+}
+
+template <bool IDS, bool CHECK>
+void launch_wave_plan(unsigned grid, int32_t kv_len_is_i64, int32_t bt_is_i64, const PlanArgs& a,
+                      const StepCheckArgs& c, hipStream_t s) {
+  if (kv_len_is_i64) {
+    if (bt_is_i64) launch_wave_plan<int64_t, int64_t, IDS, CHECK>(grid, a, c, s);
+    else launch_wave_plan<int64_t, int32_t, IDS, CHECK>(grid, a, c, s);
+  } else {
+    if (bt_is_i64) launch_wave_plan<int32_t, int64_t, IDS, CHECK>(grid, a, c, s);
+    else launch_wave_plan<int32_t, int32_t, IDS, CHECK>(grid, a, c, s);
+  }
+}
+
+// Enqueues the plan of `a` and its id lists; with `chk` (fused decode step
+// checks, arguments validated) the step check and its shared-read scan too.
+// Up to kWavePlanSeqs sequences over a table of at most kFusedTableEntries
+// entries the plan, the id lists and the step check are one launch.
+int plan_enqueue(const char* who, const PlanArgs& a, int32_t kv_len_is_i64, int32_t bt_is_i64,
+                 int32_t block_size, const StepCheckArgs* chk, hipStream_t s) {
+  // slots the plan can fill (the same bound as a launch of fixed size)
+  const int64_t slots = std::min<int64_t>(
+      a.work_cap, plan_bounds(a.num_seqs, a.max_blocks, block_size, a.num_kv_heads, a.groups_per_cu, a.cu_count)
+                      .groups);
+  const bool wave_plan = a.num_seqs <= kWavePlanSeqs;
+  // plan and id lists in one launch: a small table (work group 1 checks all
+  // of it) and lists to write; one wave per slot after the first groups
+  const bool fused = wave_plan && a.num_seqs > 0 && a.ids_cap > 0 &&
+                     static_cast<int64_t>(a.num_seqs) * a.max_blocks <= kFusedTableEntries &&
+                     slots <= kFusedSlots;
+  StepCheckArgs none{};
+  if (fused) {
+    // the step check's work group holds tables of pow2(max(64, 2 num_seqs))
+    // <= 2 kWavePlanSeqs entries
+    const bool with_check = chk && chk->slot_hmask < 2 * kWavePlanSeqs && chk->writer_hmask < 2 * kWavePlanSeqs;
+    const unsigned first = with_check ? 3 : 2;
+    const unsigned grid = first + static_cast<unsigned>((slots + kWavePlanWaves - 1) / kWavePlanWaves);
+    if (with_check) launch_wave_plan<true, true>(grid, kv_len_is_i64, bt_is_i64, a, *chk, s);
+    else launch_wave_plan<true, false>(grid, kv_len_is_i64, bt_is_i64, a, none, s);
+    if (const int rc = check_launch(who)) return rc;
+    if (chk && !with_check) step_check_launch(*chk, bt_is_i64, kv_len_is_i64, s);
+    else if (chk) step_check_scan(*chk, bt_is_i64, kv_len_is_i64, s);
+    return check_launch(who);
+  }
+  if (wave_plan) {
+    launch_wave_plan<false, false>(1, kv_len_is_i64, bt_is_i64, a, none, s);
+  } else if (kv_len_is_i64) {
+    if (bt_is_i64) decode_plan_kernel<int64_t, int64_t><<<1, kPlanThreads, 0, s>>>(a);
+    else decode_plan_kernel<int64_t, int32_t><<<1, kPlanThreads, 0, s>>>(a);
+  } else {
+    if (bt_is_i64) decode_plan_kernel<int32_t, int64_t><<<1, kPlanThreads, 0, s>>>(a);
+    else decode_plan_kernel<int32_t, int32_t><<<1, kPlanThreads, 0, s>>>(a);
+  }
+  if (const int rc = check_launch(who)) return rc;
+  if (a.num_seqs > 0 && a.ids_cap > 0) {
+    IdsArgs d;
+    d.block_table = a.block_table;
+    d.bt_stride = a.bt_stride;
+    d.num_seqs = a.num_seqs;
+    d.max_blocks = a.max_blocks;
+    d.work = a.work;
+    d.work_cap = a.work_cap;
+    d.ids = a.ids;
+    d.status = a.status;
+    d.num_blocks = a.num_blocks;
+    d.bs_log2 = a.bs_log2;
+    // one wave per slot the plan can fill, in one pass up to 4096 work groups
+    constexpr int64_t kSlotsPerGroup = kIdsThreads / 64;
+    const int grid = static_cast<int>(std::min<int64_t>(
+        4096, std::max<int64_t>(1, (slots + kSlotsPerGroup - 1) / kSlotsPerGroup)));
+    if (bt_is_i64) decode_ids_kernel<int64_t><<<grid, kIdsThreads, 0, s>>>(d);
+    else decode_ids_kernel<int32_t><<<grid, kIdsThreads, 0, s>>>(d);
+  }
+  if (chk) step_check_launch(*chk, bt_is_i64, kv_len_is_i64, s);
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace mv
+
 extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const void* block_table,
                               int32_t bt_is_i64, int64_t bt_stride, int32_t num_seqs,
                               int32_t max_blocks, int32_t block_size, int64_t num_blocks,
@@ -1878,96 +2026,38 @@ extern "C" int mv_decode_plan(const void* kv_len, int32_t kv_len_is_i64, const v
                               int64_t block_ids_capacity, int32_t* counters, int32_t* status,
                               void* stream) {
   using namespace mv;
-  if (!status) return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null status");
-  if (num_seqs < 0 || max_blocks < 0 || work_capacity < 0 || block_ids_capacity < 0 ||
-      num_blocks < 0 || num_kv_heads <= 0)
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: bad sizes");
-  if (!is_pow2(block_size))
-    return fail(MV_ERR_UNSUPPORTED, "mv_decode_plan: block_size %d is not a power of 2", block_size);
-  if (num_seqs > 0 && (!kv_len || !counters || (max_blocks > 0 && !block_table)))
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null pointer");
-  if ((work_capacity > 0 && !work_items) || (block_ids_capacity > 0 && !block_ids))
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: null work list");
-  const int64_t ids_need =
-      mv_decode_block_ids_capacity(num_seqs, max_blocks, num_kv_heads, work_capacity);
-  if (block_ids_capacity < ids_need)
-    return fail(MV_ERR_INVALID_ARGUMENT, "mv_decode_plan: block_ids capacity %lld < %lld",
-                static_cast<long long>(block_ids_capacity), static_cast<long long>(ids_need));
   PlanArgs a;
-  a.kv_len = kv_len;
-  a.block_table = block_table;
-  a.bt_stride = bt_stride;
-  a.num_seqs = num_seqs;
-  a.max_blocks = max_blocks;
-  a.bs_log2 = ilog2_exact(block_size);
-  a.num_kv_heads = num_kv_heads;
-  a.groups_per_cu = groups_per_cu;
-  a.cu_count = cu_count;
-  a.fixed_part_tokens = fixed_partition_tokens;
-  a.num_blocks = num_blocks;
-  a.work = work_items;
-  a.work_cap = work_capacity;
-  a.ids = block_ids;
-  a.ids_cap = block_ids_capacity;
-  a.counters = counters;
-  a.status = status;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  // slots the plan can fill (the same bound as a launch of fixed size)
-  const int64_t slots = std::min<int64_t>(
-      work_capacity, plan_bounds(num_seqs, max_blocks, block_size, num_kv_heads, groups_per_cu, cu_count).groups);
-  const bool wave_plan = num_seqs <= kWavePlanSeqs;
-  // plan and id lists in one launch: a small table (work group 0 checks all
-  // of it) and lists to write; one wave per slot after work group 0
-  const bool fused = wave_plan && num_seqs > 0 && block_ids_capacity > 0 &&
-                     static_cast<int64_t>(num_seqs) * max_blocks <= kFusedTableEntries &&
-                     slots <= kFusedSlots;
-  if (fused) {
-    const unsigned grid = 2 + static_cast<unsigned>((slots + kWavePlanWaves - 1) / kWavePlanWaves);
-    if (kv_len_is_i64) {
-      if (bt_is_i64) decode_plan_wave_kernel<int64_t, int64_t, true><<<grid, 64 * kWavePlanWaves, 0, s>>>(a);
-      else decode_plan_wave_kernel<int64_t, int32_t, true><<<grid, 64 * kWavePlanWaves, 0, s>>>(a);
-    } else {
-      if (bt_is_i64) decode_plan_wave_kernel<int32_t, int64_t, true><<<grid, 64 * kWavePlanWaves, 0, s>>>(a);
-      else decode_plan_wave_kernel<int32_t, int32_t, true><<<grid, 64 * kWavePlanWaves, 0, s>>>(a);
-    }
-    return check_launch("mv_decode_plan");
-  }
-  if (wave_plan) {
-    if (kv_len_is_i64) {
-      if (bt_is_i64) decode_plan_wave_kernel<int64_t, int64_t, false><<<1, 64 * kWavePlanWaves, 0, s>>>(a);
-      else decode_plan_wave_kernel<int64_t, int32_t, false><<<1, 64 * kWavePlanWaves, 0, s>>>(a);
-    } else {
-      if (bt_is_i64) decode_plan_wave_kernel<int32_t, int64_t, false><<<1, 64 * kWavePlanWaves, 0, s>>>(a);
-      else decode_plan_wave_kernel<int32_t, int32_t, false><<<1, 64 * kWavePlanWaves, 0, s>>>(a);
-    }
-  } else if (kv_len_is_i64) {
-    if (bt_is_i64) decode_plan_kernel<int64_t, int64_t><<<1, kPlanThreads, 0, s>>>(a);
-    else decode_plan_kernel<int64_t, int32_t><<<1, kPlanThreads, 0, s>>>(a);
-  } else {
-    if (bt_is_i64) decode_plan_kernel<int32_t, int64_t><<<1, kPlanThreads, 0, s>>>(a);
-    else decode_plan_kernel<int32_t, int32_t><<<1, kPlanThreads, 0, s>>>(a);
-  }
-  if (const int rc = check_launch("mv_decode_plan")) return rc;
-  if (num_seqs > 0 && block_ids_capacity > 0) {
-    IdsArgs d;
-    d.block_table = block_table;
-    d.bt_stride = bt_stride;
-    d.num_seqs = num_seqs;
-    d.max_blocks = max_blocks;
-    d.work = work_items;
-    d.work_cap = work_capacity;
-    d.ids = block_ids;
-    d.status = status;
-    d.num_blocks = num_blocks;
-    d.bs_log2 = a.bs_log2;
-    // one wave per slot the plan can fill, in one pass up to 4096 work groups
-    constexpr int64_t kSlotsPerGroup = kIdsThreads / 64;
-    const int grid = static_cast<int>(std::min<int64_t>(
-        4096, std::max<int64_t>(1, (slots + kSlotsPerGroup - 1) / kSlotsPerGroup)));
-    if (bt_is_i64) decode_ids_kernel<int64_t><<<grid, kIdsThreads, 0, s>>>(d);
-    else decode_ids_kernel<int32_t><<<grid, kIdsThreads, 0, s>>>(d);
-  }
-  return check_launch("mv_decode_plan");
+  if (const int rc = plan_prepare("mv_decode_plan", kv_len, block_table, bt_stride, num_seqs, max_blocks,
+                                  block_size, num_blocks, num_kv_heads, groups_per_cu, cu_count,
+                                  fixed_partition_tokens, work_items, work_capacity, block_ids,
+                                  block_ids_capacity, counters, status, &a))
+    return rc;
+  return plan_enqueue("mv_decode_plan", a, kv_len_is_i64, bt_is_i64, block_size, nullptr,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mv_decode_plan_step_check(
+    const void* kv_len, int32_t kv_len_is_i64, const void* block_table, int32_t bt_is_i64, int64_t bt_stride,
+    int32_t num_seqs, int32_t max_blocks, int32_t block_size, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t groups_per_cu, int32_t cu_count, int32_t fixed_partition_tokens, int32_t* work_items,
+    int64_t work_capacity, int32_t* block_ids, int64_t block_ids_capacity, int32_t* counters, int32_t* status,
+    const int64_t* slot_mapping, const int64_t* positions, const void* cos_table, const void* sin_table,
+    int64_t table_stride, int64_t max_positions, int32_t head_dim, int32_t dtype, void* cos_rows,
+    void* sin_rows, int32_t* step_status, void* check_workspace, size_t check_workspace_bytes, void* stream) {
+  using namespace mv;
+  constexpr const char* who = "mv_decode_plan_step_check";
+  PlanArgs a;
+  if (const int rc = plan_prepare(who, kv_len, block_table, bt_stride, num_seqs, max_blocks, block_size,
+                                  num_blocks, num_kv_heads, groups_per_cu, cu_count, fixed_partition_tokens,
+                                  work_items, work_capacity, block_ids, block_ids_capacity, counters, status, &a))
+    return rc;
+  StepCheckArgs c;
+  if (const int rc = step_check_prepare(who, slot_mapping, block_table, bt_stride, kv_len, num_seqs, max_blocks,
+                                        block_size, num_blocks, positions, cos_table, sin_table, table_stride,
+                                        max_positions, head_dim, dtype, cos_rows, sin_rows, step_status,
+                                        check_workspace, check_workspace_bytes, &c))
+    return rc;
+  return plan_enqueue(who, a, kv_len_is_i64, bt_is_i64, block_size, &c, static_cast<hipStream_t>(stream));
 }
 
 namespace mv {

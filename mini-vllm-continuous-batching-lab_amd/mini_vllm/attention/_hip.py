@@ -16,7 +16,7 @@ import warnings
 
 import torch  # noqa: F401  (must be loaded before the kernel library)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MV_OK = 0
 MV_ERR_INVALID_ARGUMENT = -1
@@ -93,6 +93,16 @@ SIGNATURES = {
         _I32, _I32, _I32, _I32,    # num_kv_heads, groups_per_cu, cu_count, fixed_partition_tokens
         _P, _I64, _P, _I64,        # work_items, capacity, block_ids, capacity
         _P, _P, _P,                # counters, status, stream
+    ]),
+    "mv_decode_plan_step_check": (ctypes.c_int, [
+        _P, _I32, _P, _I32, _I64,  # kv_len, is_i64, block_table, is_i64, bt_stride
+        _I32, _I32, _I32, _I64,    # num_seqs, max_blocks, block_size, num_blocks
+        _I32, _I32, _I32, _I32,    # num_kv_heads, groups_per_cu, cu_count, fixed_partition_tokens
+        _P, _I64, _P, _I64,        # work_items, capacity, block_ids, capacity
+        _P, _P, _P,                # counters, status, slot_mapping
+        _P, _P, _P, _I64, _I64,    # positions, cos, sin, table_stride, max_positions
+        _I32, _I32, _P, _P,        # head_dim, dtype, cos_rows, sin_rows
+        _P, _P, _SZ, _P,           # step_status, check_workspace, bytes, stream
     ]),
     "mv_decode_graph_bounds": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _I32, _P]),
     "mv_decode_block_ids_capacity": (_I64, [_I32, _I32, _I32, _I64]),

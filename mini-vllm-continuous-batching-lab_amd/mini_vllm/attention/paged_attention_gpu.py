@@ -580,10 +580,13 @@ class _PendingPlan:
 def _plan_launch(block_table: torch.Tensor, kv_len_after: torch.Tensor, block_size: int,
                  num_blocks: int, device: torch.device, head_dim: int, dtype: torch.dtype,
                  num_kv_heads: int, split: Tuple[int, int], capture: int,
-                 extra_words: int = 0) -> _PendingPlan:
+                 extra_words: int = 0, step_check: Optional[tuple] = None) -> _PendingPlan:
     """Enqueue mv_decode_plan (no read-back). ``extra_words`` status words
     follow the plan's in the same allocation, so a caller that launches
-    more checks reads everything back at once."""
+    more checks reads everything back at once. ``step_check``: the step
+    check's own arguments (slot_mapping ... sin_rows, then workspace and
+    its size) of ``mv_decode_plan_step_check``, which then enqueues the
+    step check with the plan, its status in the extra words."""
     lib = _hip.load()
     bt, kv = _decode_metadata(block_table, kv_len_after, device)
 
@@ -611,16 +614,20 @@ def _plan_launch(block_table: torch.Tensor, kv_len_after: torch.Tensor, block_si
     n_status = _hip.MV_PLAN_WORDS + extra_words
     buf = torch.empty(n_work + n_ids + n_cnt + n_status, dtype=torch.int32, device=device)
     base = buf.data_ptr()
-    _hip.check(
-        _hip.plan(
-            kv.data_ptr(), int(kv.dtype == torch.int64), bt.data_ptr(),
-            int(bt.dtype == torch.int64), bt.stride(0) if bt.dim() == 2 else 0, num_seqs,
-            max_blocks, block_size, num_blocks, num_kv_heads, split[0], split[1], fixed,
-            base, cap, base + 4 * n_work, n_ids, base + 4 * (n_work + n_ids),
-            base + 4 * (n_work + n_ids + n_cnt), _stream(device),
-        ),
-        "mv_decode_plan",
+    plan_args = (
+        kv.data_ptr(), int(kv.dtype == torch.int64), bt.data_ptr(),
+        int(bt.dtype == torch.int64), bt.stride(0) if bt.dim() == 2 else 0, num_seqs,
+        max_blocks, block_size, num_blocks, num_kv_heads, split[0], split[1], fixed,
+        base, cap, base + 4 * n_work, n_ids, base + 4 * (n_work + n_ids),
+        base + 4 * (n_work + n_ids + n_cnt),
     )
+    if step_check is None:
+        _hip.check(_hip.plan(*plan_args, _stream(device)), "mv_decode_plan")
+    else:
+        step_status = base + 4 * (n_work + n_ids + n_cnt + _hip.MV_PLAN_WORDS)
+        _hip.check(lib.mv_decode_plan_step_check(*plan_args, *step_check[:10], step_status,
+                                                 *step_check[10:], _stream(device)),
+                   "mv_decode_plan_step_check")
     s0 = n_work + n_ids + n_cnt
     status_all = buf[s0:]
 
@@ -746,14 +753,6 @@ def _fused_step_prepare(block_table: torch.Tensor, kv_len_after: torch.Tensor, b
             rows = _cache_get("rope_rows" + g, (positions, cos, sin), (head_dim, dtype, device, capture))
         if fused_ok is not None and (rows is not None or not rope):
             return plan, slots, fused_ok, rows
-    pending = None
-    if plan is None:
-        pending = _plan_launch(block_table, kv_len_after, block_size, num_blocks, device,
-                               head_dim, dtype, num_kv_heads, split, capture,
-                               extra_words=_hip.MV_STEP_WORDS)
-        status = pending.extra
-    else:
-        status = torch.empty(_hip.MV_STEP_WORDS, dtype=torch.int32, device=device)
     bt, kv = _decode_metadata(block_table, kv_len_after, device)
     pos = rows = None
     max_pos = 0
@@ -779,18 +778,31 @@ def _fused_step_prepare(block_table: torch.Tensor, kv_len_after: torch.Tensor, b
                 torch.empty(num_seqs, head_dim, dtype=dtype, device=device))
     ws_bytes = lib.mv_decode_write_check_workspace_bytes(num_seqs)
     ws = _check_workspace(device, ws_bytes)
-    _hip.check(
-        lib.mv_decode_step_check(
-            _ptr(slots), _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
-            bt.stride(0) if bt.dim() == 2 else 0, _ptr(kv), int(kv.dtype == torch.int64),
-            num_seqs, bt.shape[1] if bt.dim() == 2 else 0, block_size, num_blocks,
-            _ptr(pos), _ptr(tc) if rope else None, _ptr(ts) if rope else None,
+    # the step check's own arguments, in mv_decode_plan_step_check's order
+    # (its status pointer goes between the rows and the workspace)
+    step = (_ptr(slots), _ptr(pos), _ptr(tc) if rope else None, _ptr(ts) if rope else None,
             tc.stride(0) if rope else 0, max_pos, head_dim, _hip.MV_DTYPE[dtype],
-            _ptr(rows[0]) if rope else None, _ptr(rows[1]) if rope else None, _ptr(status),
-            _ptr(ws), ws_bytes, _stream(device),
-        ),
-        "mv_decode_step_check",
-    )
+            _ptr(rows[0]) if rope else None, _ptr(rows[1]) if rope else None, None,
+            _ptr(ws), ws_bytes)
+    pending = None
+    if plan is None:
+        # the plan and the step check enqueued together (one launch for
+        # small batches), their status words in one allocation
+        pending = _plan_launch(block_table, kv_len_after, block_size, num_blocks, device,
+                               head_dim, dtype, num_kv_heads, split, capture,
+                               extra_words=_hip.MV_STEP_WORDS, step_check=step[:10] + step[11:])
+        status = pending.extra
+    else:
+        status = torch.empty(_hip.MV_STEP_WORDS, dtype=torch.int32, device=device)
+        _hip.check(
+            lib.mv_decode_step_check(
+                step[0], _ptr(bt) if bt.numel() else None, int(bt.dtype == torch.int64),
+                bt.stride(0) if bt.dim() == 2 else 0, _ptr(kv), int(kv.dtype == torch.int64),
+                num_seqs, bt.shape[1] if bt.dim() == 2 else 0, block_size, num_blocks,
+                *step[1:10], _ptr(status), *step[11:], _stream(device),
+            ),
+            "mv_decode_step_check",
+        )
 
     def raise_slots(st) -> None:
         bad, dups = st[_hip.MV_STEP_SLOTS_OUT_OF_RANGE], st[_hip.MV_STEP_SLOTS_DUPLICATES]

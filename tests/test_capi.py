@@ -96,7 +96,7 @@ def test_every_declared_symbol_is_exported_and_typed(lib):
 
 
 def test_abi_queries(lib):
-    assert lib.mv_abi_version() == _hip.ABI_VERSION == 6
+    assert lib.mv_abi_version() == _hip.ABI_VERSION == 7
     assert lib.mv_decode_chunk_tokens(64, 2) == 64       # 4 waves x one 16-token tile
     assert lib.mv_decode_chunk_tokens(128, 0) == 64
     assert lib.mv_decode_chunk_tokens(96, 2) == 0

@@ -374,3 +374,83 @@ def test_step_check_equals_the_separate_checks(seed, nseq, bs, max_blocks, pool,
         _hip.MV_DTYPE[dt], None, None, _ptr(st2), _ptr(ws), nbytes, stream), "mv_decode_step_check")
     torch.cuda.synchronize()
     assert st2.tolist()[:5] == want[:4] + [0]
+
+
+def _plan_buffers(nseq, max_blocks, bs, hkv):
+    lib = _hip.load()
+    cap = nseq * hkv * max(1, -(-max_blocks * bs // 16))
+    ids_cap = lib.mv_decode_block_ids_capacity(nseq, max_blocks, hkv, cap)
+    return (torch.full((8 * cap,), -9, dtype=torch.int32, device=DEV),
+            torch.full((max(ids_cap, 4),), -9, dtype=torch.int32, device=DEV),
+            torch.full((nseq * hkv,), -9, dtype=torch.int32, device=DEV),
+            torch.full((_hip.MV_PLAN_WORDS,), -9, dtype=torch.int32, device=DEV), cap, ids_cap)
+
+
+@pytest.mark.parametrize("seed,nseq,bs,max_blocks,pool,idx", [
+    (0, 64, 16, 8, 60, torch.int64),    # one launch: plan, id lists and step check
+    (2, 33, 4, 20, 90, torch.int32),    # one launch
+    (1, 256, 16, 6, 300, torch.int64),  # over 64 sequences: the separate launches
+])
+def test_plan_step_check_equals_the_two_calls(seed, nseq, bs, max_blocks, pool, idx):
+    """mv_decode_plan_step_check gives mv_decode_plan's work list, id lists
+    and status words, and mv_decode_step_check's status words and rotary
+    rows, on the same inputs with out-of-pool slots, shared-slot reads and
+    out-of-range positions planted."""
+    say("plan + step check", seed, nseq, bs, idx)
+    lib = _hip.load()
+    hkv, d, dt, max_pos = 2, 64, torch.bfloat16, 4000
+    slots, bt, kv = shared_layout(seed, nseq, bs, max_blocks, pool)
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.randint(0, max_pos, (nseq,), generator=g)
+    pos[:2] = torch.tensor([-1, max_pos])
+    slots = torch.as_tensor(slots)
+    slots[0] = pool * bs + 5
+    cos = torch.randn(max_pos, d, generator=g).to(dt).to(DEV)
+    sin = torch.randn(max_pos, d, generator=g).to(dt).to(DEV)
+    btt, kvt = torch.from_numpy(bt).to(idx).to(DEV), torch.from_numpy(kv).to(idx).to(DEV)
+    sd, pd = slots.to(DEV), pos.to(DEV)
+    i64 = int(idx == torch.int64)
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    nbytes = lib.mv_decode_write_check_workspace_bytes(nseq)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = []
+    for combined in (False, True):
+        work, ids, cnt, st, cap, ids_cap = _plan_buffers(nseq, max_blocks, bs, hkv)
+        step = torch.full((_hip.MV_STEP_WORDS,), -7, dtype=torch.int32, device=DEV)
+        rows = [torch.full((nseq, d), float("nan"), dtype=dt, device=DEV) for _ in range(2)]
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        plan = (_ptr(kvt), i64, _ptr(btt), i64, btt.stride(0), nseq, max_blocks, bs, pool, hkv, 2, cus, 0,
+                _ptr(work), cap, _ptr(ids), ids_cap, _ptr(cnt), _ptr(st))
+        chk = (_ptr(pd), _ptr(cos), _ptr(sin), cos.stride(0), max_pos, d, _hip.MV_DTYPE[dt],
+               _ptr(rows[0]), _ptr(rows[1]))
+        if combined:
+            _hip.check(lib.mv_decode_plan_step_check(*plan, _ptr(sd), *chk, _ptr(step), _ptr(ws), nbytes,
+                                                     stream), "mv_decode_plan_step_check")
+        else:
+            _hip.check(lib.mv_decode_plan(*plan, stream), "mv_decode_plan")
+            _hip.check(lib.mv_decode_step_check(_ptr(sd), _ptr(btt), i64, btt.stride(0), _ptr(kvt), i64, nseq,
+                                                max_blocks, bs, pool, *chk, _ptr(step), _ptr(ws), nbytes,
+                                                stream), "mv_decode_step_check")
+        torch.cuda.synchronize()
+        s = st.tolist()
+        n = s[_hip.MV_PLAN_NUM_ITEMS]
+        per = s[_hip.MV_PLAN_IDS_PER_ITEM]
+        w = work[: 8 * n].view(n, 8).cpu()
+        lists = []
+        for slot, e in enumerate(w.tolist()):
+            span4 = min(per, ((e[5] - 1) // bs - e[4] // bs + 1 + 3) // 4 * 4)
+            lists.append(ids[slot * per:slot * per + span4].cpu())
+        out.append((s, w, lists, cnt.cpu(), step.tolist()[:5], [bits(r.cpu()) for r in rows]))
+    (s0, w0, l0, c0, t0, r0), (s1, w1, l1, c1, t1, r1) = out
+    assert s0 == s1
+    # the same groups with the same id lists (the 1024-thread plan kernel of
+    # the larger batch orders groups of one size by arrival)
+    m0 = {tuple(e): l.tolist() for e, l in zip(w0.tolist(), l0)}
+    m1 = {tuple(e): l.tolist() for e, l in zip(w1.tolist(), l1)}
+    assert m0 == m1 and len(m0) == s1[_hip.MV_PLAN_NUM_ITEMS]
+    if nseq <= 64:
+        assert torch.equal(w0, w1)
+    assert torch.equal(c0, c1) and not c1.any()
+    assert t0 == t1, (t0, t1)
+    assert t1[0] >= 1 and t1[4] == 2  # the planted slot and positions count
+    assert all(torch.equal(x, y) for x, y in zip(r0, r1))
