@@ -185,6 +185,33 @@ def test_bad_entry_in_a_second_id_pass_raises():
         hip_decode_attention(q, kc, kc, bt, kv, 1)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_small_batch_plans_on_random_shapes(seed):
+    """Batches of up to 64 sequences (the wave plan, in one launch or two
+    by table size) on random lengths, block sizes 1-64 and 1-8 kv heads,
+    some pieces over 64 tiles (buckets wider than one tile): every unit is
+    cut into pieces that tile [0, kv_len) once, the slots form a complete
+    list, and the id lists are the table entries."""
+    import random
+    import types
+
+    from benchmarks.paged_decode_workloads import make_layout
+
+    rnd = random.Random(1000 + seed)
+    bs = rnd.choice([1, 4, 16, 64])
+    hkv = rnd.choice([1, 2, 4, 8])
+    n = rnd.randint(1, 64)
+    top = rnd.choice([40, 300, 2048, 6000])
+    lens = [rnd.randint(1, top) for _ in range(n)]
+    spec = WorkloadSpec("small-random", 8 * hkv, hkv, 64, bs, torch.bfloat16, n, ("fixed", lens))
+    layout = make_layout(spec, seed)
+    case = types.SimpleNamespace(layout=layout, block_table=layout.block_table(),
+                                 kv_len=torch.tensor(layout.kv_lens, dtype=torch.int64))
+    say("plan: random small batch", seed, n, bs, hkv, max(lens))
+    plan = _check_plan(case)
+    assert plan.num_groups >= n * hkv
+
+
 def _plan_lists(bt, kv, bs, pool, hkv):
     plan = plan_decode(bt, kv, bs, pool, DEV, 64, torch.bfloat16, hkv)
     torch.cuda.synchronize()
