@@ -659,10 +659,21 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   }
   __syncthreads();
 
+  // One query head per thread: kWaves * 4 >= kMaxGroup >= n_rep.
+  static_assert(kWaves * 4 >= kMaxGroup, "one head per epilogue thread");
   const int q = threadIdx.x & 15;
+  const int r = threadIdx.x >> 4;
+  const bool has_row = r < a.n_rep;
   const int64_t slot_base = (static_cast<int64_t>(b) * a.num_q_heads + h * a.n_rep) * a.max_parts;
-  auto out_row = [&](int r) { return static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head; };
-  for (int r = threadIdx.x >> 4; r < a.n_rep; r += kWaves * 4) {
+  raw_t* const op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head + 2 * q;
+  // this work group's partial of head r: (max, sum) and its dim pairs, as
+  // stored (the partial O words: two fp32, or two values of the 16-bit
+  // data type)
+  uint64_t own_ml = 0;
+  uint64_t own_ov[NPAIR];
+#pragma unroll
+  for (int j = 0; j < NPAIR; ++j) own_ov[j] = 0;
+  if (has_row) {
     float mx = kNegInf;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wave_ms(w)[r]);
@@ -689,33 +700,26 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     // leaves l at least that, an exact one at least 1)
     const float inv = 1.f / sum;
     if (n_parts == 1) {
-      raw_t* op = out_row(r) + 2 * q;
 #pragma unroll
       for (int j = 0; j < NPAIR; ++j) {
         op[32 * j] = from_f32<DTYPE>(v[j].x * inv);
         op[32 * j + 1] = from_f32<DTYPE>(v[j].y * inv);
       }
     } else {
-      const int64_t slot = slot_base + static_cast<int64_t>(r) * a.max_parts + part;
-      if constexpr (kPartials16) {  // dims 2q + 32j, +1 as two 16-bit values
-        uint32_t* dst = reinterpret_cast<uint32_t*>(a.ws_o) + slot * (D / 2) + q;
+      own_ml = pack_f32x2(mx, sum);
 #pragma unroll
-        for (int j = 0; j < NPAIR; ++j)
-          store_coherent_u32(dst + 16 * j,
-                             static_cast<uint32_t>(from_f32<DTYPE>(v[j].x * inv)) |
-                                 (static_cast<uint32_t>(from_f32<DTYPE>(v[j].y * inv)) << 16));
-      } else {
-        uint64_t* dst = reinterpret_cast<uint64_t*>(a.ws_o + slot * D + 2 * q);
-#pragma unroll
-        for (int j = 0; j < NPAIR; ++j) store_coherent_u64(dst + 16 * j, pack_f32x2(v[j].x * inv, v[j].y * inv));
+      for (int j = 0; j < NPAIR; ++j) {
+        if constexpr (kPartials16)  // dims 2q + 32j, +1 as two 16-bit values
+          own_ov[j] = static_cast<uint32_t>(from_f32<DTYPE>(v[j].x * inv)) |
+                      (static_cast<uint32_t>(from_f32<DTYPE>(v[j].y * inv)) << 16);
+        else
+          own_ov[j] = pack_f32x2(v[j].x * inv, v[j].y * inv);
       }
-      if (q == 0) store_coherent_u64(reinterpret_cast<uint64_t*>(a.ws_ml) + slot, pack_f32x2(mx, sum));
     }
   }
   if (n_parts == 1) return;
 
   // ---- cross-partition merge by the last work group --------------------
-  // (the partial O words: two fp32, or two values of the 16-bit data type)
   auto ov_lo = [](uint64_t x) -> float {
     if constexpr (kPartials16) return to_f32<DTYPE>(static_cast<uint16_t>(x));
     else return unpack_lo(x);
@@ -724,6 +728,18 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     if constexpr (kPartials16) return to_f32<DTYPE>(static_cast<uint16_t>(x >> 16));
     else return unpack_hi(x);
   };
+  if (has_row) {
+    const int64_t slot = slot_base + static_cast<int64_t>(r) * a.max_parts + part;
+#pragma unroll
+    for (int j = 0; j < NPAIR; ++j) {
+      if constexpr (kPartials16)
+        store_coherent_u32(reinterpret_cast<uint32_t*>(a.ws_o) + slot * (D / 2) + q + 16 * j,
+                           static_cast<uint32_t>(own_ov[j]));
+      else
+        store_coherent_u64(reinterpret_cast<uint64_t*>(a.ws_o + slot * D + 2 * q) + 16 * j, own_ov[j]);
+    }
+    if (q == 0) store_coherent_u64(reinterpret_cast<uint64_t*>(a.ws_ml) + slot, own_ml);
+  }
   // The partials above are device-coherent stores; once every wave has
   // seen them acknowledged (vmcnt(0)), the counter increment publishes
   // them. The work group that completes the count reads all partials
@@ -742,7 +758,9 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   // together (one memory round trip per round; the round size is the
   // smallest of 4, 8, kMergeRound that fits, so few loads are wasted), then
   // folds them into a running (max, sum, o) with one rescale per round.
-  for (int r = threadIdx.x >> 4; r < a.n_rep; r += kWaves * 4) {
+  // The merging group's own partial comes from its registers (the bits it
+  // stored), not from memory.
+  if (has_row) {
     const int64_t slot0 = slot_base + static_cast<int64_t>(r) * a.max_parts;
     float m_all = kNegInf, l_all = 0.f;
     float2 acc[NPAIR];
@@ -757,7 +775,14 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       uint64_t ov[RR][NPAIR];
 #pragma unroll
       for (int pp = 0; pp < RR; ++pp) {
-        const int64_t slot = slot0 + p0 + min(pp, np - 1);
+        const int p = p0 + min(pp, np - 1);
+        if (p == part) {  // work-group uniform
+          ml[pp] = own_ml;
+#pragma unroll
+          for (int j = 0; j < NPAIR; ++j) ov[pp][j] = own_ov[j];
+          continue;
+        }
+        const int64_t slot = slot0 + p;
         ml[pp] = load_coherent_u64(reinterpret_cast<const uint64_t*>(a.ws_ml) + slot);
         if constexpr (kPartials16) {
           const uint32_t* src = reinterpret_cast<const uint32_t*>(a.ws_o) + slot * (D / 2) + q;
@@ -800,7 +825,6 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
       else fold(IntC<RMAX>{}, p0, np);
     }
     const float inv = 1.f / l_all;
-    raw_t* op = out_row(r) + 2 * q;
 #pragma unroll
     for (int j = 0; j < NPAIR; ++j) {
       op[32 * j] = from_f32<DTYPE>(acc[j].x * inv);
