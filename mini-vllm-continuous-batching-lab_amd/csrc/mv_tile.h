@@ -343,6 +343,11 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 __device__ __forceinline__ void copy_to_lds_16B(const char* src, uint32_t lds_base) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
 }
+// HBM -> LDS copy of 4 bytes per lane: lane l's bytes land at LDS address
+// lds_base + 4 l (as above).
+__device__ __forceinline__ void copy_to_lds_4B(const char* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
 // The same copy from a wave-uniform base address (SGPRs) plus this lane's
 // 32-bit byte offset (global_load_lds_dwordx4 with saddr): no 64-bit
 // address arithmetic per lane. `sbase` must be the same in every lane.

@@ -106,7 +106,8 @@ struct Traits : TileGeom<DTYPE, D> {
   // LDS is one union, laid out per phase:
   //   tile loop: [kWaves][kStages][K, V][kTileBytes], then the partition's
   //              block ids (int32, kIdCap), then the group's 16 Q rows, then
-  //              the cos and sin rows of the sequence's position (fused RoPE);
+  //              the cos and sin rows of the sequence's position (fused RoPE),
+  //              the new K and V rows and the new token's slot (fused write);
   //   epilogue:  each wave's o rows and (max, sum) in its own tile buffers;
   //              the last-group flag where the block ids were.
   static constexpr int kIdsOffset = kWaves * kWaveLds;
@@ -120,7 +121,8 @@ struct Traits : TileGeom<DTYPE, D> {
   static constexpr int kFlagOffset = kIdsOffset;
   static constexpr int kRopeOffset = kTilesEnd;  // cos row, then sin row (kRowBytes each)
   static constexpr int kNewOffset = kRopeOffset + 2 * kRowBytes;  // new K row, then V row (fused write)
-  static constexpr int kLdsBytes = kNewOffset + 2 * kRowBytes;
+  static constexpr int kSlotOffset = kNewOffset + 2 * kRowBytes;  // the new token's slot (int64)
+  static constexpr int kLdsBytes = kSlotOffset + 16;
   static_assert(kWaveEpilogueBytes <= kWaveLds, "a wave's epilogue fits its tile buffers");
   static_assert(kStages >= 2 && kStages <= 4, "tile stages");
   // Work groups one CU holds (160 KiB of LDS on gfx950), and the matching
@@ -214,6 +216,10 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   asm volatile("" ::"s"(a.work), "s"(a.block_ids), "s"(a.ids_per_item), "s"(a.num_kv_heads),
                "s"(a.q), "s"(a.q_stride_tok), "s"(a.q_stride_head), "s"(a.n_rep), "s"(a.k_cache),
                "s"(a.v_cache), "s"(a.bs_log2));
+  if constexpr (FUSED)  // the new rows' and the slot's copies, before the tile loop
+    asm volatile("" ::"s"(a.new_k), "s"(a.new_v), "s"(a.nk_st), "s"(a.nk_sh), "s"(a.nv_st), "s"(a.nv_sh),
+                 "s"(a.slots));
+  if constexpr (ROPE) asm volatile("" ::"s"(a.rope_cos), "s"(a.rope_sin));
   const int item = blockIdx.x;
   const uint32_t lds0 = lds_address(s_lds);
   int32_t* s_ids = reinterpret_cast<int32_t*>(s_lds + Tr::kIdsOffset);
@@ -275,8 +281,9 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   // loop. When that slot is the token's table position (as the block
   // manager lays it out) the token's row in the LDS tile is overwritten
   // with the new rows -- the bytes the write stores -- before it is used;
-  // otherwise the token is the one read from the pool. The rows arrive in
-  // LDS with the Q rows (wave 0's copies, before any tile copy); wave
+  // otherwise the token is the one read from the pool. The rows and the
+  // slot arrive in LDS with the Q rows (wave 0's copies, before any tile
+  // copy); wave
   // new_wave (the one whose tile holds the token) then keeps them in
   // registers, lanes [0, RP) the K row's 16-byte pieces, [RP, 2 RP) the V
   // row's, and with the fused RoPE rotates the K row there, before its
@@ -289,9 +296,6 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   uint4 new_piece = make_uint4(0, 0, 0, 0);
   const bool new_lane = wave == new_wave && lane < 2 * RP;
   const int new_pc = lane < RP ? lane : lane - RP;
-  if constexpr (FUSED) {
-    if (last_piece) new_slot = a.slots[b];
-  }
 
   // ---- Q rows of the group -> LDS (wave 0). Rows r >= n_rep repeat row
   // n_rep - 1: MFMA columns (and the softmax state per column) are
@@ -322,6 +326,12 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
                         new_pc * 16;
       copy_to_lds_16B(src, __builtin_amdgcn_readfirstlane(lds0 + Tr::kNewOffset));
     }
+    // and the slot of b's new token: lanes 0 and 1 copy its two 32-bit
+    // halves (a register load here would be waited for at once, one more
+    // memory round trip before this group's first tile)
+    if (FUSED && last_piece && lane < 2)
+      copy_to_lds_4B(reinterpret_cast<const char*>(a.slots + b) + 4 * lane,
+                     __builtin_amdgcn_readfirstlane(lds0 + Tr::kSlotOffset));
   }
 
   // LDS slot (64c + lane) of this wave's tile: its row, and the global
@@ -583,6 +593,7 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
     }
   }
   if constexpr (FUSED) {
+    if (last_piece) new_slot = *reinterpret_cast<const int64_t*>(s_lds + Tr::kSlotOffset);
     if (last_piece && wave == new_wave) {  // wave-uniform
       // the new rows, landed with the Q rows (the barrier above)
       if (new_lane) new_piece = *reinterpret_cast<const uint4*>(s_lds + Tr::kNewOffset + lane * 16);
