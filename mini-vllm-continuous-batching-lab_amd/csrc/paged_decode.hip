@@ -1476,9 +1476,9 @@ __device__ inline void wave_plan_lengths(const PlanArgs& a, WavePlan& p, int lan
 
 // Steps 2-3 after wave_plan_lengths; the deal's positions only when
 // `positions`.
-__device__ inline void wave_plan_rest(const PlanArgs& a, WavePlan& p, int* s_count, int lane, bool positions) {
+__device__ inline void wave_plan_rest(const PlanArgs& a, WavePlan& p, int* s_used, int lane, bool positions) {
   const int hkv = a.num_kv_heads;
-  s_count[lane] = 0;
+  s_used[lane] = 0;
   const int64_t total_tiles = wave_sum64(p.tiles);
   const int live_seqs = wave_sum(p.kv > 0);
   p.most_tiles = wave_max(p.tiles);
@@ -1529,11 +1529,11 @@ __device__ inline void wave_plan_rest(const PlanArgs& a, WavePlan& p, int* s_cou
     // the buckets in use (flags in LDS, this wave's own copy), then in
     // ascending order, four at a time (independent scans): the groups of
     // bucket k in earlier sequences, its total and its start
-    if (p.na > 0) s_count[p.ka] = 1;
-    if (p.nb > 0) s_count[p.kb] = 1;
+    if (p.na > 0) s_used[p.ka] = 1;
+    if (p.nb > 0) s_used[p.kb] = 1;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's own LDS stores
     __builtin_amdgcn_wave_barrier();
-    uint64_t used = __builtin_amdgcn_ballot_w64(s_count[lane] != 0);
+    uint64_t used = __builtin_amdgcn_ballot_w64(s_used[lane] != 0);
     int run = 0;  // positions taken by the buckets before
     while (used != 0) {
       int k[4], c[4], incl[4];
@@ -1611,7 +1611,7 @@ __device__ inline PieceSpan piece_span(int kv, int np, int q, int r, int j, bool
 template <typename KV, typename BT, bool IDS, bool CHECK>
 __global__ __launch_bounds__(64 * kWavePlanWaves) void decode_plan_wave_kernel(PlanArgs a, StepCheckArgs c) {
   static_assert(IDS || !CHECK, "the step check rides on the one-launch plan");
-  __shared__ int s_count[kWavePlanWaves][64];  // size buckets in use, one copy per wave
+  __shared__ int s_used[kWavePlanWaves][64];  // size buckets in use, one copy per wave
   __shared__ int64_t s_bad[kWavePlanWaves];
   constexpr int kThreads = 64 * kWavePlanWaves;
   const int lane = threadIdx.x & 63;
@@ -1677,7 +1677,7 @@ __global__ __launch_bounds__(64 * kWavePlanWaves) void decode_plan_wave_kernel(P
     if (threadIdx.x == 0) a.status[MV_PLAN_BAD_BLOCK] = static_cast<int32_t>(vmin<int64_t>(bad, INT_MAX));
     return;
   }
-  wave_plan_rest(a, p, s_count[wave], lane, !(IDS && blockIdx.x == 0));
+  wave_plan_rest(a, p, s_used[wave], lane, !(IDS && blockIdx.x == 0));
   const bool wide = p.most_tiles >= (1 << 16);  // j * r may exceed 32 bits
 
   if (IDS && blockIdx.x >= kFirstSlotGroup) {
