@@ -676,7 +676,9 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   const int r = threadIdx.x >> 4;
   const bool has_row = r < a.n_rep;
   const int64_t slot_base = (static_cast<int64_t>(b) * a.num_q_heads + h * a.n_rep) * a.max_parts;
-  raw_t* const op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok + (h * a.n_rep + r) * a.out_stride_head + 2 * q;
+  // (threads past the group's heads address head 0's row and store nothing)
+  raw_t* const op = static_cast<raw_t*>(a.out) + b * a.out_stride_tok +
+                    (h * a.n_rep + (has_row ? r : 0)) * a.out_stride_head + 2 * q;
   // this work group's partial of head r: (max, sum) and its dim pairs, as
   // stored (the partial O words: two fp32, or two values of the 16-bit
   // data type)
