@@ -755,8 +755,9 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged
   }
   // The partials above are device-coherent stores; once every wave has
   // seen them acknowledged (vmcnt(0)), the counter increment publishes
-  // them. The work group that completes the count reads all partials
-  // with device-coherent loads. No L2 writeback/invalidate is involved.
+  // them. The work group that completes the count reads the other
+  // groups' partials with device-coherent loads. No L2 writeback or
+  // invalidate is involved.
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   if (threadIdx.x == 0) {
