@@ -83,7 +83,7 @@ constexpr int kIdsFirst = 64;   // ids copied before the work item is known, for
 constexpr int kFewUnitsPerCU = 2;   // plan target when the (sequence, kv head) units fit the CUs
 constexpr int kManyUnitsPerCU = 3;  // plan target cap otherwise
 
-template <int DTYPE, int D>
+template <int DTYPE, int D, int SREQ = MV_DECODE_STAGES>
 struct Traits : TileGeom<DTYPE, D> {
   using G = TileGeom<DTYPE, D>;
   using G::kElemBytes;
@@ -97,10 +97,9 @@ struct Traits : TileGeom<DTYPE, D> {
   static constexpr int kChunk = kWaves * kTile;         // tokens per work-group iteration
   // Tile buffers per wave: up to S-1 tiles stream in while one is computed.
   // Larger tiles get at most 2 stages so two work groups still fit one CU.
-  // With the non-temporal tile copies, 2 stages beat 3 at every size
-  // measured (c2-sized batches 1 %, 8k-32k contexts 6 %); 4 lose 5 %.
-  static constexpr int kStages = kTileBytes <= 2048 ? MV_DECODE_STAGES
-                                                    : (MV_DECODE_STAGES < 2 ? MV_DECODE_STAGES : 2);
+  // SREQ = 2 by default; 3 for launches of short pieces over few units
+  // (kDeepPieceTokens): see launch_decode.
+  static constexpr int kStages = kTileBytes <= 2048 ? SREQ : (SREQ < 2 ? SREQ : 2);
   static constexpr int kStageBytes = 2 * kTileBytes;    // K tile, V tile
   static constexpr int kWaveLds = kStages * kStageBytes;
   // LDS is one union, laid out per phase:
@@ -191,12 +190,12 @@ constexpr float kLazyMin = 1.f / 4096.f;
 
 // ----------------------------------------------------------- the kernel ---
 
-template <int DTYPE, int D, bool FUSED, bool ROPE>
+template <int DTYPE, int D, bool FUSED, bool ROPE, int SREQ = MV_DECODE_STAGES>
 __global__ __launch_bounds__(kWaves * 64)
-__attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D>::kWavesPerSimd))) void paged_decode_kernel(DecodeArgs a) {
+__attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D, SREQ>::kWavesPerSimd))) void paged_decode_kernel(DecodeArgs a) {
   static_assert(FUSED || !ROPE, "the fused RoPE comes with the fused write");
   constexpr bool kPartials16 = DTYPE != MV_DTYPE_F32 && MV_DECODE_PARTIALS16;
-  using Tr = Traits<DTYPE, D>;
+  using Tr = Traits<DTYPE, D, SREQ>;
   using raw_t = typename Elem<DTYPE>::raw;
   constexpr int L = Tr::kLoads;
   constexpr int RP = Tr::kRowPieces;
@@ -1820,18 +1819,39 @@ template <int DTYPE, int D> struct GroupsOf { static constexpr int value = Trait
 
 int chunk_tokens(int head_dim, int dtype) { return trait_value<ChunkOf>(head_dim, dtype); }
 
-template <int DTYPE, int D>
-int launch_decode(const DecodeArgs& a, int num_groups, hipStream_t s) {
+// Three tile stages instead of two for a launch of short pieces over a
+// batch of few units per CU -- at least kDeepMinUnits (sequence, kv head)
+// units, at least two groups per unit (the plan's two groups per CU) and
+// pieces of at most kDeepPieceTokens: c2-like batches, whose waves stream
+// a few tiles each, gain from the deeper prefetch (layer call 10.65-10.74
+// against 10.57-10.69 us, four same-box pairs), while long pieces (c3,
+// 1504 tokens: 36.0-36.2 -> 37.0-37.3 us), three groups per CU (c4: 15.8
+// -> 17.1 us) and launches of a handful of groups (batches of 1-4
+// sequences: +0.04 to +0.1 us) lose. Tiles over 2 KiB keep two stages.
+constexpr int kDeepPieceTokens = 512;
+constexpr int kDeepMinUnits = 64;
+
+template <int DTYPE, int D, int SREQ>
+int launch_decode_s(const DecodeArgs& a, int num_groups, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>(num_groups);
-  if (a.rope_cos) paged_decode_kernel<DTYPE, D, true, true><<<grid, kWaves * 64, 0, s>>>(a);
-  else if (a.new_k) paged_decode_kernel<DTYPE, D, true, false><<<grid, kWaves * 64, 0, s>>>(a);
-  else paged_decode_kernel<DTYPE, D, false, false><<<grid, kWaves * 64, 0, s>>>(a);
+  if (a.rope_cos) paged_decode_kernel<DTYPE, D, true, true, SREQ><<<grid, kWaves * 64, 0, s>>>(a);
+  else if (a.new_k) paged_decode_kernel<DTYPE, D, true, false, SREQ><<<grid, kWaves * 64, 0, s>>>(a);
+  else paged_decode_kernel<DTYPE, D, false, false, SREQ><<<grid, kWaves * 64, 0, s>>>(a);
   return check_launch("mv_paged_decode");
 }
 
+template <int DTYPE, int D>
+int launch_decode(const DecodeArgs& a, int num_groups, bool deep, hipStream_t s) {
+  if constexpr (Traits<DTYPE, D, 3>::kStages == 3 && MV_DECODE_STAGES == 2) {
+    if (deep) return launch_decode_s<DTYPE, D, 3>(a, num_groups, s);
+  }
+  return launch_decode_s<DTYPE, D, MV_DECODE_STAGES>(a, num_groups, s);
+}
+
 template <int DTYPE>
-int launch_decode_d(const DecodeArgs& a, int d, int num_groups, hipStream_t s) {
-  return d == 64 ? launch_decode<DTYPE, 64>(a, num_groups, s) : launch_decode<DTYPE, 128>(a, num_groups, s);
+int launch_decode_d(const DecodeArgs& a, int d, int num_groups, bool deep, hipStream_t s) {
+  return d == 64 ? launch_decode<DTYPE, 64>(a, num_groups, deep, s)
+                 : launch_decode<DTYPE, 128>(a, num_groups, deep, s);
 }
 
 // The step's new rows for the fused KV write (mv_paged_decode_write).
@@ -2219,10 +2239,13 @@ int decode_launch(const void* query, int64_t q_stride_tok, int64_t q_stride_head
     a.rope_sin = static_cast<const char*>(nr->rope_sin);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t units = static_cast<int64_t>(num_seqs) * num_kv_heads;
+  const bool deep = partition_tokens <= kDeepPieceTokens && units >= kDeepMinUnits &&
+                    static_cast<int64_t>(num_work_groups) >= 2 * units;
   switch (dtype) {
-    case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, num_work_groups, s);
-    case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, num_work_groups, s);
-    default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, num_work_groups, s);
+    case MV_DTYPE_F32: return launch_decode_d<MV_DTYPE_F32>(a, head_dim, num_work_groups, deep, s);
+    case MV_DTYPE_F16: return launch_decode_d<MV_DTYPE_F16>(a, head_dim, num_work_groups, deep, s);
+    default: return launch_decode_d<MV_DTYPE_BF16>(a, head_dim, num_work_groups, deep, s);
   }
 }
 }  // namespace mv

@@ -92,7 +92,9 @@ def check_handoff(name, ins):
 
 @pytest.mark.skipif(_hipcc() is None, reason="hipcc not installed")
 @pytest.mark.parametrize("src,kernel,count", [
-    ("paged_decode.hip", "paged_decode_kernel", 18),
+    # decode: 3 dtypes x 2 head dims x (plain, fused write, fused RoPE +
+    # write), plus the three-stage forms of the 16-bit head_dim-64 kernels
+    ("paged_decode.hip", "paged_decode_kernel", 24),
     ("paged_prefill.hip", "paged_prefill_kernel", 12),
 ])
 def test_partials_are_published_before_the_counter(src, kernel, count, tmp_path):
