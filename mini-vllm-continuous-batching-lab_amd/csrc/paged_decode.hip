@@ -282,13 +282,12 @@ __attribute__((amdgpu_waves_per_eu(Traits<DTYPE, D, SREQ>::kWavesPerSimd))) void
   // with the new rows -- the bytes the write stores -- before it is used;
   // otherwise the token is the one read from the pool. The rows and the
   // slot arrive in LDS with the Q rows (wave 0's copies, before any tile
-  // copy); wave
-  // new_wave (the one whose tile holds the token) then keeps them in
-  // registers, lanes [0, RP) the K row's 16-byte pieces, [RP, 2 RP) the V
-  // row's, and with the fused RoPE rotates the K row there, before its
-  // tile loop: off the tail of the sequence's last piece (0.6 us per
-  // layer call when it was done at the last tile). The tile copies
-  // themselves are those of the plain kernel.
+  // copy); wave new_wave (the one whose tile holds the token) then keeps
+  // the rows in registers, lanes [0, RP) the K row's 16-byte pieces,
+  // [RP, 2 RP) the V row's, and with the fused RoPE rotates the K row
+  // there, before its tile loop: off the tail of the sequence's last piece
+  // (0.6 us per layer call when it was done at the last tile). The tile
+  // copies themselves are those of the plain kernel.
   const bool last_piece = FUSED && part == n_parts - 1;
   const int new_wave = ((tok_end - 1 - tok_begin) / kTile) % kWaves;
   int64_t new_slot = -1;
