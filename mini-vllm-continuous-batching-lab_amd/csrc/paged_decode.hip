@@ -939,9 +939,8 @@ __device__ int64_t block_sum64(int64_t v, int64_t* scratch) {
   v = wave_sum64(v);
   if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
   __syncthreads();
-  int64_t total = 0;
-#pragma unroll
-  for (int w = 0; w < kPlanWaves; ++w) total += scratch[w];
+  const int lane = threadIdx.x & 63;  // lane w reads wave w's sum
+  const int64_t total = wave_sum64(lane < kPlanWaves ? scratch[lane] : 0);
   __syncthreads();
   return total;
 }
@@ -1136,16 +1135,19 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     }
   }
   __syncthreads();
-  int64_t total_tiles = 0, live_seqs = 0;
-  int most_tiles = 0, least_kv = INT_MAX, bad_kv = 0, short_table = 0;
-#pragma unroll
-  for (int w = 0; w < kPlanWaves; ++w) {
-    total_tiles += s_tiles[w];
-    live_seqs += s_red5[0][w];
-    most_tiles = max(most_tiles, s_red5[1][w]);
-    least_kv = min(least_kv, s_red5[2][w]);
-    bad_kv += s_red5[3][w];
-    short_table += s_red5[4][w];
+  // the waves' totals: lane w reads wave w's, then one wave reduction per
+  // value (16 serial broadcast reads per value and thread kept the CU's LDS
+  // busy for about 1500 cycles)
+  int64_t total_tiles, live_seqs;
+  int most_tiles, least_kv, bad_kv, short_table;
+  {
+    const bool in = lane < kPlanWaves;
+    total_tiles = wave_sum64(in ? s_tiles[lane] : 0);
+    live_seqs = wave_sum(in ? s_red5[0][lane] : 0);
+    most_tiles = wave_max(in ? s_red5[1][lane] : 0);
+    least_kv = wave_min(in ? s_red5[2][lane] : INT_MAX);
+    bad_kv = wave_sum(in ? s_red5[3][lane] : 0);
+    short_table = wave_sum(in ? s_red5[4][lane] : 0);
   }
   const int64_t units = live_seqs * hkv;  // (sequence, kv head) pairs
 
@@ -1212,13 +1214,10 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
     const int incl = wave_scan_sum(np);
     if (lane == 63) s_wsum[parity][wave] = incl;
     __syncthreads();  // alternate buffers: the next chunk writes the other one
-    int before = 0, chunk = 0;
-#pragma unroll
-    for (int w = 0; w < kPlanWaves; ++w) {
-      const int t = s_wsum[parity][w];
-      before += w < wave ? t : 0;
-      chunk += t;
-    }
+    // earlier waves' and all waves' totals: lane w holds wave w's, scanned
+    const int wscan = wave_scan_sum(lane < kPlanWaves ? s_wsum[parity][lane] : 0);
+    const int before = wave == 0 ? 0 : __builtin_amdgcn_readlane(wscan, __builtin_amdgcn_readfirstlane(wave - 1));
+    const int chunk = __builtin_amdgcn_readlane(wscan, kPlanWaves - 1);
     const int64_t start = running + before + incl - np;
     if (deal) {
       // items < num_groups / hkv <= kDealMax; the wave-uniform trip count
@@ -1291,9 +1290,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanArgs a) {
       const int incl = wave_scan_sum(cnt);
       if (lane == 63) s_wsum[0][wave] = incl;
       __syncthreads();
-      int before = 0;
-#pragma unroll
-      for (int w = 0; w < kPlanWaves; ++w) before += w < wave ? s_wsum[0][w] : 0;
+      const int wscan = wave_scan_sum(lane < kPlanWaves ? s_wsum[0][lane] : 0);
+      const int before = wave == 0 ? 0 : __builtin_amdgcn_readlane(wscan, __builtin_amdgcn_readfirstlane(wave - 1));
       s_start[tid] = before + incl - cnt;
     }
     __syncthreads();
