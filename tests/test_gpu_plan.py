@@ -280,3 +280,61 @@ def test_write_through_dlpack_alias_needs_invalidation():
     work = p2.work[: 8 * g].view(g, 8).cpu().tolist()
     ends = {(w[0], w[1]): max(x[5] for x in work if (x[0], x[1]) == (w[0], w[1])) for w in work}
     assert ends[(0, 0)] == 60 and ends[(1, 0)] == 20, ends
+
+
+def _smallest_fitting_bound(kv_lens, hkv, bs, groups_per_cu, cus):
+    """The plan's piece bound L (16-token tiles) from its rules, by brute
+    force: the smallest L from the search's lower end whose groups fit the
+    resident target, the fair share when even the widest L does not fit
+    (several rounds), and twice the fair share when the fitting L is over
+    that (skewed batches)."""
+    tiles = [(k + 15) // 16 for k in kv_lens if k >= 1]
+    units = len(tiles) * hkv
+    total, most = sum(tiles), max(tiles)
+    per_cu = min(2, max(1, groups_per_cu)) if units <= cus else min(3, max(1, groups_per_cu))
+    target = per_cu * max(1, cus)
+    l_cap = max(1, ((512 - 1) * bs) // 16)
+    l_min = min(l_cap, max(4, -(-most // 128)))
+    l_top = min(l_cap, max(l_min, most))
+    l_fair = min(l_cap, max(l_min, -(-(total * hkv) // target)))
+
+    def groups(l):
+        return hkv * sum(-(-t // l) for t in tiles)
+
+    if groups(l_top) > target:
+        return l_fair
+    l = min(l_fair, l_top)
+    while groups(l) > target:
+        l += 1
+    return max(l_min, min(l_cap, 2 * l_fair)) if l > 2 * l_fair else l
+
+
+@pytest.mark.parametrize("batch,hkv,ctx,seed", [
+    (64, 2, ("uniform", 128, 2048), 0),     # the c2 shape (one launch, waves)
+    (16, 8, ("uniform", 8192, 32768), 1),   # long contexts (waves, then the id kernel)
+    (65, 2, ("uniform", 16, 4000), 2),      # the 1024-thread plan from here on
+    (128, 4, ("uniform", 512, 4096), 3),
+    (200, 1, ("lognormal", 300, 1.0, 1, 8192), 4),
+    (256, 2, ("lognormal", 300, 1.0, 1, 8192), 5),
+    (300, 2, ("uniform", 1, 3000), 6),      # past the one-wave search: block sums
+    (1000, 8, ("uniform", 1, 600), 7),
+])
+def test_piece_bound_is_the_smallest_that_fits(batch, hkv, ctx, seed):
+    """Both plan kernels search the piece bound (the wave plan up to 64
+    sequences, the 1024-thread plan above: one wave's binary search up to
+    256 sequences, block sums past that); the bound they return must be the
+    one the rules define, and the groups the ones it cuts."""
+    from benchmarks.paged_decode_workloads import make_layout
+    from mini_vllm.attention import paged_attention_gpu as pag
+
+    spec = WorkloadSpec("bound", 2 * hkv, hkv, 64, 16, torch.bfloat16, batch, ctx)
+    lay = make_layout(spec, seed)
+    say("plan bound", batch, hkv, ctx, seed)
+    bt = lay.block_table().to(DEV)
+    kv = torch.tensor(lay.kv_lens, dtype=torch.int64, device=DEV)
+    plan = plan_decode(bt, kv, 16, lay.num_blocks, DEV, 64, torch.bfloat16, hkv)
+    gpc, cus = pag._groups_per_cu(DEV, 64, torch.bfloat16)
+    want = _smallest_fitting_bound(lay.kv_lens, hkv, 16, gpc, cus)
+    assert plan.partition_tokens == 16 * want, (plan.partition_tokens, 16 * want)
+    tiles = [(k + 15) // 16 for k in lay.kv_lens]
+    assert plan.num_groups == hkv * sum(-(-t // want) for t in tiles)
